@@ -1,0 +1,232 @@
+#!/usr/bin/env python
+"""Benchmark of the rational-attention kernel path on one MI355X.
+
+A "step" is one causal bf16 rational-attention forward + backward (autograd
+API: rational_attention(...) then out.backward(dO)) at B=4, H=16, S=4096,
+D=128 with ALiBi, inputs resident in HBM. ``value`` is the algorithmic
+throughput 7*B*H*S^2*D / step time in TFLOP/s. The same JSON line carries:
+  * roofline  -- the dominant C-ABI call of the step (kat_attn_bwd or
+                 kat_attn_fwd), timed with HIP events on its launch stream
+                 inside the timed region, against the dense bf16 MFMA peak;
+  * fused_ops -- HBM GB/s of mean_error_norm, rational_swiglu and
+                 rational_softmax fwd+bwd at their benchmark shapes (bf16),
+                 with the 256 MB last-level cache flushed before each rep;
+  * cpu_baseline -- the CPU oracle (fp32) on a bounded sample of the same
+                 workload (one (b, h) head), on this host's cores.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-fused]
+"""
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "attn fwd+bwd TFLOP/s (% MFMA peak) at S=4096; fused-op HBM GB/s (% peak)"
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+
+
+def attention_inputs(torch, B, H, T, D, dev, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    ts = [torch.randn(B, H, T, D, generator=g).to(torch.bfloat16) for _ in range(4)]
+    return [t.to(dev) for t in ts]
+
+
+def bench_attention(torch, F, steps, warmup, B=4, H=16, T=4096, D=128):
+    dev = torch.device("cuda:0")
+    q, k, v, do = attention_inputs(torch, B, H, T, D, dev)
+    for t in (q, k, v):
+        t.requires_grad_(True)
+    slopes = torch.tensor([2.0 ** (-(i + 1) / 2) for i in range(H)], dtype=torch.float32,
+                          device=dev)
+    scale = 1.0 / math.sqrt(D)
+
+    def step(ev=None):
+        for t in (q, k, v):
+            t.grad = None
+        if ev is not None:
+            ev[0].record()
+        out = F.rational_attention(q, k, v, slopes, scale)
+        if ev is not None:
+            ev[1].record()
+        out.backward(do)
+        if ev is not None:
+            ev[2].record()
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    t0 = time.perf_counter()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        step(evs[i])
+    end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = start.elapsed_time(end) / steps
+    fwd_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / steps
+    bwd_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / steps
+    unit = B * H * T * T * D  # one causal S x S x D matmul = 2 * (S^2 / 2) * D flops
+    return dict(ms=ms, wall_ms=wall * 1e3 / steps, fwd_ms=fwd_ms, bwd_ms=bwd_ms,
+                flops_step=7 * unit, flops_fwd=2 * unit, flops_bwd=5 * unit)
+
+
+def bench_fused(torch, F, reps=10):
+    """fwd+bwd of each fused op at the benchmark shapes; GB/s from the
+    algorithmic bytes (each tensor read or written once)."""
+    dev = torch.device("cuda:0")
+    bf = torch.bfloat16
+    g = torch.Generator().manual_seed(1)
+    flush = torch.empty(512 * 1024 * 1024 // 4, dtype=torch.float32, device=dev)
+    res = {}
+
+    def timed(fn):
+        ts = []
+        for _ in range(reps + 2):
+            flush.fill_(1.0)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn()
+            e1.record()
+            torch.cuda.synchronize()
+            ts.append(e0.elapsed_time(e1))
+        ts = sorted(ts[2:])
+        return ts[len(ts) // 2]
+
+    # mean_error_norm: x [16384, 4096] bf16, gamma fp32
+    N, C = 16384, 4096
+    x = torch.randn(N, C, generator=g).to(bf).to(dev).requires_grad_(True)
+    w = (1 + 0.02 * torch.randn(C, generator=g)).to(dev).requires_grad_(True)
+    dy = torch.randn(N, C, generator=g).to(bf).to(dev)
+
+    def norm_step():
+        x.grad = w.grad = None
+        F.mean_error_norm(x, w).backward(dy)
+    nbytes = (2 * N * C * 2 + C * 4 + N * 4) + (3 * N * C * 2 + 2 * C * 4 + N * 4)
+    t = timed(norm_step)
+    res["mean_error_norm"] = dict(shape=[N, C], ms=t, bytes=nbytes, GBs=nbytes / t / 1e6)
+    del x, w, dy
+
+    # rational_swiglu: gate, value [16384, 11008] bf16
+    N, C = 16384, 11008
+    ga = torch.randn(N, C, generator=g).to(bf).to(dev).requires_grad_(True)
+    va = torch.randn(N, C, generator=g).to(bf).to(dev).requires_grad_(True)
+    dy = torch.randn(N, C, generator=g).to(bf).to(dev)
+
+    def swiglu_step():
+        ga.grad = va.grad = None
+        F.rational_swiglu(ga, va).backward(dy)
+    nbytes = 3 * N * C * 2 + 5 * N * C * 2
+    t = timed(swiglu_step)
+    res["rational_swiglu"] = dict(shape=[N, C], ms=t, bytes=nbytes, GBs=nbytes / t / 1e6)
+    del ga, va, dy
+
+    # rational_softmax: scores [4096, 4096] ~ N(0, 4) bf16
+    N, C = 4096, 4096
+    s = (2 * torch.randn(N, C, generator=g)).to(bf).to(dev).requires_grad_(True)
+    dy = torch.randn(N, C, generator=g).to(bf).to(dev)
+
+    def softmax_step():
+        s.grad = None
+        F.rational_softmax(s).backward(dy)
+    nbytes = 2 * N * C * 2 + 4 * N * C * 2
+    t = timed(softmax_step)
+    res["rational_softmax"] = dict(shape=[N, C], ms=t, bytes=nbytes, GBs=nbytes / t / 1e6)
+    for r in res.values():
+        r["frac_hbm_peak"] = r["GBs"] / PEAK_HBM_GBS
+    return res
+
+
+def cpu_baseline(torch, S=4096, D=128, reps=2):
+    """CPU oracle (fp32) forward + backward of one (b, h) head of the workload
+    (heads are independent, so this is an exact 1/64 slice)."""
+    import oracle as O
+    g = torch.Generator().manual_seed(0)
+    q, k, v, do = (torch.randn(1, 1, S, D, generator=g).to(torch.bfloat16) for _ in range(4))
+    slopes = torch.tensor([2.0 ** -0.5])
+    scale = 1.0 / math.sqrt(D)
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        o, L = O.attention_fwd(q, k, v, slopes, scale, dtype=torch.float32)
+        O.attention_bwd(q, k, v, o, L, do, slopes, scale, dtype=torch.float32)
+        ts.append(time.perf_counter() - t0)
+    t = min(ts)
+    flops = 7 * S * S * D
+    return {"value": flops / t / 1e12, "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"1 of 64 (b,h) heads at S={S}, D={D}: oracle fp32 fwd+bwd, "
+                      f"best of {reps} ({t:.2f} s per head)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-fused", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(the kernels shard by (batch, head) with no communication; see the design notes)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import fastalgebraictransformer_amd as F
+    from fastalgebraictransformer_amd import _lib
+    _lib.load()
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+
+    att = bench_attention(torch, F, args.steps, args.warmup)
+    value = att["flops_step"] / (att["ms"] * 1e-3) / 1e12
+    fwd_tf = att["flops_fwd"] / (att["fwd_ms"] * 1e-3) / 1e12
+    bwd_tf = att["flops_bwd"] / (att["bwd_ms"] * 1e-3) / 1e12
+    dom = "kat_attn_bwd" if att["bwd_ms"] >= att["fwd_ms"] else "kat_attn_fwd"
+    ach = bwd_tf if dom == "kat_attn_bwd" else fwd_tf
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(att["ms"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (q, k, v, dO ~ N(0,1) from seed 0)",
+        "config": {"workload": "rational_attention fwd+bwd, causal, ALiBi, bf16 in / fp32 acc",
+                   "B": 4, "H": 16, "S": 4096, "D": 128,
+                   "slopes": "2^(-(i+1)/2)", "scale": "1/sqrt(128)"},
+        "roofline": {"bound": "mfma", "call": dom, "achieved": round(ach, 2),
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": None},
+        "kernels": {"kat_attn_fwd": {"ms": round(att["fwd_ms"], 4), "TFLOPs": round(fwd_tf, 2),
+                                     "algorithmic_flops": att["flops_fwd"]},
+                    "kat_attn_bwd": {"ms": round(att["bwd_ms"], 4), "TFLOPs": round(bwd_tf, 2),
+                                     "algorithmic_flops": att["flops_bwd"]}},
+        "frac_mfma_peak_step": round(value / PEAK_BF16_TFLOPS, 4),
+    }
+    if not args.no_fused:
+        fused = bench_fused(torch, F)
+        line["fused_ops"] = {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv)
+                                 for kk, vv in r.items()} for k, r in fused.items()}
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(torch)
+        line["cpu_baseline"]["value"] = round(line["cpu_baseline"]["value"], 5)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,70 @@
+"""MI355X-native (gfx950) kernels for the algebraic transformer.
+
+Drop-in for the reference ``kernels`` package of
+SkyeGunasekaran/fastAlgebraicTransformer: the same public names
+(reference __init__.py:7-63), backed by hand-written HIP kernels in
+``libkat.so`` behind the C ABI of ``include/kat.h``.
+
+To run code written against the reference unchanged, alias this package
+under the reference's import name before importing it::
+
+    import fastalgebraictransformer_amd
+    fastalgebraictransformer_amd.install_as("kernels")
+    from kernels.fused_ops import rational_softmax   # resolves here
+"""
+
+import sys as _sys
+
+from .fused_ops import (
+    EPS,
+    MeanErrorNorm,
+    RationalSoftmax,
+    RationalSwiGLU,
+    mean_error_norm,
+    rational_softmax,
+    rational_swiglu,
+)
+from .forward import compute_alibi_slopes, rational_attention_forward
+from .backward import RationalAttentionFunction, rational_attention, rational_attention_backward
+from .algebraic_model import (
+    AlgebraicAttention,
+    AlgebraicBlock,
+    AlgebraicTransformerLM,
+    RationalMR,
+    RationalSwiGLU as RationalSwiGLUModule,
+    create_large_model,
+    create_medium_model,
+    create_small_model,
+)
+
+__all__ = [
+    "rational_softmax",
+    "rational_swiglu",
+    "mean_error_norm",
+    "RationalSoftmax",
+    "RationalSwiGLU",
+    "MeanErrorNorm",
+    "EPS",
+    "rational_attention_forward",
+    "compute_alibi_slopes",
+    "rational_attention",
+    "rational_attention_backward",
+    "RationalAttentionFunction",
+    "AlgebraicTransformerLM",
+    "RationalMR",
+    "AlgebraicAttention",
+    "AlgebraicBlock",
+    "create_small_model",
+    "create_medium_model",
+    "create_large_model",
+]
+
+
+def install_as(name="kernels"):
+    """Register this package and its submodules under ``name`` (default the
+    reference's package name ``kernels``) in ``sys.modules``."""
+    pkg = _sys.modules[__name__]
+    _sys.modules[name] = pkg
+    for sub in ("fused_ops", "forward", "backward", "algebraic_model"):
+        _sys.modules[f"{name}.{sub}"] = _sys.modules[f"{__name__}.{sub}"]
+    return pkg

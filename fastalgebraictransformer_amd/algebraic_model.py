@@ -1,0 +1,210 @@
+"""Algebraic transformer language model on top of the MI355X kernels.
+
+API-identical to the reference ``kernels.algebraic_model``
+(SkyeGunasekaran/fastAlgebraicTransformer algebraic_model.py:26-302): the same
+module classes, constructor arguments, parameter and buffer names (so
+state_dicts are interchangeable) and factory functions. On CUDA (HIP) tensors
+the norm, attention and SwiGLU run the libkat kernels; on CPU tensors the
+modules use the reference's torch formulas (algebraic_model.py:37-39, 58-60,
+112-136), as the reference does.
+"""
+
+import math
+from typing import Optional, Tuple
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+from torch.utils.checkpoint import checkpoint
+
+from .backward import rational_attention
+from .forward import compute_alibi_slopes
+from .fused_ops import EPS, mean_error_norm, rational_softmax, rational_swiglu
+
+
+class RationalMR(nn.Module):
+    """Mean-error normalisation, y = x / (mean|x| + eps) * weight
+    (reference algebraic_model.py:26-39)."""
+
+    def __init__(self, d_model: int, eps: float = EPS):
+        super().__init__()
+        self.eps = eps
+        self.weight = nn.Parameter(torch.ones(d_model))
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return mean_error_norm(x, self.weight, self.eps)
+
+
+class RationalSwiGLU(nn.Module):
+    """Gated FFN: w_out(gate * sigma(gate) * value) with [gate | value] from one
+    projection (reference algebraic_model.py:42-62)."""
+
+    def __init__(self, d_model: int, d_ffn: int, dropout: float = 0.0):
+        super().__init__()
+        self.w_gate_val = nn.Linear(d_model, 2 * d_ffn, bias=False)
+        self.w_out = nn.Linear(d_ffn, d_model, bias=False)
+        self.dropout = nn.Dropout(dropout)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        gate, value = self.w_gate_val(x).chunk(2, dim=-1)
+        return self.dropout(self.w_out(rational_swiglu(gate, value)))
+
+
+class AlgebraicAttention(nn.Module):
+    """Causal multi-head rational attention with ALiBi
+    (reference algebraic_model.py:65-136)."""
+
+    def __init__(self, d_model: int, n_head: int, dropout: float = 0.1):
+        super().__init__()
+        assert d_model % n_head == 0
+        self.d_model = d_model
+        self.n_head = n_head
+        self.d_head = d_model // n_head
+        self.scale = 1.0 / math.sqrt(self.d_head)
+        self.qkv = nn.Linear(d_model, 3 * d_model, bias=False)
+        self.out = nn.Linear(d_model, d_model, bias=False)
+        self.dropout = nn.Dropout(dropout)
+        self.register_buffer("alibi_slopes", compute_alibi_slopes(n_head))
+
+    def forward(self, x: torch.Tensor, mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+        B, T, C = x.shape
+        # [B, T, 3, H, D] -> three strided [B, H, T, D] views (no copies: the
+        # kernels take (b, h, t) strides)
+        q, k, v = self.qkv(x).view(B, T, 3, self.n_head, self.d_head).permute(2, 0, 3, 1, 4)
+        if x.is_cuda:
+            # like the reference GPU path (algebraic_model.py:93-101) the
+            # padding mask is not applied here; attention is always causal
+            y = rational_attention(q, k, v, self.alibi_slopes, self.scale, causal=True, eps=EPS)
+        else:
+            y = self._cpu_attention(q, k, v, mask)
+        y = y.transpose(1, 2).contiguous().view(B, T, C)
+        return self.dropout(self.out(y))
+
+    def _cpu_attention(self, q, k, v, mask):
+        """Reference CPU path (algebraic_model.py:112-136): full score matrix,
+        ALiBi, -1e4 causal and padding fill, rational softmax, P @ V."""
+        B, H, T, D = q.shape
+        scores = torch.matmul(q, k.transpose(-2, -1)) * self.scale
+        idx = torch.arange(T, device=q.device)
+        dist = (idx[:, None] - idx[None, :]).abs().float()
+        scores = scores + (-dist * self.alibi_slopes.view(1, H, 1, 1))
+        future = torch.ones(T, T, device=q.device, dtype=torch.bool).triu(1)
+        scores = scores.masked_fill(future[None, None], -1e4)
+        if mask is not None:
+            scores = scores.masked_fill((mask == 0)[:, None, None, :], -1e4)
+        return torch.matmul(rational_softmax(scores, eps=EPS), v)
+
+
+class AlgebraicBlock(nn.Module):
+    """Pre-norm residual block (reference algebraic_model.py:139-152)."""
+
+    def __init__(self, d_model: int, n_head: int, d_ffn: int, dropout: float):
+        super().__init__()
+        self.attn = AlgebraicAttention(d_model, n_head, dropout)
+        self.ffn = RationalSwiGLU(d_model, d_ffn, dropout)
+        self.norm1 = RationalMR(d_model)
+        self.norm2 = RationalMR(d_model)
+
+    def forward(self, x: torch.Tensor, mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+        h = x + self.attn(self.norm1(x), mask)
+        return h + self.ffn(self.norm2(h))
+
+
+class AlgebraicTransformerLM(nn.Module):
+    """Decoder-only LM with tied embedding/head (reference
+    algebraic_model.py:155-265). Extra keyword arguments are accepted and
+    ignored, as in the reference."""
+
+    def __init__(
+        self,
+        vocab_size: int,
+        d_model: int,
+        n_head: int,
+        n_layers: int,
+        d_ffn: Optional[int] = None,
+        block_size: int = 2048,
+        dropout: float = 0.1,
+        gradient_checkpointing: bool = False,
+        **kwargs,
+    ):
+        super().__init__()
+        d_ffn = int(d_model * 8 / 3) if d_ffn is None else d_ffn
+        self.block_size = block_size
+        self.gradient_checkpointing = gradient_checkpointing
+        self.n_layers = n_layers
+        self.embed = nn.Embedding(vocab_size, d_model)
+        self.blocks = nn.ModuleList(
+            [AlgebraicBlock(d_model, n_head, d_ffn, dropout) for _ in range(n_layers)])
+        self.norm = RationalMR(d_model)
+        self.head = nn.Linear(d_model, vocab_size, bias=False)
+        self.embed.weight = self.head.weight  # weight tying
+        self.apply(self._init_weights)
+
+    def _init_weights(self, module):
+        # N(0, 0.02) for Linear / Embedding weights, zero biases
+        if isinstance(module, nn.Linear):
+            std = 0.02
+            if hasattr(module, "_scale_init"):
+                std = 0.02 / math.sqrt(2 * self.n_layers)
+            nn.init.normal_(module.weight, mean=0.0, std=std)
+            if module.bias is not None:
+                nn.init.zeros_(module.bias)
+        elif isinstance(module, nn.Embedding):
+            nn.init.normal_(module.weight, mean=0.0, std=0.02)
+
+    def forward(
+        self,
+        input_ids: torch.Tensor,
+        labels: Optional[torch.Tensor] = None,
+        attention_mask: Optional[torch.Tensor] = None,
+    ) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+        x = self.embed(input_ids)
+        for block in self.blocks:
+            if self.gradient_checkpointing and self.training:
+                x = checkpoint(block, x, attention_mask, use_reentrant=False)
+            else:
+                x = block(x, attention_mask)
+        logits = self.head(self.norm(x))
+        loss = None
+        if labels is not None:
+            # next-token loss: position t predicts token t+1
+            pred = logits[..., :-1, :].contiguous()
+            tgt = labels[..., 1:].contiguous()
+            loss = F.cross_entropy(pred.view(-1, pred.size(-1)), tgt.view(-1), ignore_index=-100)
+        return logits, loss
+
+    @torch.no_grad()
+    def generate(self, idx: torch.Tensor, max_new_tokens: int, temperature: float = 1.0,
+                 top_k: Optional[int] = None) -> torch.Tensor:
+        """Sample ``max_new_tokens`` tokens, re-running the (cropped) prefix per
+        step (reference algebraic_model.py:239-265)."""
+        for _ in range(max_new_tokens):
+            ctx = idx if idx.size(1) <= self.block_size else idx[:, -self.block_size:]
+            logits, _ = self.forward(ctx)
+            logits = logits[:, -1, :]
+            if temperature != 1.0:
+                logits = logits / temperature
+            if top_k is not None:
+                kth = torch.topk(logits, min(top_k, logits.size(-1)))[0][:, [-1]]
+                logits[logits < kth] = float("-inf")
+            nxt = torch.multinomial(F.softmax(logits, dim=-1), num_samples=1)
+            idx = torch.cat((idx, nxt), dim=1)
+        return idx
+
+
+def create_small_model(vocab_size: int = 32000, **kwargs) -> AlgebraicTransformerLM:
+    """d_model 768, 12 heads, 12 layers (~125M parameters)."""
+    return AlgebraicTransformerLM(vocab_size=vocab_size, d_model=768, n_head=12, n_layers=12,
+                                  **kwargs)
+
+
+def create_medium_model(vocab_size: int = 32000, **kwargs) -> AlgebraicTransformerLM:
+    """d_model 1024, 16 heads, 24 layers (~350M parameters)."""
+    return AlgebraicTransformerLM(vocab_size=vocab_size, d_model=1024, n_head=16, n_layers=24,
+                                  **kwargs)
+
+
+def create_large_model(vocab_size: int = 32000, **kwargs) -> AlgebraicTransformerLM:
+    """d_model 1536, 24 heads, 24 layers (~760M parameters)."""
+    return AlgebraicTransformerLM(vocab_size=vocab_size, d_model=1536, n_head=24, n_layers=24,
+                                  **kwargs)

@@ -1,0 +1,153 @@
+// C ABI of the rational-attention kernels: argument checks and kernel choice.
+//
+// Kernel choice: bf16 / fp16 tensors with a head dim the MFMA kernels cover
+// (and 16-byte aligned rows) go to the MFMA kernels; everything else (fp32,
+// other head dims up to 256, unaligned views) to the fp32 tiled kernels.
+// Setting KAT_ATTN_IMPL=tiled in the environment forces the tiled kernels
+// (used by the tests to cross-check the two on the GPU).
+
+#include <stdlib.h>
+#include <string.h>
+
+#include "attn_common.h"
+#include "kat_common.h"
+#include "kat_internal.h"
+
+using namespace kat;
+
+namespace {
+
+bool force_tiled() {
+  const char* e = getenv("KAT_ATTN_IMPL");
+  return e && strcmp(e, "tiled") == 0;
+}
+
+int fill_args(const char* nm, AttnArgs& a, int64_t B, int64_t H, int64_t T, int64_t D,
+              const int64_t* strides, int n_tensors, const int64_t* l_strides) {
+  if (B < 0 || H < 0 || T < 0 || D < 0) return fail(KAT_EINVAL, "%s: negative size", nm);
+  if (B * H > 0x7fffffffLL || T > 0x7fffffffLL)
+    return fail(KAT_EUNSUPPORTED, "%s: B*H or T too large", nm);
+  if (D > 256) return fail(KAT_EUNSUPPORTED, "%s: head dim %lld > 256", nm, (long long)D);
+  if (!strides || !l_strides) return fail(KAT_EINVAL, "%s: null stride array", nm);
+  a.B = (int)B;
+  a.H = (int)H;
+  a.T = (int)T;
+  a.D = (int)D;
+  int64_t* dst[8] = {a.sq, a.sk, a.sv, a.so, a.sdo, a.sdq, a.sdk, a.sdv};
+  const int order_fwd[4] = {0, 1, 2, 3};  // q, k, v, out
+  for (int t = 0; t < 8; ++t)
+    for (int j = 0; j < 3; ++j) dst[t][j] = 0;
+  for (int t = 0; t < n_tensors; ++t) {
+    const int slot = n_tensors == 4 ? order_fwd[t] : t;
+    for (int j = 0; j < 3; ++j) dst[slot][j] = strides[3 * t + j];
+  }
+  for (int j = 0; j < 3; ++j) a.sl[j] = l_strides[j];
+  return KAT_OK;
+}
+
+template <typename T> bool rows16(const void* p, const int64_t* s) {
+  return aligned16(p) && (s[0] * (int64_t)sizeof(T)) % 16 == 0 &&
+         (s[1] * (int64_t)sizeof(T)) % 16 == 0 && (s[2] * (int64_t)sizeof(T)) % 16 == 0;
+}
+
+size_t delta_bytes(int64_t B, int64_t H, int64_t T) {
+  return (((size_t)(B * H * T) * sizeof(float)) + 255) & ~(size_t)255;
+}
+
+}  // namespace
+
+template <typename T> static int attn_fwd_t(const AttnArgs& a, hipStream_t st) {
+  if (!force_tiled() && attn_mfma_supported(a.D) && rows16<T>(a.q, a.sq) &&
+      rows16<T>(a.k, a.sk) && rows16<T>(a.v, a.sv) && rows16<T>(a.o, a.so)) {
+    const int rc = attn_fwd_mfma<T>(a, st);
+    if (rc != KAT_EUNSUPPORTED) return rc;
+  }
+  return attn_fwd_generic<T>(a, st);
+}
+
+template <typename T> static int attn_bwd_t(const AttnArgs& a, float* delta, hipStream_t st) {
+  if (int rc = attn_delta<T>(a, delta, st)) return rc;
+  if (!force_tiled() && attn_mfma_supported(a.D) && rows16<T>(a.q, a.sq) &&
+      rows16<T>(a.k, a.sk) && rows16<T>(a.v, a.sv) && rows16<T>(a.o, a.so) &&
+      rows16<T>(a.dout, a.sdo) && rows16<T>(a.dq, a.sdq) && rows16<T>(a.dk, a.sdk) &&
+      rows16<T>(a.dv, a.sdv)) {
+    const int rc = attn_bwd_mfma<T>(a, delta, st);
+    if (rc != KAT_EUNSUPPORTED) return rc;
+  }
+  return attn_bwd_generic<T>(a, delta, st);
+}
+
+extern "C" int kat_attn_fwd(const void* q, const void* k, const void* v, void* out, float* L,
+                            const float* slopes, int64_t B, int64_t H, int64_t T, int64_t D,
+                            const int64_t* strides, const int64_t* l_strides, float scale,
+                            float eps, int causal, int dtype, void* stream) {
+  (void)causal;  // always causal, as the reference (forward.py:110)
+  const char* nm = "kat_attn_fwd";
+  AttnArgs a = {};
+  if (int rc = fill_args(nm, a, B, H, T, D, strides, 4, l_strides)) return rc;
+  if (B * H * T == 0 || D == 0) return KAT_OK;
+  if (!q || !k || !v || !out || !L || !slopes) return fail(KAT_EINVAL, "%s: null pointer", nm);
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.o = out;
+  a.L = L;
+  a.slopes = slopes;
+  a.scale = scale;
+  a.eps = eps;
+  const hipStream_t st = as_stream(stream);
+  switch (dtype) {
+    case KAT_F32: return attn_fwd_generic<float>(a, st);
+    case KAT_BF16: return attn_fwd_t<bf16>(a, st);
+    case KAT_F16: return attn_fwd_t<f16>(a, st);
+    default: return fail(KAT_EUNSUPPORTED, "%s: unsupported dtype %d", nm, dtype);
+  }
+}
+
+extern "C" size_t kat_attn_bwd_workspace_size(int64_t B, int64_t H, int64_t T, int64_t D,
+                                              int dtype) {
+  (void)D;
+  (void)dtype;
+  if (B <= 0 || H <= 0 || T <= 0) return 0;
+  return delta_bytes(B, H, T);
+}
+
+extern "C" int kat_attn_bwd(const void* q, const void* k, const void* v, const void* out,
+                            const float* L, const void* dout, void* dq, void* dk, void* dv,
+                            const float* slopes, void* workspace, size_t workspace_bytes,
+                            int64_t B, int64_t H, int64_t T, int64_t D, const int64_t* strides,
+                            const int64_t* l_strides, float scale, float eps, int causal,
+                            int dtype, void* stream) {
+  (void)causal;  // always causal, as the reference (backward.py:125,222)
+  const char* nm = "kat_attn_bwd";
+  AttnArgs a = {};
+  if (int rc = fill_args(nm, a, B, H, T, D, strides, 8, l_strides)) return rc;
+  if (B * H * T == 0 || D == 0) return KAT_OK;
+  if (!q || !k || !v || !out || !L || !dout || !dq || !dk || !dv || !slopes)
+    return fail(KAT_EINVAL, "%s: null pointer", nm);
+  const size_t need = delta_bytes(B, H, T);
+  if (!workspace || workspace_bytes < need)
+    return fail(KAT_EINVAL, "%s: workspace %zu bytes < required %zu", nm, workspace_bytes, need);
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.o = const_cast<void*>(out);
+  a.dout = dout;
+  a.dq = dq;
+  a.dk = dk;
+  a.dv = dv;
+  a.L = const_cast<float*>(L);
+  a.slopes = slopes;
+  a.scale = scale;
+  a.eps = eps;
+  float* delta = reinterpret_cast<float*>(workspace);
+  const hipStream_t st = as_stream(stream);
+  switch (dtype) {
+    case KAT_F32:
+      if (int rc = attn_delta<float>(a, delta, st)) return rc;
+      return attn_bwd_generic<float>(a, delta, st);
+    case KAT_BF16: return attn_bwd_t<bf16>(a, delta, st);
+    case KAT_F16: return attn_bwd_t<f16>(a, delta, st);
+    default: return fail(KAT_EUNSUPPORTED, "%s: unsupported dtype %d", nm, dtype);
+  }
+}

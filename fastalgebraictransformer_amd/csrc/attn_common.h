@@ -1,0 +1,36 @@
+// Argument block shared by the attention kernels and their launchers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace kat {
+
+// Layout [B, H, T, D]: element (b, h, t, d) of tensor X sits at
+// X + b*sX[0] + h*sX[1] + t*sX[2] + d (unit d-stride). L: [B, H, T] fp32.
+struct AttnArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;           // forward output / backward input O
+  const void* dout;  // backward only
+  void* dq;
+  void* dk;
+  void* dv;
+  float* L;
+  const float* slopes;
+  int B, H, T, D;
+  int64_t sq[3], sk[3], sv[3], so[3], sdo[3], sdq[3], sdk[3], sdv[3], sl[3];
+  float scale, eps;
+};
+
+template <typename T> int attn_fwd_generic(const AttnArgs& a, hipStream_t st);
+template <typename T> int attn_delta(const AttnArgs& a, float* delta, hipStream_t st);
+template <typename T> int attn_bwd_generic(const AttnArgs& a, const float* delta, hipStream_t st);
+
+// bf16 / fp16 MFMA kernels; return KAT_EUNSUPPORTED when the shape is not covered.
+template <typename T> int attn_fwd_mfma(const AttnArgs& a, hipStream_t st);
+template <typename T> int attn_bwd_mfma(const AttnArgs& a, const float* delta, hipStream_t st);
+bool attn_mfma_supported(int D);
+
+}  // namespace kat

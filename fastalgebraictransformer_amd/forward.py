@@ -1,0 +1,67 @@
+"""Rational attention forward on MI355X.
+
+Same Python API as the reference ``kernels.forward``
+(SkyeGunasekaran/fastAlgebraicTransformer forward.py:21-42
+``compute_alibi_slopes`` and forward.py:267-319 ``rational_attention_forward``).
+The launch goes to ``kat_attn_fwd`` in libkat.so: a bf16/fp16 MFMA kernel for
+head dims it covers, an fp32 tiled kernel otherwise.
+"""
+
+import math
+
+import torch
+
+from . import _lib
+from .fused_ops import EPS, NEG_INF  # noqa: F401  (re-exported like the reference)
+
+
+def compute_alibi_slopes(n_heads, device=None):
+    """ALiBi slopes as in the reference (forward.py:21-42): with p the largest
+    power of two <= n_heads, head i < p gets b^(i+1) with b = 2^(-8/p); the
+    remaining n_heads - p heads get b'^k, b' = 2^(-8/(2p)), k = 1, 3, 5, ...
+    The powers are taken by torch.pow of a float base over integer exponents,
+    which is how the reference forms them (float32 result), so the slopes
+    match it bit for bit."""
+    p = 1 << int(math.floor(math.log2(n_heads)))
+    slopes = torch.pow(2.0 ** (-8.0 / p), torch.arange(1, p + 1))
+    extra = min(p, n_heads - p)
+    if extra > 0:
+        odd = torch.arange(1, 2 * extra, 2)
+        slopes = torch.cat([slopes, torch.pow(2.0 ** (-8.0 / (2 * p)), odd)])
+    slopes = slopes.float()
+    return slopes.to(device) if device is not None else slopes
+
+
+def _bht_strides(t):
+    return (t.stride(0), t.stride(1), t.stride(2))
+
+
+def _unit_d(t):
+    return t if t.stride(-1) == 1 or t.shape[-1] == 1 else t.contiguous()
+
+
+def rational_attention_forward(q, k, v, alibi_slopes, scale, causal=True, eps=EPS):
+    """Returns (output [B,H,T,D] in q's dtype, L [B,H,T] fp32 without eps).
+
+    Always causal, as the reference (``causal`` is accepted and ignored,
+    forward.py:273,110). q, k, v may be strided views with a unit last-dim
+    stride (no copies are made for them)."""
+    assert q.is_cuda and k.is_cuda and v.is_cuda
+    assert q.shape == k.shape == v.shape
+    lib = _lib.load()
+    B, H, T, D = q.shape
+    k = k.to(q.dtype)
+    v = v.to(q.dtype)
+    q, k, v = _unit_d(q), _unit_d(k), _unit_d(v)
+    slopes = alibi_slopes.to(device=q.device, dtype=torch.float32).contiguous()
+    assert slopes.numel() == H, "alibi_slopes must have n_heads entries"
+    out = torch.empty((B, H, T, D), dtype=q.dtype, device=q.device)
+    L = torch.empty((B, H, T), dtype=torch.float32, device=q.device)
+    strides = _lib.i64_array(_bht_strides(q) + _bht_strides(k) + _bht_strides(v) +
+                             _bht_strides(out))
+    lstr = _lib.i64_array(_bht_strides(L))
+    _lib.check(lib.kat_attn_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                                L.data_ptr(), slopes.data_ptr(), B, H, T, D, strides, lstr,
+                                float(scale), float(eps), int(bool(causal)),
+                                _lib.dtype_code(q), _lib.stream(q)), "kat_attn_fwd")
+    return out, L

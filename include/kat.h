@@ -1,0 +1,151 @@
+/*
+ * kat.h -- C ABI of the MI355X (gfx950) rational-attention kernel library
+ * (libkat.so).
+ *
+ * Each entry point replaces one Triton launch of the reference
+ * `kernels` package (SkyeGunasekaran/fastAlgebraicTransformer); the file:line
+ * of the launch it replaces is given beside it. The reference's Python API
+ * (autograd Functions and functional wrappers) sits above this ABI unchanged.
+ *
+ * Conventions (all entry points):
+ *   - Device pointers are raw HIP device addresses; sizes and leading
+ *     dimensions ("ld_*") and strides are in ELEMENTS, not bytes.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the null stream).
+ *     Work is enqueued asynchronously; nothing synchronises the host.
+ *   - No entry point allocates device memory. Scratch comes from the caller
+ *     through a workspace pointer whose size the matching *_workspace_size()
+ *     function returns.
+ *   - Return 0 (KAT_OK) on success; otherwise a kat_status code, with a
+ *     human-readable message in kat_last_error() (per host thread).
+ *   - Every entry point is stateless and reentrant; concurrent calls on
+ *     different streams are independent.
+ *   - Arithmetic runs in fp32 (fp64 for KAT_F64 tensors) on inputs upcast
+ *     from `dtype`; outputs are stored in `dtype`, statistics (L, mu) in fp32.
+ */
+#ifndef KAT_H_
+#define KAT_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum kat_dtype {
+  KAT_F32 = 0,
+  KAT_BF16 = 1,
+  KAT_F16 = 2,
+  KAT_F64 = 3
+} kat_dtype;
+
+typedef enum kat_status {
+  KAT_OK = 0,
+  KAT_EINVAL = 1,       /* bad argument (null pointer, negative size, bad stride) */
+  KAT_EUNSUPPORTED = 2, /* valid but unsupported combination (dtype, head dim) */
+  KAT_EHIP = 3          /* HIP runtime error at launch */
+} kat_status;
+
+/* Library version (major*10000 + minor*100 + patch). */
+int kat_version(void);
+
+/* Message of the last failed call on this host thread ("" if none). */
+const char* kat_last_error(void);
+
+/* ------------------------------------------------------------------------
+ * rational softmax over the last dim: p = sigma(x)^4 / (sum sigma(x)^4 + eps)
+ * Replaces rational_softmax_fwd_kernel[(n_rows,)](...) at fused_ops.py:450-456
+ * (kernel fused_ops.py:52-106). x, p: [n_rows, n_cols] with row strides.
+ * ---------------------------------------------------------------------- */
+int kat_rsoftmax_fwd(const void* x, void* p, int64_t n_rows, int64_t n_cols,
+                     int64_t ld_x, int64_t ld_p, float eps, int dtype, void* stream);
+
+/* dx = p * g * (dy - <dy, p>), g = 2 / ((|x|+1)^2 (sigma(x) + eps)).
+ * Replaces rational_softmax_bwd_kernel[(n_rows,)](...) at fused_ops.py:479-485
+ * (kernel fused_ops.py:113-189). */
+int kat_rsoftmax_bwd(const void* dy, const void* x, const void* p, void* dx,
+                     int64_t n_rows, int64_t n_cols, int64_t ld_dy, int64_t ld_x,
+                     int64_t ld_p, int64_t ld_dx, float eps, int dtype, void* stream);
+
+/* ------------------------------------------------------------------------
+ * rational SwiGLU: out = gate * sigma(gate) * value (elementwise).
+ * Replaces swiglu_fwd_kernel[(n_rows,)](...) at fused_ops.py:506-511
+ * (kernel fused_ops.py:196-229). Row strides let gate/value be the two halves
+ * of one packed [rows, 2F] buffer without copies.
+ * ---------------------------------------------------------------------- */
+int kat_rswiglu_fwd(const void* gate, const void* value, void* out, int64_t n_rows,
+                    int64_t n_cols, int64_t ld_gate, int64_t ld_value, int64_t ld_out,
+                    int dtype, void* stream);
+
+/* dgate = dy * value * (sigma + gate * sigma'), dvalue = dy * gate * sigma.
+ * Replaces swiglu_bwd_kernel[(n_rows,)](...) at fused_ops.py:532-537
+ * (kernel fused_ops.py:236-288). */
+int kat_rswiglu_bwd(const void* dy, const void* gate, const void* value, void* dgate,
+                    void* dvalue, int64_t n_rows, int64_t n_cols, int64_t ld_dy,
+                    int64_t ld_gate, int64_t ld_value, int64_t ld_dgate, int64_t ld_dvalue,
+                    int dtype, void* stream);
+
+/* ------------------------------------------------------------------------
+ * mean-error norm: mu = mean|x| (stored fp32, without eps),
+ * y = x / (mu + eps) * w.  w: [n_cols] of dtype_w (KAT_F32 or == dtype).
+ * Replaces mean_error_norm_fwd_kernel[(n_rows,)](...) at fused_ops.py:558-564
+ * (kernel fused_ops.py:295-342).
+ * ---------------------------------------------------------------------- */
+int kat_men_fwd(const void* x, const void* w, void* y, float* mu, int64_t n_rows,
+                int64_t n_cols, int64_t ld_x, int64_t ld_y, float eps, int dtype,
+                int dtype_w, void* stream);
+
+/* Workspace bytes kat_men_bwd needs for (n_rows, n_cols, dtype). */
+size_t kat_men_bwd_workspace_size(int64_t n_rows, int64_t n_cols, int dtype);
+
+/* dx = dy*w/mu' - sign(x) * (sum(dy*y)/n) / mu',  mu' = mu + eps, sign(0) = 0;
+ * dw = sum_rows dy * x / mu'  (fp32; fp64 when dtype is KAT_F64), reduced
+ * deterministically. Replaces mean_error_norm_bwd_kernel[(n_rows,)](...) at
+ * fused_ops.py:585-591 (kernel fused_ops.py:349-423) together with the torch
+ * grad_weight reduction at fused_ops.py:593-597. */
+int kat_men_bwd(const void* dy, const void* x, const void* w, const float* mu, void* dx,
+                void* dw, void* workspace, size_t workspace_bytes, int64_t n_rows,
+                int64_t n_cols, int64_t ld_dy, int64_t ld_x, int64_t ld_dx, float eps,
+                int dtype, int dtype_w, void* stream);
+
+/* ------------------------------------------------------------------------
+ * rational attention, layout [B, H, T, D] with arbitrary (b, h, t) strides and
+ * unit d-stride. Always causal, as the reference (the `causal` flag is
+ * accepted and ignored, forward.py:273 / backward.py:282).
+ *   s_ij = scale * <q_i, k_j> - slope_h * (i - j)   (j <= i)
+ *   f_ij = sigma(s_ij)^4,  L_i = sum_j f_ij  (fp32, stored without eps)
+ *   o_i  = sum_j f_ij v_j / (L_i + eps)
+ * strides: 12 int64 = (b, h, t) strides of q, k, v, out, in that order.
+ * l_strides: 3 int64 = (b, h, t) strides of L. slopes: fp32 [H].
+ * Replaces the host wrapper + rational_attention_fwd_kernel[(B,H,T)] launch at
+ * forward.py:267-319 (kernel forward.py:49-159). dtype KAT_BF16/KAT_F16 use
+ * the MFMA kernel (D in {32, 64, 128}); KAT_F32 and other D (<= 256) use the
+ * fp32 tiled kernel.
+ * ---------------------------------------------------------------------- */
+int kat_attn_fwd(const void* q, const void* k, const void* v, void* out, float* L,
+                 const float* slopes, int64_t B, int64_t H, int64_t T, int64_t D,
+                 const int64_t* strides, const int64_t* l_strides, float scale, float eps,
+                 int causal, int dtype, void* stream);
+
+/* Workspace bytes kat_attn_bwd needs. */
+size_t kat_attn_bwd_workspace_size(int64_t B, int64_t H, int64_t T, int64_t D, int dtype);
+
+/* Gradients of kat_attn_fwd:
+ *   Delta_i = <dO_i, O_i>,  p = f / (L + eps),  g = 2 / ((|s|+1)^2 (sigma + eps))
+ *   dS = p g (<dO_i, v_j> - Delta_i),  dq = scale dS K,  dk = scale dS^T Q,
+ *   dv = P^T dO.
+ * strides: 24 int64 = (b, h, t) strides of q, k, v, out, dout, dq, dk, dv.
+ * Replaces the host wrapper + the dq and dkv launches at backward.py:273-341
+ * (kernels backward.py:62-158 and 165-266). Deterministic (no atomics). */
+int kat_attn_bwd(const void* q, const void* k, const void* v, const void* out,
+                 const float* L, const void* dout, void* dq, void* dk, void* dv,
+                 const float* slopes, void* workspace, size_t workspace_bytes, int64_t B,
+                 int64_t H, int64_t T, int64_t D, const int64_t* strides,
+                 const int64_t* l_strides, float scale, float eps, int causal, int dtype,
+                 void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KAT_H_ */

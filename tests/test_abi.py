@@ -1,0 +1,87 @@
+"""The C-ABI library loads and exports every symbol include/kat.h declares
+(CPU only: nothing here launches a kernel)."""
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from fastalgebraictransformer_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "kat.h")
+
+
+def _declared():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(kat_[a-z0-9_]+)\s*\(", src)))
+
+
+def test_library_is_built():
+    assert os.path.exists(_lib.LIB_PATH), "run __graft_entry__.build() first"
+
+
+def test_exports_match_header():
+    declared = _declared()
+    assert declared, "no entry points parsed from include/kat.h"
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = sorted(set(re.findall(r"\bT (kat_[a-z0-9_]+)\b", out)))
+    assert exported == declared
+    assert sorted(_lib.EXPORTED) == declared
+
+
+def test_load_and_version():
+    lib = _lib.load()
+    assert lib.kat_version() >= 100
+    for name in _declared():
+        assert hasattr(lib, name)
+
+
+def test_workspace_sizes():
+    lib = _lib.load()
+    assert lib.kat_attn_bwd_workspace_size(4, 16, 4096, 128, 1) >= 4 * 16 * 4096 * 4
+    assert lib.kat_attn_bwd_workspace_size(0, 16, 4096, 128, 1) == 0
+    n = lib.kat_men_bwd_workspace_size(16384, 4096, 1)
+    assert n > 0 and n % (4096 * 4) == 0
+    assert lib.kat_men_bwd_workspace_size(8, 96, 3) % (96 * 8) == 0
+
+
+def _msg(lib):
+    return lib.kat_last_error().decode()
+
+
+def test_argument_errors_are_reported_without_launching():
+    lib = _lib.load()
+    rc = lib.kat_rswiglu_fwd(None, None, None, -1, 4, 4, 4, 4, 1, None)
+    assert rc == 1 and "negative" in _msg(lib)
+    rc = lib.kat_rsoftmax_fwd(ctypes.c_void_p(16), None, 2, 8, 8, 8, 1e-6, 0, None)
+    assert rc == 1 and "null" in _msg(lib)
+    rc = lib.kat_rsoftmax_fwd(ctypes.c_void_p(16), ctypes.c_void_p(16), 2, 8, 4, 8, 1e-6, 0, None)
+    assert rc == 1 and "leading dimension" in _msg(lib)
+    # empty inputs are a no-op success
+    assert lib.kat_rswiglu_fwd(None, None, None, 0, 8, 8, 8, 8, 1, None) == 0
+    strides = _lib.i64_array([0] * 12)
+    lstr = _lib.i64_array([0] * 3)
+    rc = lib.kat_attn_fwd(None, None, None, None, None, None, 1, 1, 8, 512, strides, lstr, 1.0,
+                          1e-6, 1, 1, None)
+    assert rc == 2 and "head dim" in _msg(lib)
+    rc = lib.kat_attn_fwd(None, None, None, None, None, None, 1, 1, 8, 64, strides, lstr, 1.0,
+                          1e-6, 1, 1, None)
+    assert rc == 1 and "null" in _msg(lib)
+    rc = lib.kat_attn_bwd(*([None] * 11), 0, 1, 1, 8, 64, _lib.i64_array([0] * 24), lstr, 1.0, 1e-6,
+                          1, 1, None)
+    assert rc == 1
+    rc = lib.kat_men_fwd(ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
+                         ctypes.c_void_p(16), 2, 8, 8, 8, 1e-6, 3, 1, None)
+    assert rc == 2 and "weight dtype" in _msg(lib)
+
+
+def test_python_side_raises_on_bad_status():
+    with pytest.raises(RuntimeError, match="kat_rswiglu_fwd"):
+        lib = _lib.load()
+        _lib.check(lib.kat_rswiglu_fwd(None, None, None, -1, 4, 4, 4, 4, 1, None),
+                   "kat_rswiglu_fwd")

@@ -1,0 +1,174 @@
+"""GPU parity of rational attention (forward and backward) against the CPU
+oracle. Tolerances (written next to each check):
+  * fp32 (tiled fp32 kernels): <= 1e-5 of max|ref| on outputs and gradients;
+    the reference bars (tests.py:210-211) are 1e-3 / 1e-2 max-abs;
+  * bf16 / fp16 (MFMA kernels, fp32 accumulation): <= 2e-2 max-abs on o, dq,
+    dk, dv, and L within 1e-2 relative.
+"""
+
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import fastalgebraictransformer_amd as F
+import oracle as O
+from _util import golden, max_abs
+
+pytestmark = pytest.mark.gpu
+dev = "cuda"
+
+
+def _t(a, dtype=torch.float32):
+    return torch.from_numpy(np.asarray(a)).to(dev, dtype)
+
+
+def _inputs(seed, B, H, T, D, dtype):
+    g = torch.Generator().manual_seed(seed)
+    return [torch.randn(B, H, T, D, generator=g).to(dtype).to(dev) for _ in range(4)]
+
+
+def _run(q, k, v, do, slopes, scale):
+    q, k, v = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+    o, L = F.rational_attention_forward(q, k, v, slopes, scale)
+    out = F.rational_attention(q, k, v, slopes, scale)
+    assert torch.equal(out, o)
+    out.backward(do)
+    torch.cuda.synchronize()
+    return o, L, q.grad, k.grad, v.grad
+
+
+def _rel_max(a, b):
+    return max_abs(a, b) / max(1e-30, float(b.detach().abs().max()))
+
+
+# ----------------------------------------------------------------- fp32 ----
+
+def test_golden_fp32(gpu):
+    z = golden("attn_f32")
+    q, k, v, do = (_t(z[n]) for n in ("q", "k", "v", "do"))
+    o, L, dq, dk, dv = _run(q, k, v, do, _t(z["slopes"]), float(z["scale"]))
+    for name, got in (("o", o), ("L", L), ("dq", dq), ("dk", dk), ("dv", dv)):
+        assert _rel_max(got, torch.from_numpy(z[name])) <= 1e-5, name
+
+
+def test_config1_fp32(gpu):
+    # B=2, H=12, S=512, D=64 fp32; scale 1/8; slopes 2^(-8(i+1)/12)
+    B, H, T, D = 2, 12, 512, 64
+    q, k, v, do = _inputs(1, B, H, T, D, torch.float32)
+    slopes = torch.tensor([2.0 ** (-8.0 * (i + 1) / H) for i in range(H)], dtype=torch.float32)
+    scale = 1.0 / math.sqrt(D)
+    o, L, dq, dk, dv = _run(q, k, v, do, slopes.to(dev), scale)
+    ro, rL = O.attention_fwd(q, k, v, slopes, scale)
+    assert _rel_max(o, ro) <= 1e-5 and _rel_max(L, rL) <= 1e-5
+    assert max_abs(o, ro) < 1e-3  # tests.py:210
+    rq, rk, rv = O.attention_bwd(q, k, v, o.detach(), L, do, slopes, scale)
+    for name, got, ref in (("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
+        assert max_abs(got, ref) < 1e-2, name  # tests.py:211
+        assert _rel_max(got, ref) <= 1e-5, name
+
+
+@pytest.mark.parametrize("B,H,T,D", [(1, 4, 32, 32), (2, 8, 64, 64), (1, 4, 128, 32),
+                                     (1, 3, 33, 20), (1, 2, 300, 160)])
+def test_reference_shapes_fp32(gpu, B, H, T, D):
+    # tests.py:183 shapes (+ ragged T / odd D), slopes from compute_alibi_slopes
+    q, k, v, do = _inputs(T + D, B, H, T, D, torch.float32)
+    slopes = F.compute_alibi_slopes(H)
+    scale = 1.0 / math.sqrt(D)
+    o, L, dq, dk, dv = _run(q, k, v, do, slopes.to(dev), scale)
+    ro, rL = O.attention_fwd(q, k, v, slopes, scale)
+    rq, rk, rv = O.attention_bwd(q, k, v, o.detach(), L, do, slopes, scale)
+    assert _rel_max(o, ro) <= 1e-5 and _rel_max(L, rL) <= 1e-5
+    for name, got, ref in (("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
+        assert _rel_max(got, ref) <= 1e-5, name
+
+
+# ------------------------------------------------------------ bf16 / fp16 ----
+
+def _check_lowp(o, L, dq, dk, dv, q, k, v, do, slopes, scale, sel=None):
+    """Compare against the fp32-upcast oracle on the same (rounded) inputs;
+    ``sel`` restricts the oracle to a subset of (b, h) pairs."""
+    if sel is not None:
+        b, h = sel
+        q, k, v, do = (t[b:b + 1, h:h + 1] for t in (q, k, v, do))
+        o, L, dq, dk, dv = (t[b:b + 1, h:h + 1] for t in (o, L, dq, dk, dv))
+        slopes = slopes[h:h + 1]
+    ro, rL = O.attention_fwd(q, k, v, slopes, scale, dtype=torch.float32)
+    assert max_abs(o, ro) <= 2e-2, ("o", max_abs(o, ro))
+    assert _rel_max(L, rL) <= 1e-2, ("L", _rel_max(L, rL))
+    # backward from the GPU forward's own O and L, as the autograd path does
+    rq, rk, rv = O.attention_bwd(q, k, v, o, L, do, slopes, scale, dtype=torch.float32)
+    for name, got, ref in (("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
+        assert max_abs(got, ref) <= 2e-2, (name, max_abs(got, ref))
+
+
+@pytest.mark.parametrize("name", ["attn_bf16_d64", "attn_bf16_d128"])
+def test_golden_bf16(gpu, name):
+    z = golden(name)
+    q, k, v, do = (_t(z[n], torch.bfloat16) for n in ("q", "k", "v", "do"))
+    o, L, dq, dk, dv = _run(q, k, v, do, _t(z["slopes"]), float(z["scale"]))
+    assert max_abs(o, torch.from_numpy(z["o"])) <= 2e-2
+    _check_lowp(o, L, dq, dk, dv, q, k, v, do, _t(z["slopes"]).cpu(), float(z["scale"]))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("B,H,T,D", [(1, 2, 64, 64), (1, 3, 200, 128), (2, 2, 333, 64),
+                                     (1, 2, 257, 32), (1, 1, 1, 128), (1, 2, 1000, 128)])
+def test_lowp_shapes(gpu, dtype, B, H, T, D):
+    q, k, v, do = _inputs(7 * T + D, B, H, T, D, dtype)
+    slopes = F.compute_alibi_slopes(H)
+    scale = 1.0 / math.sqrt(D)
+    o, L, dq, dk, dv = _run(q, k, v, do, slopes.to(dev), scale)
+    _check_lowp(o, L, dq, dk, dv, q, k, v, do, slopes, scale)
+
+
+def test_config3_bf16_sampled_heads(gpu):
+    # B=4, H=16, S=4096, D=128 bf16; slopes 2^(-(i+1)/2); heads are independent,
+    # so the oracle checks three (b, h) pairs, including the smallest and
+    # largest slope
+    B, H, T, D = 4, 16, 4096, 128
+    q, k, v, do = _inputs(3, B, H, T, D, torch.bfloat16)
+    slopes = torch.tensor([2.0 ** (-(i + 1) / 2) for i in range(H)], dtype=torch.float32)
+    scale = 1.0 / math.sqrt(D)
+    o, L, dq, dk, dv = _run(q, k, v, do, slopes.to(dev), scale)
+    for sel in ((0, 0), (2, 7), (3, 15)):
+        _check_lowp(o, L, dq, dk, dv, q, k, v, do, slopes, scale, sel=sel)
+    for t in (o, L, dq, dk, dv):
+        assert bool(torch.isfinite(t).all())
+
+
+def test_mfma_matches_tiled_kernel(gpu, monkeypatch):
+    B, H, T, D = 1, 4, 384, 128
+    q, k, v, do = _inputs(11, B, H, T, D, torch.bfloat16)
+    slopes = F.compute_alibi_slopes(H).to(dev)
+    a = _run(q, k, v, do, slopes, 0.09)
+    monkeypatch.setenv("KAT_ATTN_IMPL", "tiled")
+    b = _run(q, k, v, do, slopes, 0.09)
+    for x, y, n in zip(a, b, ("o", "L", "dq", "dk", "dv")):
+        tol = 1e-2 * max(1.0, float(y.abs().max())) if n == "L" else 2e-2
+        assert max_abs(x, y) <= tol, n
+
+
+def test_strided_qkv_views_match_contiguous(gpu):
+    # the model's layout: one [B, T, 3, H, D] buffer permuted to three views
+    B, T, H, D = 2, 150, 4, 64
+    g = torch.Generator().manual_seed(5)
+    qkv = torch.randn(B, T, 3, H, D, generator=g).to(torch.bfloat16).to(dev)
+    q, k, v = qkv.permute(2, 0, 3, 1, 4)
+    do = torch.randn(B, H, T, D, generator=g).to(torch.bfloat16).to(dev)
+    slopes = F.compute_alibi_slopes(H).to(dev)
+    a = _run(q, k, v, do, slopes, 0.125)
+    b = _run(q.contiguous(), k.contiguous(), v.contiguous(), do, slopes, 0.125)
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+
+
+def test_backward_is_deterministic(gpu):
+    q, k, v, do = _inputs(9, 1, 2, 512, 128, torch.bfloat16)
+    slopes = F.compute_alibi_slopes(2).to(dev)
+    a = _run(q, k, v, do, slopes, 0.088)
+    b = _run(q, k, v, do, slopes, 0.088)
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)

@@ -1,0 +1,61 @@
+"""AlgebraicTransformerLM on the GPU kernels against the same module's CPU
+path (the reference's torch formulation, algebraic_model.py:112-136)."""
+
+import math
+
+import pytest
+import torch
+
+import fastalgebraictransformer_amd as F
+
+pytestmark = pytest.mark.gpu
+
+
+def test_model_gpu_matches_cpu_path_fp32(gpu):
+    torch.manual_seed(0)
+    m = F.AlgebraicTransformerLM(vocab_size=1000, d_model=256, n_head=4, n_layers=2, dropout=0.0)
+    ids = torch.randint(0, 1000, (2, 64))
+    logits_c, loss_c = m(ids, labels=ids)
+    loss_c.backward()
+    grads_c = {n: p.grad.clone() for n, p in m.named_parameters()}
+    m.zero_grad(set_to_none=True)
+    mg = m.cuda()
+    logits_g, loss_g = mg(ids.cuda(), labels=ids.cuda())
+    loss_g.backward()
+    # fp32 throughout; the CPU path includes the -1e4-filled keys (~6e-18 each)
+    assert abs(loss_g.item() - loss_c.item()) <= 1e-5 * abs(loss_c.item())
+    assert torch.allclose(logits_g.cpu(), logits_c, rtol=1e-4, atol=1e-4)
+    for n, p in mg.named_parameters():
+        gc = grads_c[n]
+        err = float((p.grad.cpu() - gc).abs().max())
+        assert err <= 1e-4 * max(1.0, float(gc.abs().max())), (n, err)
+
+
+def test_model_small_bf16_autocast_step(gpu):
+    # the reference model smoke test (tests.py:275-306) under bf16 autocast
+    torch.manual_seed(0)
+    m = F.AlgebraicTransformerLM(vocab_size=1000, d_model=256, n_head=4, n_layers=2).cuda()
+    ids = torch.randint(0, 1000, (2, 64), device="cuda")
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        logits, loss = m(ids, labels=ids)
+    loss.backward()
+    assert math.isfinite(loss.item()) and abs(loss.item() - math.log(1000)) < 1.0
+    gn = math.sqrt(sum(float(p.grad.float().norm()) ** 2 for p in m.parameters()))
+    assert math.isfinite(gn) and gn > 0
+
+
+def test_model_gradient_checkpointing_matches(gpu):
+    torch.manual_seed(1)
+    m = F.AlgebraicTransformerLM(vocab_size=500, d_model=128, n_head=2, n_layers=2,
+                                 dropout=0.0).cuda()
+    ids = torch.randint(0, 500, (2, 48), device="cuda")
+    _, l1 = m(ids, labels=ids)
+    l1.backward()
+    g1 = [p.grad.clone() for p in m.parameters()]
+    m.zero_grad(set_to_none=True)
+    m.gradient_checkpointing = True
+    _, l2 = m(ids, labels=ids)
+    l2.backward()
+    assert torch.equal(l1, l2)
+    for a, p in zip(g1, m.parameters()):
+        assert torch.equal(a, p.grad)

@@ -1,0 +1,117 @@
+"""Host-side logic of the Python API (CPU only, no kernel launches)."""
+
+import math
+
+import pytest
+import torch
+
+import fastalgebraictransformer_amd as F
+import oracle as O
+from fastalgebraictransformer_amd import _lib
+
+
+def test_public_names_match_reference_surface():
+    # reference __init__.py:39-63
+    expected = {
+        "rational_softmax", "rational_swiglu", "mean_error_norm", "RationalSoftmax",
+        "RationalSwiGLU", "MeanErrorNorm", "EPS", "rational_attention_forward",
+        "compute_alibi_slopes", "rational_attention", "rational_attention_backward",
+        "RationalAttentionFunction", "AlgebraicTransformerLM", "RationalMR",
+        "AlgebraicAttention", "AlgebraicBlock", "create_small_model", "create_medium_model",
+        "create_large_model"}
+    assert set(F.__all__) == expected
+    for n in expected:
+        assert hasattr(F, n)
+    assert F.RationalSwiGLUModule is F.algebraic_model.RationalSwiGLU
+    assert F.EPS == 1e-6 and F.fused_ops.NEG_INF == -1e4
+
+
+def test_install_as_reference_name():
+    F.install_as("kernels")
+    from kernels.backward import rational_attention  # noqa: F401
+    from kernels.fused_ops import rational_softmax
+    assert rational_softmax is F.rational_softmax
+
+
+def test_alibi_slopes_match_oracle_bitwise():
+    for n in (1, 2, 3, 4, 5, 8, 12, 16, 24, 32, 48):
+        assert torch.equal(F.compute_alibi_slopes(n), O.alibi_slopes(n))
+    assert F.compute_alibi_slopes(4, device="cpu").device.type == "cpu"
+
+
+def test_autograd_functions_reject_cpu_tensors():
+    x = torch.randn(2, 8)
+    with pytest.raises(AssertionError):
+        F.RationalSoftmax.apply(x, 1e-6)
+    with pytest.raises(AssertionError):
+        F.RationalSwiGLU.apply(x, x)
+    with pytest.raises(AssertionError):
+        F.MeanErrorNorm.apply(x, torch.ones(8), 1e-6)
+    q = torch.randn(1, 2, 4, 8)
+    with pytest.raises(AssertionError):
+        F.rational_attention_forward(q, q, q, torch.ones(2), 0.3)
+    with pytest.raises(AssertionError):
+        F.rational_attention(q, q, q, torch.ones(2), 0.3)
+
+
+def test_cpu_functional_paths_follow_reference_formulas():
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(3, 5, 40, generator=g, dtype=torch.float64)
+    v = torch.randn(3, 5, 40, generator=g, dtype=torch.float64)
+    w = torch.randn(40, generator=g, dtype=torch.float64)
+    assert torch.allclose(F.rational_softmax(x), O.rational_softmax_fwd(x), rtol=1e-14, atol=0)
+    assert torch.allclose(F.rational_swiglu(x, v), O.swiglu_fwd(x, v), rtol=1e-14, atol=0)
+    assert torch.allclose(F.mean_error_norm(x, w), O.mean_error_norm_fwd(x, w)[0], rtol=1e-14,
+                          atol=0)
+
+
+def test_rows2d_views_without_copy():
+    gv = torch.randn(2, 7, 2 * 48)
+    gate, value = gv.chunk(2, dim=-1)
+    g2, ld = _lib.rows2d(gate)
+    assert ld == 96 and g2.shape == (14, 48) and g2.data_ptr() == gate.data_ptr()
+    v2, ldv = _lib.rows2d(value)
+    assert ldv == 96 and v2.data_ptr() == value.data_ptr()
+    t = torch.randn(6, 10).t()  # non-unit last-dim stride: copied
+    t2, ldt = _lib.rows2d(t)
+    assert ldt == 6 and t2.is_contiguous()
+    e = torch.randn(1, 5).expand(4, 5)  # overlapping rows: copied
+    e2, lde = _lib.rows2d(e)
+    assert lde == 5 and e2.is_contiguous()
+    s, lds = _lib.rows2d(torch.randn(9))
+    assert s.shape == (1, 9) and lds == 9
+
+
+def test_dtype_codes():
+    assert _lib.dtype_code(torch.empty(1, dtype=torch.bfloat16)) == 1
+    with pytest.raises(TypeError):
+        _lib.dtype_code(torch.empty(1, dtype=torch.int32))
+
+
+def test_model_cpu_path_matches_harness_attention():
+    torch.manual_seed(0)
+    m = F.AlgebraicTransformerLM(vocab_size=50, d_model=32, n_head=4, n_layers=2, dropout=0.0)
+    ids = torch.randint(0, 50, (2, 9))
+    logits, loss = m(ids, labels=ids)
+    assert logits.shape == (2, 9, 50) and loss.ndim == 0 and math.isfinite(loss.item())
+    loss.backward()
+    assert all(p.grad is not None for p in m.parameters())
+    # the attention module's CPU path is the reference harness formulation
+    att = m.blocks[0].attn
+    x = torch.randn(2, 9, 32)
+    q, k, v = att.qkv(x).view(2, 9, 3, 4, 8).permute(2, 0, 3, 1, 4)
+    ref = O.harness_attention(q, k, v, att.alibi_slopes, att.scale)
+    got = att._cpu_attention(q, k, v, None)
+    assert torch.allclose(got, ref.to(got.dtype), rtol=1e-5, atol=1e-6)
+
+
+def test_model_state_dict_names_match_reference_layout():
+    m = F.create_small_model(vocab_size=100)
+    names = set(m.state_dict().keys())
+    for n in ("embed.weight", "head.weight", "norm.weight", "blocks.0.attn.qkv.weight",
+              "blocks.0.attn.out.weight", "blocks.0.attn.alibi_slopes",
+              "blocks.0.ffn.w_gate_val.weight", "blocks.0.ffn.w_out.weight",
+              "blocks.0.norm1.weight", "blocks.0.norm2.weight", "blocks.11.norm2.weight"):
+        assert n in names, n
+    assert m.embed.weight is m.head.weight
+    assert m.blocks[0].ffn.w_gate_val.weight.shape == (2 * int(768 * 8 / 3), 768)
