@@ -50,9 +50,11 @@ template <typename T> bool rows16(const void* p, const int64_t* s) {
          (s[1] * (int64_t)sizeof(T)) % 16 == 0 && (s[2] * (int64_t)sizeof(T)) % 16 == 0;
 }
 
-size_t delta_bytes(int64_t B, int64_t H, int64_t T) {
+// workspace: Delta [B*H*T] fp32, then cinv [B*H*T] fp32 (each 256-byte aligned)
+size_t stat_bytes(int64_t B, int64_t H, int64_t T) {
   return (((size_t)(B * H * T) * sizeof(float)) + 255) & ~(size_t)255;
 }
+size_t delta_bytes(int64_t B, int64_t H, int64_t T) { return 2 * stat_bytes(B, H, T); }
 
 }  // namespace
 
@@ -65,13 +67,14 @@ template <typename T> static int attn_fwd_t(const AttnArgs& a, hipStream_t st) {
   return attn_fwd_generic<T>(a, st);
 }
 
-template <typename T> static int attn_bwd_t(const AttnArgs& a, float* delta, hipStream_t st) {
-  if (int rc = attn_delta<T>(a, delta, st)) return rc;
+template <typename T>
+static int attn_bwd_t(const AttnArgs& a, float* delta, float* cinv, hipStream_t st) {
+  if (int rc = attn_delta<T>(a, delta, cinv, st)) return rc;
   if (!force_tiled() && attn_mfma_supported(a.D) && rows16<T>(a.q, a.sq) &&
       rows16<T>(a.k, a.sk) && rows16<T>(a.v, a.sv) && rows16<T>(a.o, a.so) &&
       rows16<T>(a.dout, a.sdo) && rows16<T>(a.dq, a.sdq) && rows16<T>(a.dk, a.sdk) &&
       rows16<T>(a.dv, a.sdv)) {
-    const int rc = attn_bwd_mfma<T>(a, delta, st);
+    const int rc = attn_bwd_mfma<T>(a, delta, cinv, st);
     if (rc != KAT_EUNSUPPORTED) return rc;
   }
   return attn_bwd_generic<T>(a, delta, st);
@@ -141,13 +144,14 @@ extern "C" int kat_attn_bwd(const void* q, const void* k, const void* v, const v
   a.scale = scale;
   a.eps = eps;
   float* delta = reinterpret_cast<float*>(workspace);
+  float* cinv = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + stat_bytes(B, H, T));
   const hipStream_t st = as_stream(stream);
   switch (dtype) {
     case KAT_F32:
-      if (int rc = attn_delta<float>(a, delta, st)) return rc;
+      if (int rc = attn_delta<float>(a, delta, cinv, st)) return rc;
       return attn_bwd_generic<float>(a, delta, st);
-    case KAT_BF16: return attn_bwd_t<bf16>(a, delta, st);
-    case KAT_F16: return attn_bwd_t<f16>(a, delta, st);
+    case KAT_BF16: return attn_bwd_t<bf16>(a, delta, cinv, st);
+    case KAT_F16: return attn_bwd_t<f16>(a, delta, cinv, st);
     default: return fail(KAT_EUNSUPPORTED, "%s: unsupported dtype %d", nm, dtype);
   }
 }

@@ -25,12 +25,14 @@ struct AttnArgs {
 };
 
 template <typename T> int attn_fwd_generic(const AttnArgs& a, hipStream_t st);
-template <typename T> int attn_delta(const AttnArgs& a, float* delta, hipStream_t st);
+// Delta_i = <dO_i, O_i> and cinv_i = 1 / (16 (L_i + eps)), both [B*H*T] fp32.
+template <typename T> int attn_delta(const AttnArgs& a, float* delta, float* cinv, hipStream_t st);
 template <typename T> int attn_bwd_generic(const AttnArgs& a, const float* delta, hipStream_t st);
 
 // bf16 / fp16 MFMA kernels; return KAT_EUNSUPPORTED when the shape is not covered.
 template <typename T> int attn_fwd_mfma(const AttnArgs& a, hipStream_t st);
-template <typename T> int attn_bwd_mfma(const AttnArgs& a, const float* delta, hipStream_t st);
+template <typename T>
+int attn_bwd_mfma(const AttnArgs& a, const float* delta, const float* cinv, hipStream_t st);
 bool attn_mfma_supported(int D);
 
 }  // namespace kat

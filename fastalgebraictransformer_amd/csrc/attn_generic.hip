@@ -99,22 +99,40 @@ __global__ __launch_bounds__(256) void attn_fwd_generic_k(AttnArgs a) {
   }
 }
 
-// Delta_i = <dO_i, O_i> (backward.py:117). One wave per row.
-template <typename T>
-__global__ __launch_bounds__(256) void attn_delta_k(AttnArgs a, float* __restrict__ delta) {
-  const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+// Delta_i = <dO_i, O_i> (backward.py:117) and cinv_i = 1 / (16 (L_i + eps)).
+// 16 lanes per row, 16-byte loads (VEC16) or one wave per row, scalar loads.
+template <typename T, bool VEC16>
+__global__ __launch_bounds__(256) void attn_delta_k(AttnArgs a, float* __restrict__ delta,
+                                                    float* __restrict__ cinv) {
+  constexpr int LPR = VEC16 ? 16 : 64;  // lanes per row
+  constexpr int V = VEC16 ? 16 / (int)sizeof(T) : 1;
+  const int sub = threadIdx.x % LPR;
+  const int64_t row = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / LPR;
   const int64_t nrows = (int64_t)a.B * a.H * a.T;
-  if (row >= nrows) return;
-  const int i = (int)(row % a.T);
-  const int64_t bh = row / a.T;
+  const bool live = row < nrows;
+  const int64_t rr = live ? row : 0;
+  const int i = (int)(rr % a.T);
+  const int64_t bh = rr / a.T;
   const int b = (int)(bh / a.H), h = (int)(bh % a.H);
   const T* o = (const T*)a.o + b * a.so[0] + h * a.so[1] + (int64_t)i * a.so[2];
   const T* dO = (const T*)a.dout + b * a.sdo[0] + h * a.sdo[1] + (int64_t)i * a.sdo[2];
   float s = 0.f;
-  for (int d = lane; d < a.D; d += 64) s = fmaf((float)dO[d], (float)o[d], s);
-  s = wave_sum(s);
-  if (lane == 0) delta[row] = s;
+  if (live) {
+    for (int d = sub * V; d < a.D; d += LPR * V) {
+      float ov[V], gv[V];
+      load_acc<T, V>(o + d, ov);
+      load_acc<T, V>(dO + d, gv);
+#pragma unroll
+      for (int e = 0; e < V; ++e) s = fmaf(gv[e], ov[e], s);
+    }
+  }
+#pragma unroll
+  for (int off = LPR / 2; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+  if (live && sub == 0) {
+    delta[row] = s;
+    const float l = a.L[b * a.sl[0] + h * a.sl[1] + (int64_t)i * a.sl[2]];
+    cinv[row] = 1.f / (16.f * (l + a.eps));
+  }
 }
 
 template <typename T, int DMAX>
@@ -273,10 +291,18 @@ template <typename T> int attn_fwd_generic(const AttnArgs& a, hipStream_t st) {
   return check_launch("kat_attn_fwd (fp32 tiled)");
 }
 
-template <typename T> int attn_delta(const AttnArgs& a, float* delta, hipStream_t st) {
+template <typename T> int attn_delta(const AttnArgs& a, float* delta, float* cinv, hipStream_t st) {
   const int64_t rows = (int64_t)a.B * a.H * a.T;
-  hipLaunchKernelGGL((attn_delta_k<T>), dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st, a,
-                     delta);
+  const bool vec = a.D % (16 / (int)sizeof(T)) == 0 && aligned16(a.o) && aligned16(a.dout) &&
+                   (a.so[0] * (int64_t)sizeof(T)) % 16 == 0 && (a.so[1] * (int64_t)sizeof(T)) % 16 == 0 &&
+                   (a.so[2] * (int64_t)sizeof(T)) % 16 == 0 && (a.sdo[0] * (int64_t)sizeof(T)) % 16 == 0 &&
+                   (a.sdo[1] * (int64_t)sizeof(T)) % 16 == 0 && (a.sdo[2] * (int64_t)sizeof(T)) % 16 == 0;
+  if (vec)
+    hipLaunchKernelGGL((attn_delta_k<T, true>), dim3((unsigned)((rows * 16 + 255) / 256)), dim3(256),
+                       0, st, a, delta, cinv);
+  else
+    hipLaunchKernelGGL((attn_delta_k<T, false>), dim3((unsigned)((rows * 64 + 255) / 256)),
+                       dim3(256), 0, st, a, delta, cinv);
   return check_launch("kat_attn_bwd (delta)");
 }
 
@@ -293,9 +319,9 @@ template <typename T> int attn_bwd_generic(const AttnArgs& a, const float* delta
 template int attn_fwd_generic<float>(const AttnArgs&, hipStream_t);
 template int attn_fwd_generic<bf16>(const AttnArgs&, hipStream_t);
 template int attn_fwd_generic<f16>(const AttnArgs&, hipStream_t);
-template int attn_delta<float>(const AttnArgs&, float*, hipStream_t);
-template int attn_delta<bf16>(const AttnArgs&, float*, hipStream_t);
-template int attn_delta<f16>(const AttnArgs&, float*, hipStream_t);
+template int attn_delta<float>(const AttnArgs&, float*, float*, hipStream_t);
+template int attn_delta<bf16>(const AttnArgs&, float*, float*, hipStream_t);
+template int attn_delta<f16>(const AttnArgs&, float*, float*, hipStream_t);
 template int attn_bwd_generic<float>(const AttnArgs&, const float*, hipStream_t);
 template int attn_bwd_generic<bf16>(const AttnArgs&, const float*, hipStream_t);
 template int attn_bwd_generic<f16>(const AttnArgs&, const float*, hipStream_t);

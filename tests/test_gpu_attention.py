@@ -2,8 +2,12 @@
 oracle. Tolerances (written next to each check):
   * fp32 (tiled fp32 kernels): <= 1e-5 of max|ref| on outputs and gradients;
     the reference bars (tests.py:210-211) are 1e-3 / 1e-2 max-abs;
-  * bf16 / fp16 (MFMA kernels, fp32 accumulation): <= 2e-2 max-abs on o, dq,
-    dk, dv, and L within 1e-2 relative.
+  * bf16 / fp16 (MFMA kernels, fp32 accumulation): 2e-2 max-abs on o, dq,
+    dk, dv on top of the output's own quantisation:
+    elementwise |got - ref| <= 2e-2 + 1 ulp(ref) of the output dtype. The
+    outputs are stored in the input dtype (as the reference does), and for
+    |x| >= 4 half a bf16 ulp alone is >= 1.6e-2, so a bare 2e-2 bar cannot be
+    met by any bf16 result there. L (fp32) within 1e-2 relative.
 """
 
 import math
@@ -15,7 +19,7 @@ import torch
 
 import fastalgebraictransformer_amd as F
 import oracle as O
-from _util import golden, max_abs
+from _util import bf16_ulp, golden, max_abs
 
 pytestmark = pytest.mark.gpu
 dev = "cuda"
@@ -42,6 +46,24 @@ def _run(q, k, v, do, slopes, scale):
 
 def _rel_max(a, b):
     return max_abs(a, b) / max(1e-30, float(b.detach().abs().max()))
+
+
+def _ulp(ref, dtype):
+    if dtype == torch.float16:
+        a = ref.abs().to(torch.float64).clamp_min(2.0 ** -14)
+        return torch.pow(2.0, torch.floor(torch.log2(a)) - 10)
+    return bf16_ulp(ref)
+
+
+def assert_lowp(got, ref, dtype, name, bar=2e-2):
+    """|got - ref| <= bar + 1 ulp_dtype(ref), elementwise."""
+    got = got.detach().to("cpu", torch.float64)
+    ref = ref.detach().to("cpu", torch.float64)
+    err = (got - ref).abs()
+    excess = err - (bar + _ulp(ref, dtype))
+    worst = float(excess.max())
+    assert worst <= 0, (f"{name}: max err {float(err.max()):.3e} (max|ref| "
+                        f"{float(ref.abs().max()):.3e}) exceeds 2e-2 + 1 ulp by {worst:.3e}")
 
 
 # ----------------------------------------------------------------- fp32 ----
@@ -95,13 +117,14 @@ def _check_lowp(o, L, dq, dk, dv, q, k, v, do, slopes, scale, sel=None):
         q, k, v, do = (t[b:b + 1, h:h + 1] for t in (q, k, v, do))
         o, L, dq, dk, dv = (t[b:b + 1, h:h + 1] for t in (o, L, dq, dk, dv))
         slopes = slopes[h:h + 1]
+    dt = q.dtype
     ro, rL = O.attention_fwd(q, k, v, slopes, scale, dtype=torch.float32)
-    assert max_abs(o, ro) <= 2e-2, ("o", max_abs(o, ro))
+    assert_lowp(o, ro, dt, "o")
     assert _rel_max(L, rL) <= 1e-2, ("L", _rel_max(L, rL))
     # backward from the GPU forward's own O and L, as the autograd path does
     rq, rk, rv = O.attention_bwd(q, k, v, o, L, do, slopes, scale, dtype=torch.float32)
     for name, got, ref in (("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
-        assert max_abs(got, ref) <= 2e-2, (name, max_abs(got, ref))
+        assert_lowp(got, ref, dt, name)
 
 
 @pytest.mark.parametrize("name", ["attn_bf16_d64", "attn_bf16_d128"])
@@ -109,7 +132,7 @@ def test_golden_bf16(gpu, name):
     z = golden(name)
     q, k, v, do = (_t(z[n], torch.bfloat16) for n in ("q", "k", "v", "do"))
     o, L, dq, dk, dv = _run(q, k, v, do, _t(z["slopes"]), float(z["scale"]))
-    assert max_abs(o, torch.from_numpy(z["o"])) <= 2e-2
+    assert_lowp(o, torch.from_numpy(z["o"]), torch.bfloat16, "o (fixture)")
     _check_lowp(o, L, dq, dk, dv, q, k, v, do, _t(z["slopes"]).cpu(), float(z["scale"]))
 
 
@@ -140,15 +163,23 @@ def test_config3_bf16_sampled_heads(gpu):
 
 
 def test_mfma_matches_tiled_kernel(gpu, monkeypatch):
+    # the two kernel families on identical inputs: forward on (q, k, v); the
+    # backward on the same (q, k, v, O, L, dO). Both results are bf16, so the
+    # bar is 2e-2 + 2 ulp (one rounding on each side).
     B, H, T, D = 1, 4, 384, 128
     q, k, v, do = _inputs(11, B, H, T, D, torch.bfloat16)
     slopes = F.compute_alibi_slopes(H).to(dev)
-    a = _run(q, k, v, do, slopes, 0.09)
+    o_m, L_m = F.rational_attention_forward(q, k, v, slopes, 0.09)
+    g_m = F.rational_attention_backward(q, k, v, o_m, L_m, do, slopes, 0.09)
     monkeypatch.setenv("KAT_ATTN_IMPL", "tiled")
-    b = _run(q, k, v, do, slopes, 0.09)
-    for x, y, n in zip(a, b, ("o", "L", "dq", "dk", "dv")):
-        tol = 1e-2 * max(1.0, float(y.abs().max())) if n == "L" else 2e-2
-        assert max_abs(x, y) <= tol, n
+    o_t, L_t = F.rational_attention_forward(q, k, v, slopes, 0.09)
+    g_t = F.rational_attention_backward(q, k, v, o_m, L_m, do, slopes, 0.09)
+    torch.cuda.synchronize()
+    assert _rel_max(L_m, L_t) <= 1e-3
+    for x, y, n in zip((o_m,) + tuple(g_m), (o_t,) + tuple(g_t), ("o", "dq", "dk", "dv")):
+        err = (x.double() - y.double()).abs()
+        bound = 2e-2 + 2 * _ulp(y.cpu(), torch.bfloat16).to(dev)
+        assert bool((err <= bound).all()), (n, float(err.max()))
 
 
 def test_strided_qkv_views_match_contiguous(gpu):
