@@ -23,6 +23,7 @@
 // subtile and element 4 + i key 4g + i of the second.
 
 #include <algorithm>
+#include <type_traits>
 
 #include "attn_common.h"
 #include "kat_common.h"
@@ -64,6 +65,24 @@ template <> struct Mfma<f16> {
     return __builtin_bit_cast(uint32_t, b);
   }
 };
+
+// Block order. Workgroups are dispatched round-robin over the 8 XCDs (block
+// id i runs on XCD i % 8), and each XCD has its own L2. Heads are assigned to
+// XCDs (head h on XCD h % 8, when B*H is a multiple of 8) and each XCD walks
+// its heads one after another, longest (causal) tiles first, so the K/V (or
+// Q/dO) of the one or two heads in flight per XCD stay L2-resident.
+// Returns the (b*H + h) index and the tile rank (0 = most work).
+__device__ __forceinline__ void block_order(int id, int n_tiles, int BH, int& bh, int& rank) {
+  if ((BH & 7) == 0) {
+    const int xcd = id & 7, slot = id >> 3;
+    const int hl = slot / n_tiles;
+    rank = slot - hl * n_tiles;
+    bh = xcd + 8 * hl;
+  } else {
+    bh = id / n_tiles;
+    rank = id - bh * n_tiles;
+  }
+}
 
 constexpr int FBM = 128;  // queries per block
 constexpr int FBN = 64;   // keys per tile
@@ -114,20 +133,66 @@ template <> __device__ __forceinline__ i16x8 frag_to_f16<bf16>(const i16x8& v) {
   return __builtin_bit_cast(i16x8, o);
 }
 
+// Shared pieces of the forward and dQ kernels: 64-key K/V tiles staged
+// global -> VGPRs -> LDS (double-buffered), rows zero-filled past T.
+template <typename T, int D> struct KvStager {
+  static constexpr int LD = FwdSmem<D>::LD;
+  static constexpr int CPR = D / 8;                 // 16-byte chunks per row
+  static constexpr int LOADS = FBN * CPR / 256;     // chunks per thread per tile
+  i16x8 kst[LOADS], vst[LOADS];
+  __device__ __forceinline__ void load(const T* __restrict__ kp, int64_t skt,
+                                       const T* __restrict__ vp, int64_t svt, int k0, int T_,
+                                       int tid) {
+#pragma unroll
+    for (int u = 0; u < LOADS; ++u) {
+      const int c = tid + 256 * u;
+      const int row = c / CPR, col = (c % CPR) * 8;
+      const int key = k0 + row;
+      if (key < T_) {
+        kst[u] = *reinterpret_cast<const i16x8*>(kp + (int64_t)key * skt + col);
+        vst[u] = *reinterpret_cast<const i16x8*>(vp + (int64_t)key * svt + col);
+      } else {
+        kst[u] = i16x8{0, 0, 0, 0, 0, 0, 0, 0};
+        vst[u] = i16x8{0, 0, 0, 0, 0, 0, 0, 0};
+      }
+    }
+  }
+  __device__ __forceinline__ void store(FwdSmem<D>& sm, int buf, int tid) {
+#pragma unroll
+    for (int u = 0; u < LOADS; ++u) {
+      const int c = tid + 256 * u;
+      const int row = c / CPR, col = (c % CPR) * 8;
+      *reinterpret_cast<i16x8*>(&sm.k[buf][row * LD + col]) = kst[u];
+      *reinterpret_cast<i16x8*>(&sm.v[buf][row * LD + col]) = vst[u];
+    }
+  }
+};
+
+// A-operand fragment of a 16x16x32 MFMA taken transposed from a row-major
+// [row][col] LDS tile: lane (g, li) receives column c0 + li of rows
+// r0 + 4 g + {0..3} (elements 0-3) and r0 + 16 + 4 g + {0..3} (elements 4-7).
+__device__ __forceinline__ i16x8 lds_frag_tr(const short* tile, int ld, int r0, int c0, int g,
+                                             int li) {
+  const short* p0 = tile + (r0 + 4 * g + (li >> 2)) * ld + c0 + 4 * (li & 3);
+  const i16x4 lo = lds_read_tr(p0);
+  const i16x4 hi = lds_read_tr(p0 + 16 * ld);
+  return i16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
 template <typename T, int D>
 __global__ __launch_bounds__(256, 2) void attn_fwd_mfma_k(AttnArgs a) {
   typedef Mfma<T> M;
   constexpr int LD = FwdSmem<D>::LD;
   constexpr int KK = D / 32;   // k-steps of QK^T
   constexpr int DS = D / 16;   // 16-wide d subtiles of O^T
-  constexpr int CPR = D / 8;   // 16-byte chunks per row
-  constexpr int LOADS = FBN * CPR / 256;  // chunks per thread per tile (K or V)
   __shared__ FwdSmem<D> sm;
 
   const int T_ = a.T, H = a.H;
   const int n_qt = (T_ + FBM - 1) / FBM;
-  const int qt = n_qt - 1 - (int)blockIdx.x;  // longest (causal) tiles first
-  const int bh = blockIdx.y, b = bh / H, h = bh - b * H;
+  int bh, rank;
+  block_order((int)blockIdx.x, n_qt, a.B * H, bh, rank);
+  const int qt = n_qt - 1 - rank;  // longest (causal) tiles first
+  const int b = bh / H, h = bh - b * H;
   const int q0 = qt * FBM;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 4, li = lane & 15;
@@ -145,12 +210,10 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_mfma_k(AttnArgs a) {
   for (int qs = 0; qs < 2; ++qs) {
     const int qrow = qw + 16 * qs + li;
 #pragma unroll
-    for (int kk = 0; kk < KK; ++kk) {
-      if (qrow < T_)
-        qf[qs][kk] = *reinterpret_cast<const i16x8*>(qp + (int64_t)qrow * a.sq[2] + 32 * kk + 8 * g);
-      else
-        qf[qs][kk] = i16x8{0, 0, 0, 0, 0, 0, 0, 0};
-    }
+    for (int kk = 0; kk < KK; ++kk)
+      qf[qs][kk] = qrow < T_
+                       ? *reinterpret_cast<const i16x8*>(qp + (int64_t)qrow * a.sq[2] + 32 * kk + 8 * g)
+                       : i16x8{0, 0, 0, 0, 0, 0, 0, 0};
   }
   // ALiBi bias slope * (key - q) split into a per-lane part, fed to QK^T as its
   // C input (divided by scale), and a wave-uniform part added by the FMA that
@@ -167,117 +230,95 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_mfma_k(AttnArgs a) {
     for (int qs = 0; qs < 2; ++qs) oacc[ds][qs] = f32x4{0.f, 0.f, 0.f, 0.f};
   float lsum[2] = {0.f, 0.f};
 
-  const int kend = std::min(q0 + FBM, T_);
-  const int n_kt = (kend + FBN - 1) / FBN;
-
-  // global -> register staging of one K and V tile
-  i16x8 kst[LOADS], vst[LOADS];
-  auto load_tile = [&](int kt) {
-    const int k0 = kt * FBN;
+  // one 64-key tile; MASK: the tile crosses this wave's diagonal
+  auto tile = [&](auto mask_tag, int k0, const short* ks_, const short* vs_) {
+    constexpr bool MASK = decltype(mask_tag)::value;
+    // S^T = K Q^T (+ bias / scale): k-step outer, 8 independent accumulators
+    f32x4 sacc[2][4];
 #pragma unroll
-    for (int u = 0; u < LOADS; ++u) {
-      const int c = tid + 256 * u;
-      const int row = c / CPR, col = (c % CPR) * 8;
-      const int key = k0 + row;
-      if (key < T_) {
-        kst[u] = *reinterpret_cast<const i16x8*>(kp + (int64_t)key * a.sk[2] + col);
-        vst[u] = *reinterpret_cast<const i16x8*>(vp + (int64_t)key * a.sv[2] + col);
-      } else {
-        kst[u] = i16x8{0, 0, 0, 0, 0, 0, 0, 0};
-        vst[u] = i16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int qs = 0; qs < 2; ++qs) sacc[qs][ks] = cb;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      i16x8 kf[4];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) kf[ks] = lds_read16(ks_ + (16 * ks + li) * LD + 32 * kk + 8 * g);
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+        for (int qs = 0; qs < 2; ++qs) sacc[qs][ks] = M::mma(kf[ks], qf[qs][kk], sacc[qs][ks]);
+    }
+    // f' = (1 + s r)^4, r = 1 / (|s| + 1); P^T packed straight from the
+    // accumulator layout into the B operand of O^T += V^T P^T
+    i16x8 pf[2][2];
+#pragma unroll
+    for (int qs = 0; qs < 2; ++qs) {
+      float ls = 0.f;
+      uint32_t pk[4][2];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const float tterm = slope * (float)(k0 - qw + 16 * ks - 16 * qs);
+        float f[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float s = fmaf(sacc[qs][ks][j], scale, tterm);
+          const float r = __builtin_amdgcn_rcpf(fabsf(s) + 1.f);
+          const float t = fmaf(s, r, 1.f);
+          const float t2 = t * t;
+          f[j] = t2 * t2;
+          if (MASK && k0 + 16 * ks + 4 * g + j > qw + 16 * qs + li) f[j] = 0.f;
+        }
+        ls += (f[0] + f[1]) + (f[2] + f[3]);
+        pk[ks][0] = M::pack2(f[0], f[1]);
+        pk[ks][1] = M::pack2(f[2], f[3]);
+      }
+      lsum[qs] += ls;
+#pragma unroll
+      for (int kk2 = 0; kk2 < 2; ++kk2) {
+        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+        u32x4 u = {pk[2 * kk2][0], pk[2 * kk2][1], pk[2 * kk2 + 1][0], pk[2 * kk2 + 1][1]};
+        pf[qs][kk2] = __builtin_bit_cast(i16x8, u);
       }
     }
-  };
-  auto store_tile = [&](int buf) {
+    // O^T += V^T P^T, two d-subtiles at a time (4 independent chains)
 #pragma unroll
-    for (int u = 0; u < LOADS; ++u) {
-      const int c = tid + 256 * u;
-      const int row = c / CPR, col = (c % CPR) * 8;
-      *reinterpret_cast<i16x8*>(&sm.k[buf][row * LD + col]) = kst[u];
-      *reinterpret_cast<i16x8*>(&sm.v[buf][row * LD + col]) = vst[u];
+    for (int ds = 0; ds < DS; ds += 2) {
+      i16x8 vf[2][2];
+#pragma unroll
+      for (int dd = 0; dd < 2; ++dd)
+#pragma unroll
+        for (int kk2 = 0; kk2 < 2; ++kk2) vf[dd][kk2] = lds_frag_tr(vs_, LD, 32 * kk2, 16 * (ds + dd), g, li);
+#pragma unroll
+      for (int kk2 = 0; kk2 < 2; ++kk2)
+#pragma unroll
+        for (int dd = 0; dd < 2; ++dd)
+#pragma unroll
+          for (int qs = 0; qs < 2; ++qs)
+            oacc[ds + dd][qs] = M::mma(vf[dd][kk2], pf[qs][kk2], oacc[ds + dd][qs]);
     }
   };
 
-  load_tile(0);
-  store_tile(0);
+  const int kend = std::min(q0 + FBM, T_);
+  const int n_kt = (kend + FBN - 1) / FBN;
+  KvStager<T, D> stg;
+  stg.load(kp, a.sk[2], vp, a.sv[2], 0, T_, tid);
+  stg.store(sm, 0, tid);
   __syncthreads();
-
   for (int kt = 0; kt < n_kt; ++kt) {
     const int buf = kt & 1;
     const bool more = kt + 1 < n_kt;
-    if (more) load_tile(kt + 1);
+    if (more) stg.load(kp, a.sk[2], vp, a.sv[2], (kt + 1) * FBN, T_, tid);
     const int k0 = kt * FBN;
-    if (k0 <= qw + 31) {  // this wave has unmasked keys in the tile
-      const short* ks_ = sm.k[buf];
-      const short* vs_ = sm.v[buf];
-      // ---- S^T = K Q^T (+ bias / scale)
-      f32x4 sacc[2][4];
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-#pragma unroll
-        for (int qs = 0; qs < 2; ++qs) sacc[qs][ks] = cb;
-#pragma unroll
-        for (int kk = 0; kk < KK; ++kk) {
-          const i16x8 kf = lds_read16(ks_ + (16 * ks + li) * LD + 32 * kk + 8 * g);
-#pragma unroll
-          for (int qs = 0; qs < 2; ++qs) sacc[qs][ks] = M::mma(kf, qf[qs][kk], sacc[qs][ks]);
-        }
-      }
-      // ---- f' = (1 + s r)^4, r = 1 / (|s| + 1); causal mask on diagonal tiles
-      const bool diag = k0 + FBN - 1 > qw;
-      i16x8 pf[2][2];
-#pragma unroll
-      for (int qs = 0; qs < 2; ++qs) {
-        const int qrow = qw + 16 * qs + li;
-        float ls = 0.f;
-        uint32_t pk[4][2];
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          const float tterm = slope * (float)(k0 - qw + 16 * ks - 16 * qs);
-          float f[4];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const float s = fmaf(sacc[qs][ks][j], scale, tterm);
-            const float r = __builtin_amdgcn_rcpf(fabsf(s) + 1.f);
-            const float t = fmaf(s, r, 1.f);
-            const float t2 = t * t;
-            float fv = t2 * t2;
-            if (diag) fv = (k0 + 16 * ks + 4 * g + j > qrow) ? 0.f : fv;
-            f[j] = fv;
-            ls += fv;
-          }
-          pk[ks][0] = M::pack2(f[0], f[1]);
-          pk[ks][1] = M::pack2(f[2], f[3]);
-        }
-        lsum[qs] += ls;
-#pragma unroll
-        for (int kk2 = 0; kk2 < 2; ++kk2) {
-          typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-          u32x4 u = {pk[2 * kk2][0], pk[2 * kk2][1], pk[2 * kk2 + 1][0], pk[2 * kk2 + 1][1]};
-          pf[qs][kk2] = __builtin_bit_cast(i16x8, u);
-        }
-      }
-      // ---- O^T += V^T P^T
-#pragma unroll
-      for (int ds = 0; ds < DS; ++ds) {
-#pragma unroll
-        for (int kk2 = 0; kk2 < 2; ++kk2) {
-          // source lane s = li of group g: row (32 kk2 + 4 g + s / 4) [+16],
-          // column 16 ds + 4 (s % 4)
-          const short* p0 = vs_ + (32 * kk2 + 4 * g + (li >> 2)) * LD + 16 * ds + 4 * (li & 3);
-          const i16x4 lo = lds_read_tr(p0);
-          const i16x4 hi = lds_read_tr(p0 + 16 * LD);
-          const i16x8 vf = i16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-#pragma unroll
-          for (int qs = 0; qs < 2; ++qs) oacc[ds][qs] = M::mma(vf, pf[qs][kk2], oacc[ds][qs]);
-        }
-      }
-    }
-    if (more) store_tile(buf ^ 1);
+    if (k0 + FBN - 1 <= qw)
+      tile(std::false_type{}, k0, sm.k[buf], sm.v[buf]);
+    else if (k0 <= qw + 31)
+      tile(std::true_type{}, k0, sm.k[buf], sm.v[buf]);
+    if (more) stg.store(sm, buf ^ 1, tid);
     __syncthreads();
   }
 
-  // ---- epilogue: L' across the 4 lane groups, normalise, store
+  // epilogue: L' across the 4 lane groups, normalise, store
   T* __restrict__ op = (T*)a.o + b * a.so[0] + h * a.so[1];
   float* __restrict__ Lp = a.L + b * a.sl[0] + h * a.sl[1];
 #pragma unroll
@@ -329,14 +370,14 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_mfma_k(AttnArgs a,
   constexpr int LD = FwdSmem<D>::LD;
   constexpr int KK = D / 32;
   constexpr int DS = D / 16;
-  constexpr int CPR = D / 8;
-  constexpr int LOADS = FBN * CPR / 256;
   __shared__ FwdSmem<D> sm;
 
   const int T_ = a.T, H = a.H;
   const int n_qt = (T_ + FBM - 1) / FBM;
-  const int qt = n_qt - 1 - (int)blockIdx.x;
-  const int bh = blockIdx.y, b = bh / H, h = bh - b * H;
+  int bh, rank;
+  block_order((int)blockIdx.x, n_qt, a.B * H, bh, rank);
+  const int qt = n_qt - 1 - rank;
+  const int b = bh / H, h = bh - b * H;
   const int q0 = qt * FBM;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 4, li = lane & 15;
@@ -376,109 +417,93 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_mfma_k(AttnArgs a,
 #pragma unroll
     for (int qs = 0; qs < 2; ++qs) dqacc[ds][qs] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const int kend = std::min(q0 + FBM, T_);
-  const int n_kt = (kend + FBN - 1) / FBN;
-  i16x8 kst[LOADS], vst[LOADS];
-  auto load_tile = [&](int kt) {
-    const int k0 = kt * FBN;
+  auto tile = [&](auto mask_tag, int k0, const short* ks_, const short* vs_) {
+    constexpr bool MASK = decltype(mask_tag)::value;
+    f32x4 sacc[2][4], pacc[2][4];
 #pragma unroll
-    for (int u = 0; u < LOADS; ++u) {
-      const int c = tid + 256 * u;
-      const int row = c / CPR, col = (c % CPR) * 8;
-      const int key = k0 + row;
-      if (key < T_) {
-        kst[u] = *reinterpret_cast<const i16x8*>(kp + (int64_t)key * a.sk[2] + col);
-        vst[u] = *reinterpret_cast<const i16x8*>(vp + (int64_t)key * a.sv[2] + col);
-      } else {
-        kst[u] = i16x8{0, 0, 0, 0, 0, 0, 0, 0};
-        vst[u] = i16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int qs = 0; qs < 2; ++qs) {
+        sacc[qs][ks] = cb;
+        pacc[qs][ks] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      i16x8 kf[4], vf[4];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        kf[ks] = lds_read16(ks_ + (16 * ks + li) * LD + 32 * kk + 8 * g);
+        vf[ks] = lds_read16(vs_ + (16 * ks + li) * LD + 32 * kk + 8 * g);
+      }
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+        for (int qs = 0; qs < 2; ++qs) {
+          sacc[qs][ks] = M::mma(kf[ks], qf[qs][kk], sacc[qs][ks]);
+          pacc[qs][ks] = M::mma(vf[ks], dof[qs][kk], pacc[qs][ks]);
+        }
+    }
+    i16x8 dsf[2][2];
+#pragma unroll
+    for (int qs = 0; qs < 2; ++qs) {
+      uint32_t pk[4][2];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const float tterm = slope * (float)(k0 - qw + 16 * ks - 16 * qs);
+        float d[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float s = fmaf(sacc[qs][ks][j], scale, tterm);
+          const float r = __builtin_amdgcn_rcpf(fabsf(s) + 1.f);
+          const float t = fmaf(s, r, 1.f);
+          const float u = t * r;
+          d[j] = (u * u * t) * fmaf(pacc[qs][ks][j], c4[qs], nc4d[qs]);
+          if (MASK && k0 + 16 * ks + 4 * g + j > qw + 16 * qs + li) d[j] = 0.f;
+        }
+        pk[ks][0] = pack2_f16(d[0], d[1]);
+        pk[ks][1] = pack2_f16(d[2], d[3]);
+      }
+#pragma unroll
+      for (int kk2 = 0; kk2 < 2; ++kk2) {
+        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+        u32x4 uu = {pk[2 * kk2][0], pk[2 * kk2][1], pk[2 * kk2 + 1][0], pk[2 * kk2 + 1][1]};
+        dsf[qs][kk2] = __builtin_bit_cast(i16x8, uu);
       }
     }
-  };
-  auto store_tile = [&](int buf) {
 #pragma unroll
-    for (int u = 0; u < LOADS; ++u) {
-      const int c = tid + 256 * u;
-      const int row = c / CPR, col = (c % CPR) * 8;
-      *reinterpret_cast<i16x8*>(&sm.k[buf][row * LD + col]) = kst[u];
-      *reinterpret_cast<i16x8*>(&sm.v[buf][row * LD + col]) = vst[u];
+    for (int ds = 0; ds < DS; ds += 2) {
+      i16x8 kt[2][2];
+#pragma unroll
+      for (int dd = 0; dd < 2; ++dd)
+#pragma unroll
+        for (int kk2 = 0; kk2 < 2; ++kk2)
+          kt[dd][kk2] = frag_to_f16<T>(lds_frag_tr(ks_, LD, 32 * kk2, 16 * (ds + dd), g, li));
+#pragma unroll
+      for (int kk2 = 0; kk2 < 2; ++kk2)
+#pragma unroll
+        for (int dd = 0; dd < 2; ++dd)
+#pragma unroll
+          for (int qs = 0; qs < 2; ++qs)
+            dqacc[ds + dd][qs] = mma_f16(kt[dd][kk2], dsf[qs][kk2], dqacc[ds + dd][qs]);
     }
   };
 
-  load_tile(0);
-  store_tile(0);
+  const int kend = std::min(q0 + FBM, T_);
+  const int n_kt = (kend + FBN - 1) / FBN;
+  KvStager<T, D> stg;
+  stg.load(kp, a.sk[2], vp, a.sv[2], 0, T_, tid);
+  stg.store(sm, 0, tid);
   __syncthreads();
   for (int kt = 0; kt < n_kt; ++kt) {
     const int buf = kt & 1;
     const bool more = kt + 1 < n_kt;
-    if (more) load_tile(kt + 1);
+    if (more) stg.load(kp, a.sk[2], vp, a.sv[2], (kt + 1) * FBN, T_, tid);
     const int k0 = kt * FBN;
-    if (k0 <= qw + 31) {
-      const short* ks_ = sm.k[buf];
-      const short* vs_ = sm.v[buf];
-      f32x4 sacc[2][4], pacc[2][4];
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-#pragma unroll
-        for (int qs = 0; qs < 2; ++qs) {
-          sacc[qs][ks] = cb;
-          pacc[qs][ks] = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
-#pragma unroll
-        for (int kk = 0; kk < KK; ++kk) {
-          const i16x8 kf = lds_read16(ks_ + (16 * ks + li) * LD + 32 * kk + 8 * g);
-          const i16x8 vf = lds_read16(vs_ + (16 * ks + li) * LD + 32 * kk + 8 * g);
-#pragma unroll
-          for (int qs = 0; qs < 2; ++qs) {
-            sacc[qs][ks] = M::mma(kf, qf[qs][kk], sacc[qs][ks]);
-            pacc[qs][ks] = M::mma(vf, dof[qs][kk], pacc[qs][ks]);
-          }
-        }
-      }
-      const bool diag = k0 + FBN - 1 > qw;
-      i16x8 dsf[2][2];
-#pragma unroll
-      for (int qs = 0; qs < 2; ++qs) {
-        const int qrow = qw + 16 * qs + li;
-        uint32_t pk[4][2];
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          const float tterm = slope * (float)(k0 - qw + 16 * ks - 16 * qs);
-          float d[4];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const float s = fmaf(sacc[qs][ks][j], scale, tterm);
-            const float r = __builtin_amdgcn_rcpf(fabsf(s) + 1.f);
-            const float t = fmaf(s, r, 1.f);
-            const float u = t * r;
-            float dsv = (u * u * t) * fmaf(pacc[qs][ks][j], c4[qs], nc4d[qs]);
-            if (diag) dsv = (k0 + 16 * ks + 4 * g + j > qrow) ? 0.f : dsv;
-            d[j] = dsv;
-          }
-          pk[ks][0] = pack2_f16(d[0], d[1]);
-          pk[ks][1] = pack2_f16(d[2], d[3]);
-        }
-#pragma unroll
-        for (int kk2 = 0; kk2 < 2; ++kk2) {
-          typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-          u32x4 uu = {pk[2 * kk2][0], pk[2 * kk2][1], pk[2 * kk2 + 1][0], pk[2 * kk2 + 1][1]};
-          dsf[qs][kk2] = __builtin_bit_cast(i16x8, uu);
-        }
-      }
-#pragma unroll
-      for (int ds = 0; ds < DS; ++ds) {
-#pragma unroll
-        for (int kk2 = 0; kk2 < 2; ++kk2) {
-          const short* p0 = ks_ + (32 * kk2 + 4 * g + (li >> 2)) * LD + 16 * ds + 4 * (li & 3);
-          const i16x4 lo = lds_read_tr(p0);
-          const i16x4 hi = lds_read_tr(p0 + 16 * LD);
-          const i16x8 kf = frag_to_f16<T>(i16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
-#pragma unroll
-          for (int qs = 0; qs < 2; ++qs) dqacc[ds][qs] = mma_f16(kf, dsf[qs][kk2], dqacc[ds][qs]);
-        }
-      }
-    }
-    if (more) store_tile(buf ^ 1);
+    if (k0 + FBN - 1 <= qw)
+      tile(std::false_type{}, k0, sm.k[buf], sm.v[buf]);
+    else if (k0 <= qw + 31)
+      tile(std::true_type{}, k0, sm.k[buf], sm.v[buf]);
+    if (more) stg.store(sm, buf ^ 1, tid);
     __syncthreads();
   }
 
@@ -529,8 +554,11 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_mfma_k(AttnArgs a,
   __shared__ DkvSmem<D> sm;
 
   const int T_ = a.T, H = a.H;
-  const int bh = blockIdx.y, b = bh / H, h = bh - b * H;
-  const int k0 = (int)blockIdx.x * KBN;  // block 0 has the most query tiles: first
+  const int n_kb = (T_ + KBN - 1) / KBN;
+  int bh, kb;
+  block_order((int)blockIdx.x, n_kb, a.B * H, bh, kb);  // kb 0 has the most query tiles
+  const int b = bh / H, h = bh - b * H;
+  const int k0 = kb * KBN;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 4, li = lane & 15;
   const int kw = k0 + 32 * w;
@@ -573,6 +601,86 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_mfma_k(AttnArgs a,
       dkacc[ds][ks] = f32x4{0.f, 0.f, 0.f, 0.f};
       dvacc[ds][ks] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
+
+  // one 32-query half (queries qh .. qh + 31) of the LDS tile; MASK: some
+  // pair of the half has key > q
+  auto half = [&](auto mask_tag, int qh, int r0, const short* qs_, const short* os_,
+                  const float* c4s, const float* nds) {
+    constexpr bool MASK = decltype(mask_tag)::value;
+    f32x4 sacc[2][2], pacc[2][2];
+#pragma unroll
+    for (int qs = 0; qs < 2; ++qs)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        sacc[qs][ks] = cb;
+        pacc[qs][ks] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      i16x8 qa[2], oa[2];
+#pragma unroll
+      for (int qs = 0; qs < 2; ++qs) {
+        const int row = r0 + 16 * qs + li;
+        qa[qs] = lds_read16(qs_ + row * LD + 32 * kk + 8 * g);
+        oa[qs] = lds_read16(os_ + row * LD + 32 * kk + 8 * g);
+      }
+#pragma unroll
+      for (int qs = 0; qs < 2; ++qs)
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          sacc[qs][ks] = M::mma(qa[qs], kf[ks][kk], sacc[qs][ks]);
+          pacc[qs][ks] = M::mma(oa[qs], vf[ks][kk], pacc[qs][ks]);
+        }
+    }
+    uint32_t ppk[2][2][2], dpk[2][2][2];  // [ks][qs][pair]
+#pragma unroll
+    for (int qs = 0; qs < 2; ++qs) {
+      const f32x4 c4v = *reinterpret_cast<const f32x4*>(c4s + r0 + 16 * qs + 4 * g);
+      const f32x4 ndv = *reinterpret_cast<const f32x4*>(nds + r0 + 16 * qs + 4 * g);
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const float tterm = slope * (float)(kw + 16 * ks - qh - 16 * qs);
+        float pv[4], dv[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float s = fmaf(sacc[qs][ks][j], scale, tterm);
+          const float r = __builtin_amdgcn_rcpf(fabsf(s) + 1.f);
+          const float t = fmaf(s, r, 1.f);
+          const float t2 = t * t;
+          const float u = t * r;
+          pv[j] = (t2 * t2) * (0.25f * c4v[j]);
+          dv[j] = (u * u * t) * fmaf(pacc[qs][ks][j], c4v[j], ndv[j]);
+          if (MASK && kw + 16 * ks + li > qh + 16 * qs + 4 * g + j) {
+            pv[j] = 0.f;
+            dv[j] = 0.f;
+          }
+        }
+        ppk[ks][qs][0] = M::pack2(pv[0], pv[1]);
+        ppk[ks][qs][1] = M::pack2(pv[2], pv[3]);
+        dpk[ks][qs][0] = pack2_f16(dv[0], dv[1]);
+        dpk[ks][qs][1] = pack2_f16(dv[2], dv[3]);
+      }
+    }
+    i16x8 pf[2], dsf[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+      u32x4 u1 = {ppk[ks][0][0], ppk[ks][0][1], ppk[ks][1][0], ppk[ks][1][1]};
+      u32x4 u2 = {dpk[ks][0][0], dpk[ks][0][1], dpk[ks][1][0], dpk[ks][1][1]};
+      pf[ks] = __builtin_bit_cast(i16x8, u1);
+      dsf[ks] = __builtin_bit_cast(i16x8, u2);
+    }
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds) {
+      const i16x8 ot = lds_frag_tr(os_, LD, r0, 16 * ds, g, li);
+      const i16x8 qtr = frag_to_f16<T>(lds_frag_tr(qs_, LD, r0, 16 * ds, g, li));
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        dvacc[ds][ks] = M::mma(ot, pf[ks], dvacc[ds][ks]);
+        dkacc[ds][ks] = mma_f16(qtr, dsf[ks], dkacc[ds][ks]);
+      }
+    }
+  };
 
   const int qstart = k0;  // causal: queries >= first key of the block
   const int n_qt = qstart < T_ ? (T_ - qstart + KBQ - 1) / KBQ : 0;
@@ -626,89 +734,20 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_mfma_k(AttnArgs a,
     const int q0 = qstart + it * KBQ;
     const short* qs_ = sm.q[buf];
     const short* os_ = sm.o[buf];
+    const float* c4s = sm.c4[buf];
+    const float* nds = sm.nc4d[buf];
+    if (q0 >= kw + 31) {  // every pair of the tile has key <= q
+      half(std::false_type{}, q0, 0, qs_, os_, c4s, nds);
+      half(std::false_type{}, q0 + 32, 32, qs_, os_, c4s, nds);
+    } else {
 #pragma unroll
-    for (int h2 = 0; h2 < 2; ++h2) {
-      const int qh = q0 + 32 * h2;
-      if (qh + 31 < kw) continue;  // every pair in this half has key > q
-      f32x4 sacc[2][2], pacc[2][2];
-#pragma unroll
-      for (int qs = 0; qs < 2; ++qs)
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          sacc[qs][ks] = cb;
-          pacc[qs][ks] = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
-#pragma unroll
-      for (int kk = 0; kk < KK; ++kk) {
-#pragma unroll
-        for (int qs = 0; qs < 2; ++qs) {
-          const int row = 32 * h2 + 16 * qs + li;
-          const i16x8 qa = lds_read16(qs_ + row * LD + 32 * kk + 8 * g);
-          const i16x8 oa = lds_read16(os_ + row * LD + 32 * kk + 8 * g);
-#pragma unroll
-          for (int ks = 0; ks < 2; ++ks) {
-            sacc[qs][ks] = M::mma(qa, kf[ks][kk], sacc[qs][ks]);
-            pacc[qs][ks] = M::mma(oa, vf[ks][kk], pacc[qs][ks]);
-          }
-        }
-      }
-      const bool diag = qh < kw + 31;
-      uint32_t ppk[2][2][2], dpk[2][2][2];  // [ks][qs][pair]
-#pragma unroll
-      for (int qs = 0; qs < 2; ++qs) {
-        const f32x4 c4v = *reinterpret_cast<const f32x4*>(&sm.c4[buf][32 * h2 + 16 * qs + 4 * g]);
-        const f32x4 ndv = *reinterpret_cast<const f32x4*>(&sm.nc4d[buf][32 * h2 + 16 * qs + 4 * g]);
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          const float tterm = slope * (float)(kw + 16 * ks - qh - 16 * qs);
-          const int key = kw + 16 * ks + li;
-          float pv[4], dv[4];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const float s = fmaf(sacc[qs][ks][j], scale, tterm);
-            const float r = __builtin_amdgcn_rcpf(fabsf(s) + 1.f);
-            const float t = fmaf(s, r, 1.f);
-            const float t2 = t * t;
-            const float u = t * r;
-            float p = (t2 * t2) * (0.25f * c4v[j]);
-            float dsv = (u * u * t) * fmaf(pacc[qs][ks][j], c4v[j], ndv[j]);
-            if (diag && key > qh + 16 * qs + 4 * g + j) {
-              p = 0.f;
-              dsv = 0.f;
-            }
-            pv[j] = p;
-            dv[j] = dsv;
-          }
-          ppk[ks][qs][0] = M::pack2(pv[0], pv[1]);
-          ppk[ks][qs][1] = M::pack2(pv[2], pv[3]);
-          dpk[ks][qs][0] = pack2_f16(dv[0], dv[1]);
-          dpk[ks][qs][1] = pack2_f16(dv[2], dv[3]);
-        }
-      }
-      i16x8 pf[2], dsf[2];
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-        u32x4 u1 = {ppk[ks][0][0], ppk[ks][0][1], ppk[ks][1][0], ppk[ks][1][1]};
-        u32x4 u2 = {dpk[ks][0][0], dpk[ks][0][1], dpk[ks][1][0], dpk[ks][1][1]};
-        pf[ks] = __builtin_bit_cast(i16x8, u1);
-        dsf[ks] = __builtin_bit_cast(i16x8, u2);
-      }
-#pragma unroll
-      for (int ds = 0; ds < DS; ++ds) {
-        const int off = (32 * h2 + 4 * g + (li >> 2)) * LD + 16 * ds + 4 * (li & 3);
-        const i16x4 olo = lds_read_tr(os_ + off);
-        const i16x4 ohi = lds_read_tr(os_ + off + 16 * LD);
-        const i16x4 qlo = lds_read_tr(qs_ + off);
-        const i16x4 qhi = lds_read_tr(qs_ + off + 16 * LD);
-        const i16x8 ot = i16x8{olo[0], olo[1], olo[2], olo[3], ohi[0], ohi[1], ohi[2], ohi[3]};
-        const i16x8 qtr =
-            frag_to_f16<T>(i16x8{qlo[0], qlo[1], qlo[2], qlo[3], qhi[0], qhi[1], qhi[2], qhi[3]});
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          dvacc[ds][ks] = M::mma(ot, pf[ks], dvacc[ds][ks]);
-          dkacc[ds][ks] = mma_f16(qtr, dsf[ks], dkacc[ds][ks]);
-        }
+      for (int h2 = 0; h2 < 2; ++h2) {
+        const int qh = q0 + 32 * h2;
+        if (qh + 31 < kw) continue;  // every pair of the half has key > q
+        if (qh >= kw + 31)
+          half(std::false_type{}, qh, 32 * h2, qs_, os_, c4s, nds);
+        else
+          half(std::true_type{}, qh, 32 * h2, qs_, os_, c4s, nds);
       }
     }
     if (more) store_tile(buf ^ 1);
@@ -740,8 +779,9 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_mfma_k(AttnArgs a,
 bool attn_mfma_supported(int D) { return D == 64 || D == 128; }
 
 template <typename T> int attn_fwd_mfma(const AttnArgs& a, hipStream_t st) {
-  dim3 grid((a.T + FBM - 1) / FBM, a.B * a.H);
-  if (grid.y > 65535u) return KAT_EUNSUPPORTED;
+  const int64_t nb = (int64_t)((a.T + FBM - 1) / FBM) * a.B * a.H;
+  if (nb > 0x7fffffffLL) return KAT_EUNSUPPORTED;
+  dim3 grid((unsigned)nb);
   if (a.D == 128)
     hipLaunchKernelGGL((attn_fwd_mfma_k<T, 128>), grid, dim3(256), 0, st, a);
   else if (a.D == 64)
@@ -753,9 +793,10 @@ template <typename T> int attn_fwd_mfma(const AttnArgs& a, hipStream_t st) {
 
 template <typename T>
 int attn_bwd_mfma(const AttnArgs& a, const float* delta, const float* cinv, hipStream_t st) {
-  if ((unsigned)(a.B * a.H) > 65535u) return KAT_EUNSUPPORTED;
-  dim3 gk((a.T + KBN - 1) / KBN, a.B * a.H);
-  dim3 gq((a.T + FBM - 1) / FBM, a.B * a.H);
+  const int64_t nk = (int64_t)((a.T + KBN - 1) / KBN) * a.B * a.H;
+  const int64_t nq = (int64_t)((a.T + FBM - 1) / FBM) * a.B * a.H;
+  if (nk > 0x7fffffffLL || nq > 0x7fffffffLL) return KAT_EUNSUPPORTED;
+  dim3 gk((unsigned)nk), gq((unsigned)nq);
   if (a.D == 128) {
     hipLaunchKernelGGL((attn_bwd_dkv_mfma_k<T, 128>), gk, dim3(256), 0, st, a, delta, cinv);
     if (int rc = check_launch("kat_attn_bwd (dkv, mfma)")) return rc;
