@@ -35,13 +35,19 @@ template <typename T> struct Raw {
   typedef VecT<T, V> type;
 };
 
+// Streaming 16-byte accesses. Every tensor is touched once per kernel, so the
+// loads and stores are non-temporal (they do not displace reusable lines in
+// L2 / MALL); on the MI355X this lifts a plain copy from ~5.5 to ~6.4 TB/s.
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 template <typename T, int V>
 __device__ __forceinline__ VecT<T, V> ld_vec(const T* __restrict__ p) {
-  return *reinterpret_cast<const VecT<T, V>*>(p);
+  static_assert(sizeof(VecT<T, V>) == 16, "16-byte vectors");
+  const u32x4_t r = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+  return __builtin_bit_cast(VecT<T, V>, r);
 }
 template <typename T, int V>
 __device__ __forceinline__ void st_vec(T* __restrict__ p, const VecT<T, V>& v) {
-  *reinterpret_cast<VecT<T, V>*>(p) = v;
+  __builtin_nontemporal_store(__builtin_bit_cast(u32x4_t, v), reinterpret_cast<u32x4_t*>(p));
 }
 template <typename T, int V> __device__ __forceinline__ VecT<T, V> zero_vec() {
   VecT<T, V> z;
@@ -189,46 +195,112 @@ __global__ __launch_bounds__(kEwThreads) void swiglu_bwd_scalar_k(
 // rational softmax -- fused_ops.py:52-189
 // ============================================================================
 
+// Row-resident kernels: a 256-thread block owns one row at a time and each
+// thread a fixed column slice (16-byte chunks tid, tid + 256, ...), so per-row
+// reductions are one wave reduction plus a 4-entry LDS exchange. Blocks are
+// persistent over rows (row = blockIdx.x + i * gridDim.x) and keep the next
+// two rows' loads in flight while the current one is reduced and written,
+// which keeps HBM busy without relying on occupancy alone.
+
+// Block-wide sum for 256 threads; `par` alternates per row so consecutive rows
+// use different LDS slots and one barrier per row suffices.
+template <typename A> __device__ __forceinline__ A block_sum_par(A v, A (*red)[kRowWaves], int par) {
+  v = wave_sum(v);
+  if ((threadIdx.x & 63) == 0) red[par][threadIdx.x >> 6] = v;
+  __syncthreads();
+  return (red[par][0] + red[par][1]) + (red[par][2] + red[par][3]);
+}
+
+// Loads this thread's chunks of one row. Chunks past the row end re-read the
+// row's first chunk (always in bounds) and are masked where they are used:
+// a conditional load here would compile to a branch that waits for the data
+// on the spot, serialising the prefetch.
+template <typename T, int NCH>
+__device__ __forceinline__ void load_row(const T* __restrict__ base, int n_cols, VecT<T, Raw<T>::V> (&r)[NCH]) {
+  constexpr int V = Raw<T>::V;
+#pragma unroll
+  for (int k = 0; k < NCH; ++k) {
+    const int col = ((int)threadIdx.x + 256 * k) * V;
+    r[k] = ld_vec<T, V>(base + (col < n_cols ? col : 0));
+  }
+}
+__device__ __forceinline__ bool chunk_in(int k, int V, int n_cols) {
+  return ((int)threadIdx.x + 256 * k) * V < n_cols;
+}
+
+// The weight values of this thread's chunks, with 16-byte loads (the caller
+// checks 16-byte alignment of w); out-of-row chunks read chunk 0.
+template <typename T, typename W, int NCH>
+__device__ __forceinline__ void load_weight(const W* __restrict__ w, int n_cols,
+                                            typename AccT<T>::type (&wv)[NCH][Raw<T>::V]) {
+  constexpr int V = Raw<T>::V;
+  constexpr int PER = 16 / (int)sizeof(W);  // weights per 16-byte load
+#pragma unroll
+  for (int k = 0; k < NCH; ++k) {
+    const int col = ((int)threadIdx.x + 256 * k) * V;
+    const W* base = w + (col < n_cols ? col : 0);
+    if constexpr (V % PER == 0) {
+#pragma unroll
+      for (int j = 0; j < V / PER; ++j) {
+        const VecT<W, PER> r = *reinterpret_cast<const VecT<W, PER>*>(base + j * PER);
+#pragma unroll
+        for (int e = 0; e < PER; ++e) wv[k][j * PER + e] = (typename AccT<T>::type)r.v[e];
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < V; ++e) wv[k][e] = (typename AccT<T>::type)base[e];
+    }
+  }
+}
+
 template <typename T, int NCH>
 __global__ __launch_bounds__(256) void rsoftmax_fwd_k(const T* __restrict__ x, T* __restrict__ p,
                                                       int64_t n_rows, int n_cols, int64_t ldx,
                                                       int64_t ldp, float eps) {
   typedef typename AccT<T>::type A;
   constexpr int V = Raw<T>::V;
-  const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * kRowWaves + (threadIdx.x >> 6);
-  if (row >= n_rows) return;
-  const T* xr = x + row * ldx;
-  VecT<T, V> raw[NCH];
+  __shared__ A red[2][kRowWaves];
+  const int64_t G = gridDim.x;
+  int64_t row = blockIdx.x;
+  // rows `row`, `row + G` in flight; rows past the end clamp to the last row
+  // (loaded, never used) so no load sits behind a branch
+  const int64_t last = n_rows - 1;
+  VecT<T, V> cur[NCH], nx1[NCH];
+  load_row<T, NCH>(x + std::min(row, last) * ldx, n_cols, cur);
+  load_row<T, NCH>(x + std::min(row + G, last) * ldx, n_cols, nx1);
+  for (int par = 0; row < n_rows; row += G, par ^= 1) {
+    VecT<T, V> nx2[NCH];
+    load_row<T, NCH>(x + std::min(row + 2 * G, last) * ldx, n_cols, nx2);
+    A f[NCH][V];
+    A sum = A(0);
 #pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    const int col = (c * 64 + lane) * V;
-    raw[c] = col < n_cols ? ld_vec<T, V>(xr + col) : zero_vec<T, V>();
-  }
-  A f[NCH][V];
-  A sum = A(0);
+    for (int k = 0; k < NCH; ++k) {
+      const bool in = ((int)threadIdx.x + 256 * k) * V < n_cols;
 #pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    const bool in = (c * 64 + lane) * V < n_cols;
-#pragma unroll
-    for (int i = 0; i < V; ++i) {
-      const A s = rsig(to_acc(raw[c].v[i]));  // fused_ops.py:81-86
-      const A s2 = s * s;
-      f[c][i] = s2 * s2;
-      sum += in ? f[c][i] : A(0);
+      for (int i = 0; i < V; ++i) {
+        const A sg = rsig(to_acc(cur[k].v[i]));  // fused_ops.py:81-86
+        const A s2 = sg * sg;
+        f[k][i] = s2 * s2;
+        sum += in ? f[k][i] : A(0);
+      }
     }
-  }
-  sum = wave_sum(sum);
-  const A inv = A(1) / (sum + A(eps));  // fused_ops.py:90
-  T* pr = p + row * ldp;
+    sum = block_sum_par(sum, red, par);
+    const A inv = A(1) / (sum + A(eps));  // fused_ops.py:90
+    T* pr = p + row * ldp;
 #pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    const int col = (c * 64 + lane) * V;
-    if (col < n_cols) {
-      VecT<T, V> o;
+    for (int k = 0; k < NCH; ++k) {
+      const int col = ((int)threadIdx.x + 256 * k) * V;
+      if (col < n_cols) {
+        VecT<T, V> o;
 #pragma unroll
-      for (int i = 0; i < V; ++i) o.v[i] = from_acc<T>(f[c][i] * inv);  // fused_ops.py:104
-      st_vec<T, V>(pr + col, o);
+        for (int i = 0; i < V; ++i) o.v[i] = from_acc<T>(f[k][i] * inv);  // fused_ops.py:104
+        st_vec<T, V>(pr + col, o);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < NCH; ++k) {
+      cur[k] = nx1[k];
+      nx1[k] = nx2[k];
     }
   }
 }
@@ -242,39 +314,61 @@ __global__ __launch_bounds__(256) void rsoftmax_bwd_k(const T* __restrict__ dy,
                                                       float eps) {
   typedef typename AccT<T>::type A;
   constexpr int V = Raw<T>::V;
-  const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * kRowWaves + (threadIdx.x >> 6);
-  if (row >= n_rows) return;
-  VecT<T, V> ry[NCH], rp[NCH], rx[NCH];
-#pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    const int col = (c * 64 + lane) * V;
-    const bool in = col < n_cols;
-    ry[c] = in ? ld_vec<T, V>(dy + row * lddy + col) : zero_vec<T, V>();
-    rp[c] = in ? ld_vec<T, V>(p + row * ldp + col) : zero_vec<T, V>();
-    rx[c] = in ? ld_vec<T, V>(x + row * ldx + col) : zero_vec<T, V>();
+  __shared__ A red[2][kRowWaves];
+  const int64_t G = gridDim.x;
+  int64_t row = blockIdx.x;
+  const int64_t last = n_rows - 1;
+  VecT<T, V> cy[NCH], cp[NCH], cx[NCH], y1[NCH], p1[NCH], x1[NCH];
+  {
+    const int64_t r0 = std::min(row, last), r1 = std::min(row + G, last);
+    load_row<T, NCH>(dy + r0 * lddy, n_cols, cy);
+    load_row<T, NCH>(p + r0 * ldp, n_cols, cp);
+    load_row<T, NCH>(x + r0 * ldx, n_cols, cx);
+    load_row<T, NCH>(dy + r1 * lddy, n_cols, y1);
+    load_row<T, NCH>(p + r1 * ldp, n_cols, p1);
+    load_row<T, NCH>(x + r1 * ldx, n_cols, x1);
   }
-  A dot = A(0);
-#pragma unroll
-  for (int c = 0; c < NCH; ++c)
-#pragma unroll
-    for (int i = 0; i < V; ++i) dot += to_acc(ry[c].v[i]) * to_acc(rp[c].v[i]);  // :167
-  dot = wave_sum(dot);
   const A e = A(eps);
+  for (int par = 0; row < n_rows; row += G, par ^= 1) {
+    VecT<T, V> ny[NCH], np[NCH], nx[NCH];
+    {
+      const int64_t r2 = std::min(row + 2 * G, last);
+      load_row<T, NCH>(dy + r2 * lddy, n_cols, ny);
+      load_row<T, NCH>(p + r2 * ldp, n_cols, np);
+      load_row<T, NCH>(x + r2 * ldx, n_cols, nx);
+    }
+    A dot = A(0);
 #pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    const int col = (c * 64 + lane) * V;
-    if (col < n_cols) {
-      VecT<T, V> o;
+    for (int k = 0; k < NCH; ++k) {
+      const bool in = chunk_in(k, V, n_cols);
 #pragma unroll
-      for (int i = 0; i < V; ++i) {
-        const A xx = to_acc(rx[c].v[i]);
-        const A den = fabs(xx) + A(1);  // fused_ops.py:179-187
-        const A sig = A(0.5) * (xx / den + A(1));
-        const A g = A(2) / (den * den * (sig + e));
-        o.v[i] = from_acc<T>(to_acc(rp[c].v[i]) * g * (to_acc(ry[c].v[i]) - dot));
+      for (int i = 0; i < V; ++i) dot += in ? to_acc(cy[k].v[i]) * to_acc(cp[k].v[i]) : A(0);  // :167
+    }
+    dot = block_sum_par(dot, red, par);
+#pragma unroll
+    for (int k = 0; k < NCH; ++k) {
+      const int col = ((int)threadIdx.x + 256 * k) * V;
+      if (col < n_cols) {
+        VecT<T, V> o;
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+          const A xx = to_acc(cx[k].v[i]);
+          const A den = fabs(xx) + A(1);  // fused_ops.py:179-187
+          const A sig = A(0.5) * (xx / den + A(1));
+          const A g = A(2) / (den * den * (sig + e));
+          o.v[i] = from_acc<T>(to_acc(cp[k].v[i]) * g * (to_acc(cy[k].v[i]) - dot));
+        }
+        st_vec<T, V>(dx + row * lddx + col, o);
       }
-      st_vec<T, V>(dx + row * lddx + col, o);
+    }
+#pragma unroll
+    for (int k = 0; k < NCH; ++k) {
+      cy[k] = y1[k];
+      cp[k] = p1[k];
+      cx[k] = x1[k];
+      y1[k] = ny[k];
+      p1[k] = np[k];
+      x1[k] = nx[k];
     }
   }
 }
@@ -340,40 +434,52 @@ __global__ __launch_bounds__(256) void men_fwd_k(const T* __restrict__ x, const 
                                                  int64_t ldy, float eps) {
   typedef typename AccT<T>::type A;
   constexpr int V = Raw<T>::V;
-  const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * kRowWaves + (threadIdx.x >> 6);
-  if (row >= n_rows) return;
-  VecT<T, V> rx[NCH];
+  __shared__ A red[2][kRowWaves];
+  A wv[NCH][V];
+  load_weight<T, W, NCH>(w, n_cols, wv);
+  const int64_t G = gridDim.x;
+  int64_t row = blockIdx.x;
+  const int64_t last = n_rows - 1;
+  VecT<T, V> cur[NCH], nx1[NCH];
+  load_row<T, NCH>(x + std::min(row, last) * ldx, n_cols, cur);
+  load_row<T, NCH>(x + std::min(row + G, last) * ldx, n_cols, nx1);
+  for (int par = 0; row < n_rows; row += G, par ^= 1) {
+    VecT<T, V> nx2[NCH];
+    load_row<T, NCH>(x + std::min(row + 2 * G, last) * ldx, n_cols, nx2);
+    A s = A(0);
 #pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    const int col = (c * 64 + lane) * V;
-    rx[c] = col < n_cols ? ld_vec<T, V>(x + row * ldx + col) : zero_vec<T, V>();
-  }
-  A s = A(0);
+    for (int k = 0; k < NCH; ++k) {
+      const bool in = chunk_in(k, V, n_cols);
 #pragma unroll
-  for (int c = 0; c < NCH; ++c)
+      for (int i = 0; i < V; ++i) s += in ? fabs(to_acc(cur[k].v[i])) : A(0);  // fused_ops.py:324
+    }
+    s = block_sum_par(s, red, par);
+    const A mean = s / A(n_cols);          // fused_ops.py:326
+    const A inv = A(1) / (mean + A(eps));  // fused_ops.py:327
+    if (threadIdx.x == 0) mu[row] = (float)mean;  // fused_ops.py:330 (no eps)
 #pragma unroll
-    for (int i = 0; i < V; ++i) s += fabs(to_acc(rx[c].v[i]));  // fused_ops.py:324
-  s = wave_sum(s);
-  const A mean = s / A(n_cols);                  // fused_ops.py:326
-  const A inv = A(1) / (mean + A(eps));          // fused_ops.py:327
-  if (lane == 0) mu[row] = (float)mean;          // fused_ops.py:330 (no eps)
+    for (int k = 0; k < NCH; ++k) {
+      const int col = ((int)threadIdx.x + 256 * k) * V;
+      if (col < n_cols) {
+        VecT<T, V> o;
 #pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    const int col = (c * 64 + lane) * V;
-    if (col < n_cols) {
-      VecT<T, V> o;
+        for (int i = 0; i < V; ++i) o.v[i] = from_acc<T>(to_acc(cur[k].v[i]) * inv * wv[k][i]);  // :340
+        st_vec<T, V>(y + row * ldy + col, o);
+      }
+    }
 #pragma unroll
-      for (int i = 0; i < V; ++i)
-        o.v[i] = from_acc<T>(to_acc(rx[c].v[i]) * inv * (A)w[col + i]);  // :340
-      st_vec<T, V>(y + row * ldy + col, o);
+    for (int k = 0; k < NCH; ++k) {
+      cur[k] = nx1[k];
+      nx1[k] = nx2[k];
     }
   }
 }
 
-// Persistent over rows: each wave takes rows wave_id, wave_id + waves_total,
-// ...; per-lane dgamma partials live in registers and are combined per block
-// through LDS into partial[blockIdx.x][n_cols].
+// Each thread owns fixed columns, so its dgamma partial over the block's rows
+// needs no cross-thread reduction: it goes straight to partial[block][col].
+// Each block keeps kNormPf rows in flight ahead of the one it is reducing.
+constexpr int kNormPf = 2;
+
 template <typename T, typename W, int NCH>
 __global__ __launch_bounds__(256) void men_bwd_k(
     const T* __restrict__ dy, const T* __restrict__ x, const W* __restrict__ w,
@@ -381,69 +487,78 @@ __global__ __launch_bounds__(256) void men_bwd_k(
     int64_t n_rows, int n_cols, int64_t lddy, int64_t ldx, int64_t lddx, float eps) {
   typedef typename AccT<T>::type A;
   constexpr int V = Raw<T>::V;
-  __shared__ A red[kRowWaves][64 * V];
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  constexpr int PF = kNormPf;
+  __shared__ A red[2][kRowWaves];
   A wv[NCH][V], dg[NCH][V];
+  load_weight<T, W, NCH>(w, n_cols, wv);
 #pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    const int col = (c * 64 + lane) * V;
+  for (int k = 0; k < NCH; ++k)
 #pragma unroll
-    for (int i = 0; i < V; ++i) {
-      wv[c][i] = col < n_cols ? (A)w[col + i] : A(0);
-      dg[c][i] = A(0);
-    }
-  }
+    for (int i = 0; i < V; ++i) dg[k][i] = A(0);
   const A e = A(eps);
-  for (int64_t row = (int64_t)blockIdx.x * kRowWaves + wave; row < n_rows;
-       row += (int64_t)gridDim.x * kRowWaves) {
-    VecT<T, V> ry[NCH], rx[NCH];
+  const int64_t G = gridDim.x;
+  int64_t row = blockIdx.x;
+  // ring of rows row, row + G, ..., row + PF*G: slot 0 is reduced next
+  VecT<T, V> by[PF + 1][NCH], bx[PF + 1][NCH];
+  float bm[PF + 1];
+  // Rows past the end are clamped to the last row (loaded, never used):
+  // a conditional load would make the compiler wait for it on the spot.
+  const int64_t last = n_rows - 1;
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-      const int col = (c * 64 + lane) * V;
-      const bool in = col < n_cols;
-      ry[c] = in ? ld_vec<T, V>(dy + row * lddy + col) : zero_vec<T, V>();
-      rx[c] = in ? ld_vec<T, V>(x + row * ldx + col) : zero_vec<T, V>();
+  for (int j = 0; j < PF; ++j) {
+    const int64_t r = std::min(row + j * G, last);
+    load_row<T, NCH>(dy + r * lddy, n_cols, by[j]);
+    load_row<T, NCH>(x + r * ldx, n_cols, bx[j]);
+    bm[j] = mu[r];  // the row statistic travels with its row
+  }
+  for (int par = 0; row < n_rows; row += G, par ^= 1) {
+    {
+      const int64_t r = std::min(row + PF * G, last);
+      load_row<T, NCH>(dy + r * lddy, n_cols, by[PF]);
+      load_row<T, NCH>(x + r * ldx, n_cols, bx[PF]);
+      bm[PF] = mu[r];
     }
-    const A inv = A(1) / ((A)mu[row] + e);  // fused_ops.py:389-390
+    const A inv = A(1) / ((A)bm[0] + e);  // fused_ops.py:389-390
     A cs = A(0);
 #pragma unroll
-    for (int c = 0; c < NCH; ++c)
+    for (int k = 0; k < NCH; ++k) {
+      const bool in = chunk_in(k, V, n_cols);
 #pragma unroll
       for (int i = 0; i < V; ++i)
-        cs += to_acc(ry[c].v[i]) * (to_acc(rx[c].v[i]) * inv * wv[c][i]);  // :404-405
-    cs = wave_sum(cs);
+        cs += in ? to_acc(by[0][k].v[i]) * (to_acc(bx[0][k].v[i]) * inv * wv[k][i]) : A(0);  // :404-405
+    }
+    cs = block_sum_par(cs, red, par);
     const A corr = cs / A(n_cols);  // fused_ops.py:408
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-      const int col = (c * 64 + lane) * V;
+    for (int k = 0; k < NCH; ++k) {
+      const int col = ((int)threadIdx.x + 256 * k) * V;
+      const bool in = col < n_cols;
       VecT<T, V> o;
 #pragma unroll
       for (int i = 0; i < V; ++i) {
-        const A yy = to_acc(ry[c].v[i]);
-        const A xx = to_acc(rx[c].v[i]);
-        o.v[i] = from_acc<T>(yy * wv[c][i] * inv - sign_of(xx) * corr * inv);  // :418-421
-        dg[c][i] += yy * (xx * inv);  // fused_ops.py:595-597
+        const A yy = to_acc(by[0][k].v[i]);
+        const A xx = to_acc(bx[0][k].v[i]);
+        o.v[i] = from_acc<T>(yy * wv[k][i] * inv - sign_of(xx) * corr * inv);  // :418-421
+        dg[k][i] += in ? yy * (xx * inv) : A(0);  // fused_ops.py:595-597
       }
-      if (col < n_cols) st_vec<T, V>(dx + row * lddx + col, o);
+      if (in) st_vec<T, V>(dx + row * lddx + col, o);
+    }
+#pragma unroll
+    for (int j = 0; j < PF; ++j) {
+      bm[j] = bm[j + 1];
+#pragma unroll
+      for (int k = 0; k < NCH; ++k) {
+        by[j][k] = by[j + 1][k];
+        bx[j][k] = bx[j + 1][k];
+      }
     }
   }
-  // Combine the 4 waves' partials chunk by chunk (fixed order).
 #pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    __syncthreads();
+  for (int k = 0; k < NCH; ++k) {
+    const int col = ((int)threadIdx.x + 256 * k) * V;
 #pragma unroll
-    for (int i = 0; i < V; ++i) red[wave][lane * V + i] = dg[c][i];
-    __syncthreads();
-    for (int t = threadIdx.x; t < 64 * V; t += blockDim.x) {
-      const int col = c * 64 * V + t;
-      if (col < n_cols) {
-        A s = A(0);
-#pragma unroll
-        for (int ww = 0; ww < kRowWaves; ++ww) s += red[ww][t];
-        partial[(int64_t)blockIdx.x * n_cols + col] = s;
-      }
-    }
+    for (int i = 0; i < V; ++i)
+      if (col + i < n_cols) partial[(int64_t)blockIdx.x * n_cols + col + i] = dg[k][i];
   }
 }
 
@@ -497,8 +612,9 @@ __global__ __launch_bounds__(256) void men_bwd_mp_k(
   }
 }
 
-// dw[c] = sum_g partial[g][c], fixed order: 16 waves stride over g, then the
-// 16 wave sums are added in wave order.
+// dw[c] = sum_g partial[g][c] in a fixed order. A block owns 64 columns; its
+// 16 waves stride over g with 4 independent accumulators each (loads stay in
+// flight), then the 16 wave sums are added in wave order.
 template <typename A>
 __global__ __launch_bounds__(1024) void colsum_k(const A* __restrict__ partial, int G, int n_cols,
                                                  A* __restrict__ out) {
@@ -506,10 +622,18 @@ __global__ __launch_bounds__(1024) void colsum_k(const A* __restrict__ partial, 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int col = blockIdx.x * 64 + lane;
-  A s = A(0);
-  if (col < n_cols)
-    for (int g = wave; g < G; g += 16) s += partial[(int64_t)g * n_cols + col];
-  red[wave][lane] = s;
+  A s0 = A(0), s1 = A(0), s2 = A(0), s3 = A(0);
+  if (col < n_cols) {
+    int g = wave;
+    for (; g + 48 < G; g += 64) {
+      s0 += partial[(int64_t)g * n_cols + col];
+      s1 += partial[(int64_t)(g + 16) * n_cols + col];
+      s2 += partial[(int64_t)(g + 32) * n_cols + col];
+      s3 += partial[(int64_t)(g + 48) * n_cols + col];
+    }
+    for (; g < G; g += 16) s0 += partial[(int64_t)g * n_cols + col];
+  }
+  red[wave][lane] = (s0 + s1) + (s2 + s3);
   __syncthreads();
   if (wave == 0 && col < n_cols) {
     A t = A(0);
@@ -527,6 +651,15 @@ template <typename A> __global__ void fill_zero_k(A* __restrict__ p, int64_t n) 
 // ============================================================================
 // Host launchers
 // ============================================================================
+
+// Persistent row grids: up to `per_cu` 256-thread blocks per compute unit,
+// and at least 4 rows per block so the two-row prefetch (which clamps past
+// the last row) wastes little.
+constexpr int kRowBlocksPerCU = 8;
+static inline int64_t row_grid(int64_t rows, int per_cu) {
+  const int64_t cap = std::min<int64_t>((int64_t)per_cu * num_cus(), (rows + 3) / 4);
+  return std::max<int64_t>(1, std::min<int64_t>(rows, cap));
+}
 
 static inline int pick_nch(int64_t n_cols, int per) {
   const int64_t need = (n_cols + per - 1) / per;
@@ -618,9 +751,9 @@ static int rsoftmax_fwd_t(const T* x, T* p, int64_t rows, int64_t cols, int64_t 
                           float eps, hipStream_t st) {
   constexpr int V = Raw<T>::V;
   const bool vec = cols % V == 0 && ldx % V == 0 && ldp % V == 0 && aligned16(x) && aligned16(p);
-  const int nch = vec ? pick_nch(cols, 64 * V) : 0;
+  const int nch = vec ? pick_nch(cols, 256 * V) : 0;
   if (nch) {
-    const int64_t blocks = (rows + kRowWaves - 1) / kRowWaves;
+    const int64_t blocks = row_grid(rows, kRowBlocksPerCU);
     KAT_NCH_SWITCH(nch, hipLaunchKernelGGL((rsoftmax_fwd_k<T, N>), dim3((unsigned)blocks),
                                            dim3(256), 0, st, x, p, rows, (int)cols, ldx, ldp, eps));
   } else {
@@ -637,9 +770,9 @@ static int rsoftmax_bwd_t(const T* dy, const T* x, const T* p, T* dx, int64_t ro
   constexpr int V = Raw<T>::V;
   const bool vec = cols % V == 0 && lddy % V == 0 && ldx % V == 0 && ldp % V == 0 &&
                    lddx % V == 0 && aligned16(dy) && aligned16(x) && aligned16(p) && aligned16(dx);
-  const int nch = vec ? pick_nch(cols, 64 * V) : 0;
+  const int nch = vec ? pick_nch(cols, 256 * V) : 0;
   if (nch) {
-    const int64_t blocks = (rows + kRowWaves - 1) / kRowWaves;
+    const int64_t blocks = row_grid(rows, kRowBlocksPerCU);
     KAT_NCH_SWITCH(nch, hipLaunchKernelGGL((rsoftmax_bwd_k<T, N>), dim3((unsigned)blocks),
                                            dim3(256), 0, st, dy, x, p, dx, rows, (int)cols, lddy,
                                            ldx, ldp, lddx, eps));
@@ -654,10 +787,11 @@ template <typename T, typename W>
 static int men_fwd_t(const T* x, const W* w, T* y, float* mu, int64_t rows, int64_t cols,
                      int64_t ldx, int64_t ldy, float eps, hipStream_t st) {
   constexpr int V = Raw<T>::V;
-  const bool vec = cols % V == 0 && ldx % V == 0 && ldy % V == 0 && aligned16(x) && aligned16(y);
-  const int nch = vec ? pick_nch(cols, 64 * V) : 0;
+  const bool vec = cols % V == 0 && ldx % V == 0 && ldy % V == 0 && aligned16(x) &&
+                   aligned16(y) && aligned16(w);
+  const int nch = vec ? pick_nch(cols, 256 * V) : 0;
   if (nch) {
-    const int64_t blocks = (rows + kRowWaves - 1) / kRowWaves;
+    const int64_t blocks = row_grid(rows, kRowBlocksPerCU);
     KAT_NCH_SWITCH(nch, hipLaunchKernelGGL((men_fwd_k<T, W, N>), dim3((unsigned)blocks), dim3(256),
                                            0, st, x, w, y, mu, rows, (int)cols, ldx, ldy, eps));
   } else {
@@ -668,10 +802,11 @@ static int men_fwd_t(const T* x, const W* w, T* y, float* mu, int64_t rows, int6
   return check_launch("kat_men_fwd");
 }
 
+// dgamma partials cost G x cols x 4 bytes of extra traffic (written here,
+// read by colsum_k): two blocks per CU.
 static int men_bwd_grid(int64_t rows, bool resident) {
-  const int64_t want = resident ? (rows + kRowWaves - 1) / kRowWaves : rows;
-  const int64_t cap = 2LL * num_cus();
-  return (int)std::max<int64_t>(1, std::min<int64_t>(want, cap));
+  (void)resident;
+  return (int)row_grid(rows, 2);
 }
 
 template <typename T, typename W>
@@ -682,8 +817,8 @@ static int men_bwd_t(const T* dy, const T* x, const W* w, const float* mu, T* dx
   typedef typename AccT<T>::type A;
   constexpr int V = Raw<T>::V;
   const bool vec = cols % V == 0 && lddy % V == 0 && ldx % V == 0 && lddx % V == 0 &&
-                   aligned16(dy) && aligned16(x) && aligned16(dx);
-  const int nch = vec ? pick_nch(cols, 64 * V) : 0;
+                   aligned16(dy) && aligned16(x) && aligned16(dx) && aligned16(w);
+  const int nch = vec ? pick_nch(cols, 256 * V) : 0;
   const int G = men_bwd_grid(rows, nch != 0);
   const size_t need = (size_t)G * (size_t)cols * sizeof(A);
   if (ws_bytes < need || (need && ws == nullptr))
