@@ -3,11 +3,15 @@
 // Kernel choice: bf16 / fp16 tensors with a head dim the MFMA kernels cover
 // (and 16-byte aligned rows) go to the MFMA kernels; everything else (fp32,
 // other head dims up to 256, unaligned views) to the fp32 tiled kernels.
-// Setting KAT_ATTN_IMPL=tiled in the environment forces the tiled kernels
-// (used by the tests to cross-check the two on the GPU).
+// KAT_ATTN_IMPL in the environment overrides the choice: "tiled" forces the
+// tiled kernels, "mfma" makes a bf16 / fp16 call that cannot take the MFMA
+// kernels fail with KAT_EUNSUPPORTED instead of falling back (both used by the
+// tests to pin which kernels they exercise).
 
 #include <stdlib.h>
 #include <string.h>
+
+#include <algorithm>
 
 #include "attn_common.h"
 #include "kat_common.h"
@@ -20,6 +24,10 @@ namespace {
 bool force_tiled() {
   const char* e = getenv("KAT_ATTN_IMPL");
   return e && strcmp(e, "tiled") == 0;
+}
+bool require_mfma() {
+  const char* e = getenv("KAT_ATTN_IMPL");
+  return e && strcmp(e, "mfma") == 0;
 }
 
 int fill_args(const char* nm, AttnArgs& a, int64_t B, int64_t H, int64_t T, int64_t D,
@@ -50,11 +58,19 @@ template <typename T> bool rows16(const void* p, const int64_t* s) {
          (s[1] * (int64_t)sizeof(T)) % 16 == 0 && (s[2] * (int64_t)sizeof(T)) % 16 == 0;
 }
 
-// workspace: Delta [B*H*T] fp32, then cinv [B*H*T] fp32 (each 256-byte aligned)
+// workspace of the tiled path: Delta [B*H*T] fp32, then cinv [B*H*T] fp32 (each
+// 256-byte aligned); the MFMA path lays out its own (attn_mfma_workspace). One
+// buffer of the larger size serves whichever path a call takes.
 size_t stat_bytes(int64_t B, int64_t H, int64_t T) {
   return (((size_t)(B * H * T) * sizeof(float)) + 255) & ~(size_t)255;
 }
 size_t delta_bytes(int64_t B, int64_t H, int64_t T) { return 2 * stat_bytes(B, H, T); }
+size_t bwd_workspace(int64_t B, int64_t H, int64_t T, int64_t D, int dtype) {
+  size_t n = delta_bytes(B, H, T);
+  if ((dtype == KAT_BF16 || dtype == KAT_F16) && attn_mfma_supported((int)D))
+    n = std::max(n, attn_mfma_workspace(B, H, T, D));
+  return n;
+}
 
 }  // namespace
 
@@ -64,19 +80,23 @@ template <typename T> static int attn_fwd_t(const AttnArgs& a, hipStream_t st) {
     const int rc = attn_fwd_mfma<T>(a, st);
     if (rc != KAT_EUNSUPPORTED) return rc;
   }
+  if (require_mfma()) return fail(KAT_EUNSUPPORTED, "kat_attn_fwd: shape / layout not covered by the MFMA kernels");
   return attn_fwd_generic<T>(a, st);
 }
 
 template <typename T>
-static int attn_bwd_t(const AttnArgs& a, float* delta, float* cinv, hipStream_t st) {
-  if (int rc = attn_delta<T>(a, delta, cinv, st)) return rc;
+static int attn_bwd_t(const AttnArgs& a, void* ws, hipStream_t st) {
   if (!force_tiled() && attn_mfma_supported(a.D) && rows16<T>(a.q, a.sq) &&
       rows16<T>(a.k, a.sk) && rows16<T>(a.v, a.sv) && rows16<T>(a.o, a.so) &&
       rows16<T>(a.dout, a.sdo) && rows16<T>(a.dq, a.sdq) && rows16<T>(a.dk, a.sdk) &&
       rows16<T>(a.dv, a.sdv)) {
-    const int rc = attn_bwd_mfma<T>(a, delta, cinv, st);
+    const int rc = attn_bwd_mfma<T>(a, ws, st);
     if (rc != KAT_EUNSUPPORTED) return rc;
   }
+  if (require_mfma()) return fail(KAT_EUNSUPPORTED, "kat_attn_bwd: shape / layout not covered by the MFMA kernels");
+  float* delta = reinterpret_cast<float*>(ws);
+  float* cinv = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + stat_bytes(a.B, a.H, a.T));
+  if (int rc = attn_delta<T>(a, delta, cinv, st)) return rc;
   return attn_bwd_generic<T>(a, delta, st);
 }
 
@@ -109,10 +129,8 @@ extern "C" int kat_attn_fwd(const void* q, const void* k, const void* v, void* o
 
 extern "C" size_t kat_attn_bwd_workspace_size(int64_t B, int64_t H, int64_t T, int64_t D,
                                               int dtype) {
-  (void)D;
-  (void)dtype;
-  if (B <= 0 || H <= 0 || T <= 0) return 0;
-  return delta_bytes(B, H, T);
+  if (B <= 0 || H <= 0 || T <= 0 || D < 0) return 0;
+  return bwd_workspace(B, H, T, D, dtype);
 }
 
 extern "C" int kat_attn_bwd(const void* q, const void* k, const void* v, const void* out,
@@ -128,7 +146,7 @@ extern "C" int kat_attn_bwd(const void* q, const void* k, const void* v, const v
   if (B * H * T == 0 || D == 0) return KAT_OK;
   if (!q || !k || !v || !out || !L || !dout || !dq || !dk || !dv || !slopes)
     return fail(KAT_EINVAL, "%s: null pointer", nm);
-  const size_t need = delta_bytes(B, H, T);
+  const size_t need = bwd_workspace(B, H, T, D, dtype);
   if (!workspace || workspace_bytes < need)
     return fail(KAT_EINVAL, "%s: workspace %zu bytes < required %zu", nm, workspace_bytes, need);
   a.q = q;
@@ -150,8 +168,8 @@ extern "C" int kat_attn_bwd(const void* q, const void* k, const void* v, const v
     case KAT_F32:
       if (int rc = attn_delta<float>(a, delta, cinv, st)) return rc;
       return attn_bwd_generic<float>(a, delta, st);
-    case KAT_BF16: return attn_bwd_t<bf16>(a, delta, cinv, st);
-    case KAT_F16: return attn_bwd_t<f16>(a, delta, cinv, st);
+    case KAT_BF16: return attn_bwd_t<bf16>(a, workspace, st);
+    case KAT_F16: return attn_bwd_t<f16>(a, workspace, st);
     default: return fail(KAT_EUNSUPPORTED, "%s: unsupported dtype %d", nm, dtype);
   }
 }

@@ -30,9 +30,11 @@ template <typename T> int attn_delta(const AttnArgs& a, float* delta, float* cin
 template <typename T> int attn_bwd_generic(const AttnArgs& a, const float* delta, hipStream_t st);
 
 // bf16 / fp16 MFMA kernels; return KAT_EUNSUPPORTED when the shape is not covered.
+// The backward runs its own prep pass; ws holds attn_mfma_workspace() bytes:
+// per-row stats (float2), then fp16 copies of Q and K ([B*H][T][D] each).
 template <typename T> int attn_fwd_mfma(const AttnArgs& a, hipStream_t st);
-template <typename T>
-int attn_bwd_mfma(const AttnArgs& a, const float* delta, const float* cinv, hipStream_t st);
+template <typename T> int attn_bwd_mfma(const AttnArgs& a, void* ws, hipStream_t st);
 bool attn_mfma_supported(int D);
+size_t attn_mfma_workspace(int64_t B, int64_t H, int64_t T, int64_t D);
 
 }  // namespace kat

@@ -1,224 +1,98 @@
 // bf16 / fp16 MFMA rational attention for gfx950 (CDNA4).
 //
-// Forward (one block = 128 queries of one (b, h); 4 waves x 32 queries):
-//   for each 64-key tile (K, V row-major in LDS, double-buffered, padded rows):
-//     S^T[key][q] = K . Q^T             v_mfma_f32_16x16x32_{bf16,f16}
-//       A = K rows from LDS (ds_read_b128), B = Q^T fragments kept in VGPRs,
-//       C initialised with the ALiBi bias / scale, so one FMA gives
-//       s = scale * q.k - slope * (q - key)
-//     f' = (1 + s / (|s| + 1))^4 = 16 sigma(s)^4     (one v_rcp_f32 per score)
-//     O^T[d][q] += V^T . P^T            A = V^T via ds_read_tr16_b64 from the
-//                                       row-major V tile, B = P^T straight from
-//                                       the S^T accumulator registers
-//   L' = sum f' (per lane, then across the 4 lane groups),
-//   o = O / (L' + 16 eps), L = L' / 16.
-// The factor 16 is exact in binary floating point, so o and L equal the
-// reference's f = sigma^4 formulation (forward.py:137-159) up to rounding.
-// There is no running-max rescale: sigma^4 lies in (0, 1).
+// Three kernels carry the attention math, plus a streaming prep pass:
+//   attn_fwd_k      O, L      query-tile blocks; K, V tiles stream through LDS
+//   attn_bwd_prep_k Delta, stats, fp16 copies of Q and K (row-parallel)
+//   attn_bwd_dq_k   dQ        query-tile blocks; fp16 K and V tiles stream
+//   attn_bwd_dkv_k  dK, dV    key-tile blocks; fp16 Q and dO tiles stream
+// No atomics: every output element is written by one wave, so results are
+// deterministic.
 //
-// MFMA 16x16x32 operand layout (lane l, g = l / 16): A[m = l % 16][k-set of g],
-// B[k-set of g][n = l % 16], C[4g + j][l % 16]. A and B use the same k-set per
-// lane group, so any consistent assignment of keys to (g, element) is valid;
-// here lane group g, element i < 4 holds key 4g + i of the first 16-key
-// subtile and element 4 + i key 4g + i of the second.
+// Common structure. Each wave owns 32 rows (queries, or keys for dK/dV) whose
+// operand fragments stay in VGPRs as the B operand of v_mfma_f32_16x16x32; the
+// streamed side is staged 64 rows at a time by LDS-DMA into a swizzled,
+// double-buffered LDS tile and read as the A operand, either row-wise
+// (ds_read_b128) or transposed (ds_read_b64_tr_b16). A 64-row tile is worked in
+// 16-row halves: S (and dP) for a half, the elementwise map for it, and the
+// product that consumes the result once two halves (32 rows = one MFMA k-step)
+// are ready; the compiler interleaves the MFMAs of one half with the VALU work
+// of the previous one.
+//
+// Forward math (forward.py:137-159 semantics). Per score,
+//   s  = scale q.k - slope (i - j),  r = 1 / (|s| + 1),  t = 1 + s r = 2 sigma(s)
+//   f' = t^4 = 16 sigma^4            (no running max: sigma^4 lies in (0, 1))
+//   L' = sum_j f',  o = (sum_j f' v_j) / (L' + 16 eps),  L = L' / 16.
+// The factor 16 is exact in binary floating point. The ALiBi bias is split into
+// a per-lane part fed to QK^T as its C input (divided by scale) and a wave-uniform
+// part added by the FMA that applies the scale.
+//
+// Backward math. With cinv_i = 1 / (16 (L_i + eps)):
+//   p  = t^4 cinv_i,   dS = p g (dP - Delta_i) = 4 cinv_i t^3 r^2 (dP - Delta_i)
+//   dQ = scale dS K,   dK = scale dS^T Q,   dV = P^T dO.
+// The reference writes g = 2 / ((|s|+1)^2 (sigma + eps)) (backward.py:145);
+// these kernels use sigma in place of sigma + eps, a relative change of
+// eps / (sigma + eps) in dS: <= 2e-6 wherever s >= 0, and otherwise on scores
+// whose p <= (r / 2)^4 / L is itself negligible.
 
 #include <algorithm>
 #include <type_traits>
 
 #include "attn_common.h"
-#include "kat_common.h"
+#include "attn_mfma_dev.h"
 #include "kat_internal.h"
 
 namespace kat {
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef short i16x4 __attribute__((ext_vector_type(4)));
-typedef short i16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+using namespace mfma;
 
-template <typename T> struct Mfma;
-template <> struct Mfma<bf16> {
-  typedef bf16x8 frag;
-  static __device__ __forceinline__ f32x4 mma(const i16x8& a, const i16x8& b, const f32x4& c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16((bf16x8)a, (bf16x8)b, c, 0, 0, 0);
-  }
-  static __device__ __forceinline__ uint32_t pack2(float x, float y) {
-    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-    typedef float f32x2 __attribute__((ext_vector_type(2)));
-    f32x2 f = {x, y};
-    bf16x2 b = __builtin_convertvector(f, bf16x2);
-    return __builtin_bit_cast(uint32_t, b);
-  }
-};
-template <> struct Mfma<f16> {
-  typedef f16x8 frag;
-  static __device__ __forceinline__ f32x4 mma(const i16x8& a, const i16x8& b, const f32x4& c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16((f16x8)a, (f16x8)b, c, 0, 0, 0);
-  }
-  static __device__ __forceinline__ uint32_t pack2(float x, float y) {
-    typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-    typedef float f32x2 __attribute__((ext_vector_type(2)));
-    f32x2 f = {x, y};
-    f16x2 b = __builtin_convertvector(f, f16x2);
-    return __builtin_bit_cast(uint32_t, b);
-  }
-};
+constexpr int kNW = 4;         // waves per block
+constexpr int kRows = 32;      // rows owned per wave
+constexpr int kBM = kNW * kRows;  // rows owned per block
+constexpr int kBN = 64;        // streamed rows per LDS tile
 
-// Block order. Workgroups are dispatched round-robin over the 8 XCDs (block
-// id i runs on XCD i % 8), and each XCD has its own L2. Heads are assigned to
-// XCDs (head h on XCD h % 8, when B*H is a multiple of 8) and each XCD walks
-// its heads one after another, longest (causal) tiles first, so the K/V (or
-// Q/dO) of the one or two heads in flight per XCD stay L2-resident.
-// Returns the (b*H + h) index and the tile rank (0 = most work).
-__device__ __forceinline__ void block_order(int id, int n_tiles, int BH, int& bh, int& rank) {
-  if ((BH & 7) == 0) {
-    const int xcd = id & 7, slot = id >> 3;
-    const int hl = slot / n_tiles;
-    rank = slot - hl * n_tiles;
-    bh = xcd + 8 * hl;
-  } else {
-    bh = id / n_tiles;
-    rank = id - bh * n_tiles;
-  }
-}
-
-constexpr int FBM = 128;  // queries per block
-constexpr int FBN = 64;   // keys per tile
-constexpr int FWAVES = 4;
-
-template <int D> struct FwdSmem {
-  static constexpr int LD = D + 16;  // padded row (elements): spreads rows over banks
-  short k[2][FBN * LD];
-  short v[2][FBN * LD];
-};
-
-__device__ __forceinline__ i16x8 lds_read16(const short* p) {
-  return *reinterpret_cast<const i16x8*>(p);
-}
-
-// Transposing LDS read (gfx950): within each 16-lane group, result lane i,
-// element j = the 16-bit element (i % 4) of the 8 bytes addressed by source
-// lane i / 4 + 4 j. With source lane s addressing row (r0 + s / 4), column
-// (c0 + 4 (s % 4)) of a row-major tile, lane i receives rows r0..r0+3 at
-// column c0 + i.
-__device__ __forceinline__ i16x4 lds_read_tr(const short* p) {
-  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
-}
-
-// fp16 products for dS: dS = p g (dP - Delta) is rounded to fp16 (11-bit
-// significand) rather than bf16 before the dQ = dS K and dK = dS^T Q
-// products, so its rounding error is 4x smaller; the K / Q operands of those
-// products are converted bf16 -> fp16, which is exact for |x| in
-// [2^-14, 65504]. Larger magnitudes are clamped to +-65504, and smaller ones
-// keep fp16's subnormal spacing 2^-24.
-__device__ __forceinline__ f32x4 mma_f16(const i16x8& a, const i16x8& b, const f32x4& c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16((f16x8)a, (f16x8)b, c, 0, 0, 0);
-}
-__device__ __forceinline__ uint32_t pack2_f16(float x, float y) { return Mfma<f16>::pack2(x, y); }
-
-template <typename T> __device__ __forceinline__ i16x8 frag_to_f16(const i16x8& v);
-template <> __device__ __forceinline__ i16x8 frag_to_f16<f16>(const i16x8& v) { return v; }
-template <> __device__ __forceinline__ i16x8 frag_to_f16<bf16>(const i16x8& v) {
-  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-  const u32x4 w = __builtin_bit_cast(u32x4, v);
-  u32x4 o;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const float lo = __builtin_bit_cast(float, w[e] << 16);
-    const float hi = __builtin_bit_cast(float, w[e] & 0xffff0000u);
-    o[e] = pack2_f16(fminf(fmaxf(lo, -65504.f), 65504.f), fminf(fmaxf(hi, -65504.f), 65504.f));
-  }
-  return __builtin_bit_cast(i16x8, o);
-}
-
-// Shared pieces of the forward and dQ kernels: 64-key K/V tiles staged
-// global -> VGPRs -> LDS (double-buffered), rows zero-filled past T.
-template <typename T, int D> struct KvStager {
-  static constexpr int LD = FwdSmem<D>::LD;
-  static constexpr int CPR = D / 8;                 // 16-byte chunks per row
-  static constexpr int LOADS = FBN * CPR / 256;     // chunks per thread per tile
-  i16x8 kst[LOADS], vst[LOADS];
-  __device__ __forceinline__ void load(const T* __restrict__ kp, int64_t skt,
-                                       const T* __restrict__ vp, int64_t svt, int k0, int T_,
-                                       int tid) {
-#pragma unroll
-    for (int u = 0; u < LOADS; ++u) {
-      const int c = tid + 256 * u;
-      const int row = c / CPR, col = (c % CPR) * 8;
-      const int key = k0 + row;
-      if (key < T_) {
-        kst[u] = *reinterpret_cast<const i16x8*>(kp + (int64_t)key * skt + col);
-        vst[u] = *reinterpret_cast<const i16x8*>(vp + (int64_t)key * svt + col);
-      } else {
-        kst[u] = i16x8{0, 0, 0, 0, 0, 0, 0, 0};
-        vst[u] = i16x8{0, 0, 0, 0, 0, 0, 0, 0};
-      }
-    }
-  }
-  __device__ __forceinline__ void store(FwdSmem<D>& sm, int buf, int tid) {
-#pragma unroll
-    for (int u = 0; u < LOADS; ++u) {
-      const int c = tid + 256 * u;
-      const int row = c / CPR, col = (c % CPR) * 8;
-      *reinterpret_cast<i16x8*>(&sm.k[buf][row * LD + col]) = kst[u];
-      *reinterpret_cast<i16x8*>(&sm.v[buf][row * LD + col]) = vst[u];
-    }
-  }
-};
-
-// A-operand fragment of a 16x16x32 MFMA taken transposed from a row-major
-// [row][col] LDS tile: lane (g, li) receives column c0 + li of rows
-// r0 + 4 g + {0..3} (elements 0-3) and r0 + 16 + 4 g + {0..3} (elements 4-7).
-__device__ __forceinline__ i16x8 lds_frag_tr(const short* tile, int ld, int r0, int c0, int g,
-                                             int li) {
-  const short* p0 = tile + (r0 + 4 * g + (li >> 2)) * ld + c0 + 4 * (li & 3);
-  const i16x4 lo = lds_read_tr(p0);
-  const i16x4 hi = lds_read_tr(p0 + 16 * ld);
-  return i16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-}
-
+// ============================================================================
+// Forward: 128 queries per block, 4 waves x 32 queries, 2 blocks per CU.
+//   S^T[key][q]  = K Q^T (+ bias)   A = K  (LDS rows)         B = Q^T (VGPRs)
+//   O^T[d][q]   += V^T P^T          A = V^T (LDS transposed)  B = P^T (from S^T)
+// ============================================================================
 template <typename T, int D>
-__global__ __launch_bounds__(256, 2) void attn_fwd_mfma_k(AttnArgs a) {
+__global__ __launch_bounds__(256, 2) void attn_fwd_k(AttnArgs a) {
   typedef Mfma<T> M;
-  constexpr int LD = FwdSmem<D>::LD;
-  constexpr int KK = D / 32;   // k-steps of QK^T
-  constexpr int DS = D / 16;   // 16-wide d subtiles of O^T
-  __shared__ FwdSmem<D> sm;
+  constexpr int KK = D / 32;  // k-steps of QK^T
+  constexpr int DS = D / 16;  // 16-wide d subtiles of O^T
+  __shared__ short sk[2][kBN * D];
+  __shared__ short sv[2][kBN * D];
 
   const int T_ = a.T, H = a.H;
-  const int n_qt = (T_ + FBM - 1) / FBM;
   int bh, rank;
-  block_order((int)blockIdx.x, n_qt, a.B * H, bh, rank);
-  const int qt = n_qt - 1 - rank;  // longest (causal) tiles first
+  block_order((int)blockIdx.x, a.B * H, bh, rank);
+  const int n_qt = (T_ + kBM - 1) / kBM;
+  const int q0 = (n_qt - 1 - rank) * kBM;
   const int b = bh / H, h = bh - b * H;
-  const int q0 = qt * FBM;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 4, li = lane & 15;
-  const int qw = q0 + 32 * w;  // first query of this wave
+  const int qw = q0 + kRows * w;
 
-  const T* __restrict__ qp = (const T*)a.q + b * a.sq[0] + h * a.sq[1];
-  const T* __restrict__ kp = (const T*)a.k + b * a.sk[0] + h * a.sk[1];
-  const T* __restrict__ vp = (const T*)a.v + b * a.sv[0] + h * a.sv[1];
+  const T* qp = (const T*)a.q + b * a.sq[0] + h * a.sq[1];
+  const T* kp = (const T*)a.k + b * a.sk[0] + h * a.sk[1];
+  const T* vp = (const T*)a.v + b * a.sv[0] + h * a.sv[1];
+  const uint32_t sq2 = (uint32_t)a.sq[2], sk2 = (uint32_t)a.sk[2], sv2 = (uint32_t)a.sv[2];
+  const uint32_t kbytes = row_bytes(T_, sk2, D), vbytes = row_bytes(T_, sv2, D);
   const float slope = a.slopes[h];
   const float scale = a.scale;
 
   // Q^T fragments (B operand): lane (g, li) holds Q[qw + 16 qs + li][32 kk + 8 g .. +7]
   i16x8 qf[2][KK];
+  {
+    const __amdgpu_buffer_rsrc_t rq = rsrc(qp, row_bytes(T_, sq2, D));
 #pragma unroll
-  for (int qs = 0; qs < 2; ++qs) {
-    const int qrow = qw + 16 * qs + li;
+    for (int qs = 0; qs < 2; ++qs)
 #pragma unroll
-    for (int kk = 0; kk < KK; ++kk)
-      qf[qs][kk] = qrow < T_
-                       ? *reinterpret_cast<const i16x8*>(qp + (int64_t)qrow * a.sq[2] + 32 * kk + 8 * g)
-                       : i16x8{0, 0, 0, 0, 0, 0, 0, 0};
+      for (int kk = 0; kk < KK; ++kk)
+        qf[qs][kk] = load16(rq, ((uint32_t)(qw + 16 * qs + li) * sq2 + 32 * kk + 8 * g) * 2);
   }
-  // ALiBi bias slope * (key - q) split into a per-lane part, fed to QK^T as its
-  // C input (divided by scale), and a wave-uniform part added by the FMA that
-  // applies the scale: element (qs, ks, j) has key = k0 + 16 ks + 4 g + j and
-  // q = qw + 16 qs + li.
+  // element (qs, j) of a 16-key half starting at key kh: key = kh + 4 g + j,
+  // q = qw + 16 qs + li; bias slope (key - q) = per-lane part + uniform part
   f32x4 cb;
 #pragma unroll
   for (int j = 0; j < 4; ++j) cb[j] = (slope / scale) * (float)(4 * g + j - li);
@@ -230,91 +104,86 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_mfma_k(AttnArgs a) {
     for (int qs = 0; qs < 2; ++qs) oacc[ds][qs] = f32x4{0.f, 0.f, 0.f, 0.f};
   float lsum[2] = {0.f, 0.f};
 
-  // one 64-key tile; MASK: the tile crosses this wave's diagonal
-  auto tile = [&](auto mask_tag, int k0, const short* ks_, const short* vs_) {
-    constexpr bool MASK = decltype(mask_tag)::value;
-    // S^T = K Q^T (+ bias / scale): k-step outer, 8 independent accumulators
-    f32x4 sacc[2][4];
+  TileDma<D, kNW> dk, dv;
+  dk.init(w, lane, sk2);
+  dv.init(w, lane, sv2);
+
+  // S^T of the 16 keys at tile rows hr .. hr + 15
+  auto m1 = [&](int hr, f32x4 (&s_)[2], const short* ks_) {
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-      for (int qs = 0; qs < 2; ++qs) sacc[qs][ks] = cb;
+    for (int qs = 0; qs < 2; ++qs) s_[qs] = cb;
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {
-      i16x8 kf[4];
+      const i16x8 kf = lds16(ks_ + soff<D>(hr + li, 32 * kk + 8 * g));
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) kf[ks] = lds_read16(ks_ + (16 * ks + li) * LD + 32 * kk + 8 * g);
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-        for (int qs = 0; qs < 2; ++qs) sacc[qs][ks] = M::mma(kf[ks], qf[qs][kk], sacc[qs][ks]);
-    }
-    // f' = (1 + s r)^4, r = 1 / (|s| + 1); P^T packed straight from the
-    // accumulator layout into the B operand of O^T += V^T P^T
-    i16x8 pf[2][2];
-#pragma unroll
-    for (int qs = 0; qs < 2; ++qs) {
-      float ls = 0.f;
-      uint32_t pk[4][2];
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const float tterm = slope * (float)(k0 - qw + 16 * ks - 16 * qs);
-        float f[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float s = fmaf(sacc[qs][ks][j], scale, tterm);
-          const float r = __builtin_amdgcn_rcpf(fabsf(s) + 1.f);
-          const float t = fmaf(s, r, 1.f);
-          const float t2 = t * t;
-          f[j] = t2 * t2;
-          if (MASK && k0 + 16 * ks + 4 * g + j > qw + 16 * qs + li) f[j] = 0.f;
-        }
-        ls += (f[0] + f[1]) + (f[2] + f[3]);
-        pk[ks][0] = M::pack2(f[0], f[1]);
-        pk[ks][1] = M::pack2(f[2], f[3]);
-      }
-      lsum[qs] += ls;
-#pragma unroll
-      for (int kk2 = 0; kk2 < 2; ++kk2) {
-        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-        u32x4 u = {pk[2 * kk2][0], pk[2 * kk2][1], pk[2 * kk2 + 1][0], pk[2 * kk2 + 1][1]};
-        pf[qs][kk2] = __builtin_bit_cast(i16x8, u);
-      }
-    }
-    // O^T += V^T P^T, two d-subtiles at a time (4 independent chains)
-#pragma unroll
-    for (int ds = 0; ds < DS; ds += 2) {
-      i16x8 vf[2][2];
-#pragma unroll
-      for (int dd = 0; dd < 2; ++dd)
-#pragma unroll
-        for (int kk2 = 0; kk2 < 2; ++kk2) vf[dd][kk2] = lds_frag_tr(vs_, LD, 32 * kk2, 16 * (ds + dd), g, li);
-#pragma unroll
-      for (int kk2 = 0; kk2 < 2; ++kk2)
-#pragma unroll
-        for (int dd = 0; dd < 2; ++dd)
-#pragma unroll
-          for (int qs = 0; qs < 2; ++qs)
-            oacc[ds + dd][qs] = M::mma(vf[dd][kk2], pf[qs][kk2], oacc[ds + dd][qs]);
+      for (int qs = 0; qs < 2; ++qs) s_[qs] = M::mma(kf, qf[qs][kk], s_[qs]);
     }
   };
+  // f' of those scores, packed as P^T; row sums into lsum
+  auto vh = [&](auto mask_tag, int kh, const f32x4 (&s_)[2], uint32_t (&pk)[2][2]) {
+    constexpr bool MASK = decltype(mask_tag)::value;
+#pragma unroll
+    for (int qs = 0; qs < 2; ++qs) {
+      const float tterm = slope * (float)(kh - qw - 16 * qs);
+      float f[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float s = fmaf(s_[qs][j], scale, tterm);
+        const float r = __builtin_amdgcn_rcpf(fabsf(s) + 1.f);
+        const float t = fmaf(s, r, 1.f);
+        const float t2 = t * t;
+        f[j] = t2 * t2;
+        if (MASK && kh + 4 * g + j > qw + 16 * qs + li) f[j] = 0.f;
+      }
+      lsum[qs] += (f[0] + f[1]) + (f[2] + f[3]);
+      pk[qs][0] = M::pack2(f[0], f[1]);
+      pk[qs][1] = M::pack2(f[2], f[3]);
+    }
+  };
+  // O^T += V^T P^T over the 32 keys at tile rows r0 .. r0 + 31
+  auto m2 = [&](int r0, const uint32_t (&pa)[2][2], const uint32_t (&pb)[2][2], const short* vs_) {
+    i16x8 pf[2];
+#pragma unroll
+    for (int qs = 0; qs < 2; ++qs) pf[qs] = pack_frag(pa[qs][0], pa[qs][1], pb[qs][0], pb[qs][1]);
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds) {
+      const i16x8 vt = frag_tr<D>(vs_, r0, 16 * ds, g, li);
+#pragma unroll
+      for (int qs = 0; qs < 2; ++qs) oacc[ds][qs] = M::mma(vt, pf[qs], oacc[ds][qs]);
+    }
+  };
+  auto tile = [&](auto mask_tag, int k0, const short* ks_, const short* vs_) {
+    f32x4 sA[2], sB[2];
+    uint32_t pa0[2][2], pb0[2][2], pa1[2][2], pb1[2][2];
+    m1(0, sA, ks_);
+    m1(16, sB, ks_);
+    vh(mask_tag, k0, sA, pa0);
+    m1(32, sA, ks_);
+    vh(mask_tag, k0 + 16, sB, pb0);
+    m2(0, pa0, pb0, vs_);
+    m1(48, sB, ks_);
+    vh(mask_tag, k0 + 32, sA, pa1);
+    vh(mask_tag, k0 + 48, sB, pb1);
+    m2(32, pa1, pb1, vs_);
+  };
 
-  const int kend = std::min(q0 + FBM, T_);
-  const int n_kt = (kend + FBN - 1) / FBN;
-  KvStager<T, D> stg;
-  stg.load(kp, a.sk[2], vp, a.sv[2], 0, T_, tid);
-  stg.store(sm, 0, tid);
+  const int n_kt = (std::min(q0 + kBM, T_) + kBN - 1) / kBN;
+  dk.issue(sk[0], kp, kbytes, 0, sk2, w);
+  dv.issue(sv[0], vp, vbytes, 0, sv2, w);
+  dma_wait();
   __syncthreads();
   for (int kt = 0; kt < n_kt; ++kt) {
     const int buf = kt & 1;
-    const bool more = kt + 1 < n_kt;
-    if (more) stg.load(kp, a.sk[2], vp, a.sv[2], (kt + 1) * FBN, T_, tid);
-    const int k0 = kt * FBN;
-    if (k0 + FBN - 1 <= qw)
-      tile(std::false_type{}, k0, sm.k[buf], sm.v[buf]);
-    else if (k0 <= qw + 31)
-      tile(std::true_type{}, k0, sm.k[buf], sm.v[buf]);
-    if (more) stg.store(sm, buf ^ 1, tid);
+    if (kt + 1 < n_kt) {
+      dk.issue(sk[buf ^ 1], kp, kbytes, (kt + 1) * kBN, sk2, w);
+      dv.issue(sv[buf ^ 1], vp, vbytes, (kt + 1) * kBN, sv2, w);
+    }
+    const int k0 = kt * kBN;
+    if (k0 + kBN - 1 <= qw)
+      tile(std::false_type{}, k0, sk[buf], sv[buf]);
+    else if (k0 <= qw + kRows - 1)
+      tile(std::true_type{}, k0, sk[buf], sv[buf]);
+    dma_wait();
     __syncthreads();
   }
 
@@ -333,79 +202,102 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_mfma_k(AttnArgs a) {
       T* orow = op + (int64_t)qrow * a.so[2];
 #pragma unroll
       for (int ds = 0; ds < DS; ++ds) {
-        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
         const f32x4 o = oacc[ds][qs];
-        u32x2 u = {M::pack2(o[0] * inv, o[1] * inv), M::pack2(o[2] * inv, o[3] * inv)};
-        *reinterpret_cast<u32x2*>(orow + 16 * ds + 4 * g) = u;
+        *reinterpret_cast<u32x2*>(orow + 16 * ds + 4 * g) =
+            u32x2{M::pack2(o[0] * inv, o[1] * inv), M::pack2(o[2] * inv, o[3] * inv)};
       }
     }
   }
 }
 
 // ============================================================================
-// Backward.  Per score (j <= i), with t = 1 + s r, r = 1 / (|s| + 1)
-// (so sigma = t / 2) and cinv_i = 1 / (16 (L_i + eps)):
-//   p  = sigma^4 / (L_i + eps)                 = t^4 cinv_i
-//   dS = p g (dP - Delta_i), g = 2 r^2 / sigma = 4 cinv_i t^3 r^2 (dP - Delta_i)
-// The reference writes g = 2 / ((|s|+1)^2 (sigma + eps)) (backward.py:145);
-// these kernels use sigma in place of sigma + eps, a relative change of
-// eps / (sigma + eps) in dS: <= 2e-6 wherever s >= 0, and otherwise on scores
-// whose p <= (r / 2)^4 / L is itself negligible.
-//   dQ  = scale dS K      -- attn_bwd_dq_mfma_k   (query-tile blocks)
-//   dK  = scale dS^T Q    -- attn_bwd_dkv_mfma_k  (key-tile blocks)
-//   dV  = P^T dO
-// Both kernels recompute S (and dP); no atomics, so results are deterministic.
-// dS enters the dQ and dK products in fp16 (see frag_to_f16).
+// Backward prep (row-parallel, D / 8 lanes per row, 8 elements per lane):
+//   Delta_i = <dO_i, O_i>,  stats_i = (4 cinv_i, -4 cinv_i Delta_i),
+//   q16 / k16 = Q / K rounded to fp16 (clamped to +-65504), [B*H][T][D].
 // ============================================================================
-
-// dQ: mirrors the forward (128 queries per block, 64-key K/V tiles in LDS).
-//   S^T  = K Q^T (+bias)   A = K  (LDS, b128)      B = Q^T  (VGPRs)
-//   dP^T = V dO^T          A = V  (LDS, b128)      B = dO^T (VGPRs)
-//   dQ^T += K^T dS^T       A = K^T (LDS, transposing read)  B = dS^T (registers)
 template <typename T, int D>
-__global__ __launch_bounds__(256) void attn_bwd_dq_mfma_k(AttnArgs a,
-                                                         const float* __restrict__ delta,
-                                                         const float* __restrict__ cinv) {
+__global__ __launch_bounds__(256) void attn_bwd_prep_k(AttnArgs a, float2* __restrict__ stats,
+                                                       f16* __restrict__ q16, f16* __restrict__ k16) {
+  constexpr int LPR = D / 8;
+  const int sub = threadIdx.x % LPR;
+  const int64_t row = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / LPR;
+  const int64_t nrows = (int64_t)a.B * a.H * a.T;
+  if (row >= nrows) return;
+  const int i = (int)(row % a.T);
+  const int64_t bh = row / a.T;
+  const int b = (int)(bh / a.H), h = (int)(bh % a.H);
+  const int d = 8 * sub;
+  const i16x8 ov = *reinterpret_cast<const i16x8*>((const T*)a.o + b * a.so[0] + h * a.so[1] + (int64_t)i * a.so[2] + d);
+  const i16x8 gv = *reinterpret_cast<const i16x8*>((const T*)a.dout + b * a.sdo[0] + h * a.sdo[1] + (int64_t)i * a.sdo[2] + d);
+  const i16x8 qv = *reinterpret_cast<const i16x8*>((const T*)a.q + b * a.sq[0] + h * a.sq[1] + (int64_t)i * a.sq[2] + d);
+  const i16x8 kv = *reinterpret_cast<const i16x8*>((const T*)a.k + b * a.sk[0] + h * a.sk[1] + (int64_t)i * a.sk[2] + d);
+  const VecT<T, 8> o8 = __builtin_bit_cast(VecT<T, 8>, ov), g8 = __builtin_bit_cast(VecT<T, 8>, gv);
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) s = fmaf((float)g8.v[e], (float)o8.v[e], s);
+#pragma unroll
+  for (int off = LPR / 2; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+  *reinterpret_cast<i16x8*>(q16 + row * D + d) = to_f16x8<T>(qv);
+  *reinterpret_cast<i16x8*>(k16 + row * D + d) = to_f16x8<T>(kv);
+  if (sub == 0) {
+    const float l = a.L[b * a.sl[0] + h * a.sl[1] + (int64_t)i * a.sl[2]];
+    const float c4 = 4.f / (16.f * (l + a.eps));
+    stats[row] = make_float2(c4, -c4 * s);
+  }
+}
+
+// ============================================================================
+// dQ: mirrors the forward (128 queries per block, 2 blocks per CU).
+//   S^T  = K16 Q16^T (+bias)  A = K16 (LDS rows)         B = Q16^T (VGPRs)
+//   dP^T = V dO^T             A = V   (LDS rows)         B = dO^T  (VGPRs)
+//   dQ^T += K16^T dS^T        A = K16^T (LDS transposed) B = dS^T  (from S^T, dP^T)
+// ============================================================================
+template <typename T, int D>
+__global__ __launch_bounds__(256, 2) void attn_bwd_dq_k(AttnArgs a, const float2* __restrict__ stats,
+                                                        const f16* __restrict__ k16) {
   typedef Mfma<T> M;
-  constexpr int LD = FwdSmem<D>::LD;
   constexpr int KK = D / 32;
   constexpr int DS = D / 16;
-  __shared__ FwdSmem<D> sm;
+  __shared__ short sk[2][kBN * D];
+  __shared__ short sv[2][kBN * D];
 
   const int T_ = a.T, H = a.H;
-  const int n_qt = (T_ + FBM - 1) / FBM;
   int bh, rank;
-  block_order((int)blockIdx.x, n_qt, a.B * H, bh, rank);
-  const int qt = n_qt - 1 - rank;
+  block_order((int)blockIdx.x, a.B * H, bh, rank);
+  const int n_qt = (T_ + kBM - 1) / kBM;
+  const int q0 = (n_qt - 1 - rank) * kBM;
   const int b = bh / H, h = bh - b * H;
-  const int q0 = qt * FBM;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 4, li = lane & 15;
-  const int qw = q0 + 32 * w;
+  const int qw = q0 + kRows * w;
 
-  const T* __restrict__ qp = (const T*)a.q + b * a.sq[0] + h * a.sq[1];
-  const T* __restrict__ kp = (const T*)a.k + b * a.sk[0] + h * a.sk[1];
-  const T* __restrict__ vp = (const T*)a.v + b * a.sv[0] + h * a.sv[1];
-  const T* __restrict__ dop = (const T*)a.dout + b * a.sdo[0] + h * a.sdo[1];
+  const T* qp = (const T*)a.q + b * a.sq[0] + h * a.sq[1];
+  const f16* kp = k16 + (int64_t)bh * T_ * D;
+  const T* vp = (const T*)a.v + b * a.sv[0] + h * a.sv[1];
+  const T* dop = (const T*)a.dout + b * a.sdo[0] + h * a.sdo[1];
+  const uint32_t sq2 = (uint32_t)a.sq[2], sv2 = (uint32_t)a.sv[2], sdo2 = (uint32_t)a.sdo[2];
+  const uint32_t kbytes = row_bytes(T_, D, D), vbytes = row_bytes(T_, sv2, D);
   const float slope = a.slopes[h];
   const float scale = a.scale;
 
   i16x8 qf[2][KK], dof[2][KK];
   float c4[2], nc4d[2];  // 4 cinv_q and -4 cinv_q Delta_q for q = qw + 16 qs + li
+  {
+    const __amdgpu_buffer_rsrc_t rq = rsrc(qp, row_bytes(T_, sq2, D));
+    const __amdgpu_buffer_rsrc_t ro = rsrc(dop, row_bytes(T_, sdo2, D));
 #pragma unroll
-  for (int qs = 0; qs < 2; ++qs) {
-    const int qrow = qw + 16 * qs + li;
-    const bool ok = qrow < T_;
+    for (int qs = 0; qs < 2; ++qs) {
+      const int qrow = qw + 16 * qs + li;
 #pragma unroll
-    for (int kk = 0; kk < KK; ++kk) {
-      qf[qs][kk] = ok ? *reinterpret_cast<const i16x8*>(qp + (int64_t)qrow * a.sq[2] + 32 * kk + 8 * g)
-                      : i16x8{0, 0, 0, 0, 0, 0, 0, 0};
-      dof[qs][kk] = ok ? *reinterpret_cast<const i16x8*>(dop + (int64_t)qrow * a.sdo[2] + 32 * kk + 8 * g)
-                       : i16x8{0, 0, 0, 0, 0, 0, 0, 0};
+      for (int kk = 0; kk < KK; ++kk) {
+        qf[qs][kk] = to_f16x8<T>(load16(rq, ((uint32_t)qrow * sq2 + 32 * kk + 8 * g) * 2));
+        dof[qs][kk] = load16(ro, ((uint32_t)qrow * sdo2 + 32 * kk + 8 * g) * 2);
+      }
+      const bool ok = qrow < T_;
+      const float2 st = stats[(int64_t)bh * T_ + (ok ? qrow : 0)];
+      c4[qs] = ok ? st.x : 0.f;
+      nc4d[qs] = ok ? st.y : 0.f;
     }
-    const int64_t ri = (int64_t)bh * T_ + qrow;
-    c4[qs] = ok ? 4.f * cinv[ri] : 0.f;
-    nc4d[qs] = ok ? -c4[qs] * delta[ri] : 0.f;
   }
   f32x4 cb;
 #pragma unroll
@@ -417,93 +309,92 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_mfma_k(AttnArgs a,
 #pragma unroll
     for (int qs = 0; qs < 2; ++qs) dqacc[ds][qs] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  auto tile = [&](auto mask_tag, int k0, const short* ks_, const short* vs_) {
-    constexpr bool MASK = decltype(mask_tag)::value;
-    f32x4 sacc[2][4], pacc[2][4];
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-      for (int qs = 0; qs < 2; ++qs) {
-        sacc[qs][ks] = cb;
-        pacc[qs][ks] = f32x4{0.f, 0.f, 0.f, 0.f};
-      }
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk) {
-      i16x8 kf[4], vf[4];
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        kf[ks] = lds_read16(ks_ + (16 * ks + li) * LD + 32 * kk + 8 * g);
-        vf[ks] = lds_read16(vs_ + (16 * ks + li) * LD + 32 * kk + 8 * g);
-      }
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-        for (int qs = 0; qs < 2; ++qs) {
-          sacc[qs][ks] = M::mma(kf[ks], qf[qs][kk], sacc[qs][ks]);
-          pacc[qs][ks] = M::mma(vf[ks], dof[qs][kk], pacc[qs][ks]);
-        }
-    }
-    i16x8 dsf[2][2];
+  TileDma<D, kNW> dk, dv;
+  dk.init(w, lane, D);
+  dv.init(w, lane, sv2);
+
+  // S^T and dP^T of the 16 keys at tile rows hr .. hr + 15
+  auto m1 = [&](int hr, f32x4 (&s_)[2], f32x4 (&p_)[2], const short* ks_, const short* vs_) {
 #pragma unroll
     for (int qs = 0; qs < 2; ++qs) {
-      uint32_t pk[4][2];
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const float tterm = slope * (float)(k0 - qw + 16 * ks - 16 * qs);
-        float d[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float s = fmaf(sacc[qs][ks][j], scale, tterm);
-          const float r = __builtin_amdgcn_rcpf(fabsf(s) + 1.f);
-          const float t = fmaf(s, r, 1.f);
-          const float u = t * r;
-          d[j] = (u * u * t) * fmaf(pacc[qs][ks][j], c4[qs], nc4d[qs]);
-          if (MASK && k0 + 16 * ks + 4 * g + j > qw + 16 * qs + li) d[j] = 0.f;
-        }
-        pk[ks][0] = pack2_f16(d[0], d[1]);
-        pk[ks][1] = pack2_f16(d[2], d[3]);
-      }
-#pragma unroll
-      for (int kk2 = 0; kk2 < 2; ++kk2) {
-        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-        u32x4 uu = {pk[2 * kk2][0], pk[2 * kk2][1], pk[2 * kk2 + 1][0], pk[2 * kk2 + 1][1]};
-        dsf[qs][kk2] = __builtin_bit_cast(i16x8, uu);
-      }
+      s_[qs] = cb;
+      p_[qs] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 #pragma unroll
-    for (int ds = 0; ds < DS; ds += 2) {
-      i16x8 kt[2][2];
+    for (int kk = 0; kk < KK; ++kk) {
+      const i16x8 kf = lds16(ks_ + soff<D>(hr + li, 32 * kk + 8 * g));
+      const i16x8 vf = lds16(vs_ + soff<D>(hr + li, 32 * kk + 8 * g));
 #pragma unroll
-      for (int dd = 0; dd < 2; ++dd)
-#pragma unroll
-        for (int kk2 = 0; kk2 < 2; ++kk2)
-          kt[dd][kk2] = frag_to_f16<T>(lds_frag_tr(ks_, LD, 32 * kk2, 16 * (ds + dd), g, li));
-#pragma unroll
-      for (int kk2 = 0; kk2 < 2; ++kk2)
-#pragma unroll
-        for (int dd = 0; dd < 2; ++dd)
-#pragma unroll
-          for (int qs = 0; qs < 2; ++qs)
-            dqacc[ds + dd][qs] = mma_f16(kt[dd][kk2], dsf[qs][kk2], dqacc[ds + dd][qs]);
+      for (int qs = 0; qs < 2; ++qs) {
+        s_[qs] = mma_f16(kf, qf[qs][kk], s_[qs]);
+        p_[qs] = M::mma(vf, dof[qs][kk], p_[qs]);
+      }
     }
   };
+  // dS of those scores, packed fp16 as dS^T
+  auto vh = [&](auto mask_tag, int kh, const f32x4 (&s_)[2], const f32x4 (&p_)[2], uint32_t (&pk)[2][2]) {
+    constexpr bool MASK = decltype(mask_tag)::value;
+#pragma unroll
+    for (int qs = 0; qs < 2; ++qs) {
+      const float tterm = slope * (float)(kh - qw - 16 * qs);
+      float d[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float s = fmaf(s_[qs][j], scale, tterm);
+        const float r = __builtin_amdgcn_rcpf(fabsf(s) + 1.f);
+        const float t = fmaf(s, r, 1.f);
+        const float u = t * r;
+        d[j] = (u * u * t) * fmaf(p_[qs][j], c4[qs], nc4d[qs]);
+        if (MASK && kh + 4 * g + j > qw + 16 * qs + li) d[j] = 0.f;
+      }
+      pk[qs][0] = pack2_f16(d[0], d[1]);
+      pk[qs][1] = pack2_f16(d[2], d[3]);
+    }
+  };
+  // dQ^T += K16^T dS^T over the 32 keys at tile rows r0 .. r0 + 31
+  auto m2 = [&](int r0, const uint32_t (&pa)[2][2], const uint32_t (&pb)[2][2], const short* ks_) {
+    i16x8 dsf[2];
+#pragma unroll
+    for (int qs = 0; qs < 2; ++qs) dsf[qs] = pack_frag(pa[qs][0], pa[qs][1], pb[qs][0], pb[qs][1]);
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds) {
+      const i16x8 kt = frag_tr<D>(ks_, r0, 16 * ds, g, li);
+#pragma unroll
+      for (int qs = 0; qs < 2; ++qs) dqacc[ds][qs] = mma_f16(kt, dsf[qs], dqacc[ds][qs]);
+    }
+  };
+  auto tile = [&](auto mask_tag, int k0, const short* ks_, const short* vs_) {
+    f32x4 sA[2], pA[2], sB[2], pB[2];
+    uint32_t da0[2][2], db0[2][2], da1[2][2], db1[2][2];
+    m1(0, sA, pA, ks_, vs_);
+    m1(16, sB, pB, ks_, vs_);
+    vh(mask_tag, k0, sA, pA, da0);
+    m1(32, sA, pA, ks_, vs_);
+    vh(mask_tag, k0 + 16, sB, pB, db0);
+    m2(0, da0, db0, ks_);
+    m1(48, sB, pB, ks_, vs_);
+    vh(mask_tag, k0 + 32, sA, pA, da1);
+    vh(mask_tag, k0 + 48, sB, pB, db1);
+    m2(32, da1, db1, ks_);
+  };
 
-  const int kend = std::min(q0 + FBM, T_);
-  const int n_kt = (kend + FBN - 1) / FBN;
-  KvStager<T, D> stg;
-  stg.load(kp, a.sk[2], vp, a.sv[2], 0, T_, tid);
-  stg.store(sm, 0, tid);
+  const int n_kt = (std::min(q0 + kBM, T_) + kBN - 1) / kBN;
+  dk.issue(sk[0], kp, kbytes, 0, D, w);
+  dv.issue(sv[0], vp, vbytes, 0, sv2, w);
+  dma_wait();
   __syncthreads();
   for (int kt = 0; kt < n_kt; ++kt) {
     const int buf = kt & 1;
-    const bool more = kt + 1 < n_kt;
-    if (more) stg.load(kp, a.sk[2], vp, a.sv[2], (kt + 1) * FBN, T_, tid);
-    const int k0 = kt * FBN;
-    if (k0 + FBN - 1 <= qw)
-      tile(std::false_type{}, k0, sm.k[buf], sm.v[buf]);
-    else if (k0 <= qw + 31)
-      tile(std::true_type{}, k0, sm.k[buf], sm.v[buf]);
-    if (more) stg.store(sm, buf ^ 1, tid);
+    if (kt + 1 < n_kt) {
+      dk.issue(sk[buf ^ 1], kp, kbytes, (kt + 1) * kBN, D, w);
+      dv.issue(sv[buf ^ 1], vp, vbytes, (kt + 1) * kBN, sv2, w);
+    }
+    const int k0 = kt * kBN;
+    if (k0 + kBN - 1 <= qw)
+      tile(std::false_type{}, k0, sk[buf], sv[buf]);
+    else if (k0 <= qw + kRows - 1)
+      tile(std::true_type{}, k0, sk[buf], sv[buf]);
+    dma_wait();
     __syncthreads();
   }
 
@@ -515,80 +406,70 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_mfma_k(AttnArgs a,
       T* row = dqp + (int64_t)qrow * a.sdq[2];
 #pragma unroll
       for (int ds = 0; ds < DS; ++ds) {
-        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
         const f32x4 o = dqacc[ds][qs];
-        u32x2 uu = {M::pack2(o[0] * scale, o[1] * scale), M::pack2(o[2] * scale, o[3] * scale)};
-        *reinterpret_cast<u32x2*>(row + 16 * ds + 4 * g) = uu;
+        *reinterpret_cast<u32x2*>(row + 16 * ds + 4 * g) =
+            u32x2{M::pack2(o[0] * scale, o[1] * scale), M::pack2(o[2] * scale, o[3] * scale)};
       }
     }
   }
 }
 
-// dK, dV: 128 keys per block (4 waves x 32 keys); 64-query Q / dO tiles in LDS,
-// processed in two 32-query halves.
-//   S  = Q K^T (+bias)    A = Q  (LDS, b128)               B = K^T (VGPRs)
-//   dP = dO V^T           A = dO (LDS, b128)               B = V^T (VGPRs)
-//   dV^T += dO^T P        A = dO^T (LDS, transposing read) B = P  (registers)
-//   dK^T += Q^T dS        A = Q^T  (LDS, transposing read) B = dS (registers)
-constexpr int KBN = 128;  // keys per block
-constexpr int KBQ = 64;   // queries per LDS tile
-
-template <int D> struct DkvSmem {
-  static constexpr int LD = D + 16;
-  short q[2][KBQ * LD];
-  short o[2][KBQ * LD];  // dO
-  float c4[2][KBQ];      // 4 cinv_q
-  float nc4d[2][KBQ];    // -4 cinv_q Delta_q
-};
-
+// ============================================================================
+// dK, dV: 128 keys per block (4 waves x 32 keys, one block per CU: the K / V
+// fragments and the dK / dV accumulators of 32 keys take ~200 VGPRs); 64-query
+// Q16 / dO tiles and their stats stream through LDS.
+//   S  = Q16 K16^T (+bias)   A = Q16 (LDS rows)          B = K16^T (VGPRs)
+//   dP = dO V^T              A = dO  (LDS rows)          B = V^T   (VGPRs)
+//   dV^T += dO^T P           A = dO^T (LDS transposed)   B = P     (from S)
+//   dK^T += Q16^T dS         A = Q16^T (LDS transposed)  B = dS    (from S, dP)
+// ============================================================================
 template <typename T, int D>
-__global__ __launch_bounds__(256) void attn_bwd_dkv_mfma_k(AttnArgs a,
-                                                          const float* __restrict__ delta,
-                                                          const float* __restrict__ cinv) {
+__global__ __launch_bounds__(256, 1) void attn_bwd_dkv_k(AttnArgs a, const float2* __restrict__ stats,
+                                                         const f16* __restrict__ q16) {
   typedef Mfma<T> M;
-  constexpr int LD = DkvSmem<D>::LD;
   constexpr int KK = D / 32;
   constexpr int DS = D / 16;
-  constexpr int CPR = D / 8;
-  constexpr int LOADS = KBQ * CPR / 256;
-  __shared__ DkvSmem<D> sm;
+  __shared__ short sq[2][kBN * D];
+  __shared__ short so[2][kBN * D];
+  __shared__ float2 sst[2][kBN];
 
   const int T_ = a.T, H = a.H;
-  const int n_kb = (T_ + KBN - 1) / KBN;
-  int bh, kb;
-  block_order((int)blockIdx.x, n_kb, a.B * H, bh, kb);  // kb 0 has the most query tiles
+  int bh, rank;
+  block_order((int)blockIdx.x, a.B * H, bh, rank);  // rank 0: the first keys (most queries)
+  const int k0 = rank * kBM;
   const int b = bh / H, h = bh - b * H;
-  const int k0 = kb * KBN;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 4, li = lane & 15;
-  const int kw = k0 + 32 * w;
+  const int kw = k0 + kRows * w;
 
-  const T* __restrict__ qp = (const T*)a.q + b * a.sq[0] + h * a.sq[1];
-  const T* __restrict__ kp = (const T*)a.k + b * a.sk[0] + h * a.sk[1];
-  const T* __restrict__ vp = (const T*)a.v + b * a.sv[0] + h * a.sv[1];
-  const T* __restrict__ dop = (const T*)a.dout + b * a.sdo[0] + h * a.sdo[1];
-  const float* __restrict__ dl = delta + (int64_t)bh * T_;
-  const float* __restrict__ ci = cinv + (int64_t)bh * T_;
+  const f16* qp = q16 + (int64_t)bh * T_ * D;
+  const T* kp = (const T*)a.k + b * a.sk[0] + h * a.sk[1];
+  const T* vp = (const T*)a.v + b * a.sv[0] + h * a.sv[1];
+  const T* dop = (const T*)a.dout + b * a.sdo[0] + h * a.sdo[1];
+  const float2* stp = stats + (int64_t)bh * T_;
+  const uint32_t sk2 = (uint32_t)a.sk[2], sv2 = (uint32_t)a.sv[2], sdo2 = (uint32_t)a.sdo[2];
+  const uint32_t qbytes = row_bytes(T_, D, D), obytes = row_bytes(T_, sdo2, D);
+  const uint32_t stbytes = (uint32_t)T_ * 8u;
   const float slope = a.slopes[h];
   const float scale = a.scale;
 
-  // K^T / V^T fragments (B operands): lane (g, li) holds row kw + 16 ks + li,
+  // K16^T / V^T fragments (B operands): lane (g, li) holds row kw + 16 ks + li,
   // columns 32 kk + 8 g .. +7
   i16x8 kf[2][KK], vf[2][KK];
+  {
+    const __amdgpu_buffer_rsrc_t rk = rsrc(kp, row_bytes(T_, sk2, D));
+    const __amdgpu_buffer_rsrc_t rv = rsrc(vp, row_bytes(T_, sv2, D));
 #pragma unroll
-  for (int ks = 0; ks < 2; ++ks) {
-    const int key = kw + 16 * ks + li;
-    const bool ok = key < T_;
+    for (int ks = 0; ks < 2; ++ks) {
+      const uint32_t key = (uint32_t)(kw + 16 * ks + li);
 #pragma unroll
-    for (int kk = 0; kk < KK; ++kk) {
-      kf[ks][kk] = ok ? *reinterpret_cast<const i16x8*>(kp + (int64_t)key * a.sk[2] + 32 * kk + 8 * g)
-                      : i16x8{0, 0, 0, 0, 0, 0, 0, 0};
-      vf[ks][kk] = ok ? *reinterpret_cast<const i16x8*>(vp + (int64_t)key * a.sv[2] + 32 * kk + 8 * g)
-                      : i16x8{0, 0, 0, 0, 0, 0, 0, 0};
+      for (int kk = 0; kk < KK; ++kk) {
+        kf[ks][kk] = to_f16x8<T>(load16(rk, (key * sk2 + 32 * kk + 8 * g) * 2));
+        vf[ks][kk] = load16(rv, (key * sv2 + 32 * kk + 8 * g) * 2);
+      }
     }
   }
-  // S layout: lane (g, li) element j holds q = qh + 16 qs + 4 g + j,
-  // key = kw + 16 ks + li; bias slope * (key - q) = per-lane part + uniform part
+  // S layout: lane (g, li) element j holds q = qh + 4 g + j, key = kw + 16 ks + li
   f32x4 cb;
 #pragma unroll
   for (int j = 0; j < 4; ++j) cb[j] = (slope / scale) * (float)(li - 4 * g - j);
@@ -602,155 +483,119 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_mfma_k(AttnArgs a,
       dvacc[ds][ks] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
-  // one 32-query half (queries qh .. qh + 31) of the LDS tile; MASK: some
-  // pair of the half has key > q
-  auto half = [&](auto mask_tag, int qh, int r0, const short* qs_, const short* os_,
-                  const float* c4s, const float* nds) {
-    constexpr bool MASK = decltype(mask_tag)::value;
-    f32x4 sacc[2][2], pacc[2][2];
+  TileDma<D, kNW> dq_, do_;
+  dq_.init(w, lane, D);
+  do_.init(w, lane, sdo2);
+  // stats of a 64-query tile: 512 bytes, lanes 0..31 of wave 0
+  const uint32_t st_off = (uint32_t)lane * 16u;
+  auto issue = [&](int buf, int qrow0) {
+    dq_.issue(sq[buf], qp, qbytes, qrow0, D, w);
+    do_.issue(so[buf], dop, obytes, qrow0, sdo2, w);
+    if (w == 0 && lane < 32) {
+      const uint32_t skip = (uint32_t)qrow0 * 8u;
+      dma16(rsrc_words((const char*)stp + skip, stbytes > skip ? stbytes - skip : 0u), sst[buf], st_off);
+    }
+  };
+
+  // S and dP of the 16 queries at tile rows hr .. hr + 15
+  auto m1 = [&](int hr, f32x4 (&s_)[2], f32x4 (&p_)[2], const short* qs_, const short* os_) {
 #pragma unroll
-    for (int qs = 0; qs < 2; ++qs)
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        sacc[qs][ks] = cb;
-        pacc[qs][ks] = f32x4{0.f, 0.f, 0.f, 0.f};
-      }
+    for (int ks = 0; ks < 2; ++ks) {
+      s_[ks] = cb;
+      p_[ks] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {
-      i16x8 qa[2], oa[2];
-#pragma unroll
-      for (int qs = 0; qs < 2; ++qs) {
-        const int row = r0 + 16 * qs + li;
-        qa[qs] = lds_read16(qs_ + row * LD + 32 * kk + 8 * g);
-        oa[qs] = lds_read16(os_ + row * LD + 32 * kk + 8 * g);
-      }
-#pragma unroll
-      for (int qs = 0; qs < 2; ++qs)
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          sacc[qs][ks] = M::mma(qa[qs], kf[ks][kk], sacc[qs][ks]);
-          pacc[qs][ks] = M::mma(oa[qs], vf[ks][kk], pacc[qs][ks]);
-        }
-    }
-    uint32_t ppk[2][2][2], dpk[2][2][2];  // [ks][qs][pair]
-#pragma unroll
-    for (int qs = 0; qs < 2; ++qs) {
-      const f32x4 c4v = *reinterpret_cast<const f32x4*>(c4s + r0 + 16 * qs + 4 * g);
-      const f32x4 ndv = *reinterpret_cast<const f32x4*>(nds + r0 + 16 * qs + 4 * g);
+      const i16x8 qa = lds16(qs_ + soff<D>(hr + li, 32 * kk + 8 * g));
+      const i16x8 oa = lds16(os_ + soff<D>(hr + li, 32 * kk + 8 * g));
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        const float tterm = slope * (float)(kw + 16 * ks - qh - 16 * qs);
-        float pv[4], dv[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float s = fmaf(sacc[qs][ks][j], scale, tterm);
-          const float r = __builtin_amdgcn_rcpf(fabsf(s) + 1.f);
-          const float t = fmaf(s, r, 1.f);
-          const float t2 = t * t;
-          const float u = t * r;
-          pv[j] = (t2 * t2) * (0.25f * c4v[j]);
-          dv[j] = (u * u * t) * fmaf(pacc[qs][ks][j], c4v[j], ndv[j]);
-          if (MASK && kw + 16 * ks + li > qh + 16 * qs + 4 * g + j) {
-            pv[j] = 0.f;
-            dv[j] = 0.f;
-          }
-        }
-        ppk[ks][qs][0] = M::pack2(pv[0], pv[1]);
-        ppk[ks][qs][1] = M::pack2(pv[2], pv[3]);
-        dpk[ks][qs][0] = pack2_f16(dv[0], dv[1]);
-        dpk[ks][qs][1] = pack2_f16(dv[2], dv[3]);
+        s_[ks] = mma_f16(qa, kf[ks][kk], s_[ks]);
+        p_[ks] = M::mma(oa, vf[ks][kk], p_[ks]);
       }
     }
+  };
+  // P (input dtype) and dS (fp16) of those scores
+  auto vh = [&](auto mask_tag, int qh, int hr, const f32x4 (&s_)[2], const f32x4 (&p_)[2],
+                const float2* st_, uint32_t (&pp)[2][2], uint32_t (&dp)[2][2]) {
+    constexpr bool MASK = decltype(mask_tag)::value;
+    const f32x4 s01 = *reinterpret_cast<const f32x4*>(st_ + hr + 4 * g);
+    const f32x4 s23 = *reinterpret_cast<const f32x4*>(st_ + hr + 4 * g + 2);
+    const float c4v[4] = {s01[0], s01[2], s23[0], s23[2]};
+    const float ndv[4] = {s01[1], s01[3], s23[1], s23[3]};
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const float tterm = slope * (float)(kw + 16 * ks - qh);
+      float pv[4], dv[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float s = fmaf(s_[ks][j], scale, tterm);
+        const float r = __builtin_amdgcn_rcpf(fabsf(s) + 1.f);
+        const float t = fmaf(s, r, 1.f);
+        const float t2 = t * t;
+        const float u = t * r;
+        pv[j] = (t2 * t2) * (0.25f * c4v[j]);
+        dv[j] = (u * u * t) * fmaf(p_[ks][j], c4v[j], ndv[j]);
+        if (MASK && kw + 16 * ks + li > qh + 4 * g + j) {
+          pv[j] = 0.f;
+          dv[j] = 0.f;
+        }
+      }
+      pp[ks][0] = M::pack2(pv[0], pv[1]);
+      pp[ks][1] = M::pack2(pv[2], pv[3]);
+      dp[ks][0] = pack2_f16(dv[0], dv[1]);
+      dp[ks][1] = pack2_f16(dv[2], dv[3]);
+    }
+  };
+  // dV^T += dO^T P and dK^T += Q16^T dS over the 32 queries at tile rows r0 .. r0 + 31
+  auto m2 = [&](int r0, const uint32_t (&pa)[2][2], const uint32_t (&pb)[2][2],
+                const uint32_t (&da)[2][2], const uint32_t (&db)[2][2], const short* qs_,
+                const short* os_) {
     i16x8 pf[2], dsf[2];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-      u32x4 u1 = {ppk[ks][0][0], ppk[ks][0][1], ppk[ks][1][0], ppk[ks][1][1]};
-      u32x4 u2 = {dpk[ks][0][0], dpk[ks][0][1], dpk[ks][1][0], dpk[ks][1][1]};
-      pf[ks] = __builtin_bit_cast(i16x8, u1);
-      dsf[ks] = __builtin_bit_cast(i16x8, u2);
+      pf[ks] = pack_frag(pa[ks][0], pa[ks][1], pb[ks][0], pb[ks][1]);
+      dsf[ks] = pack_frag(da[ks][0], da[ks][1], db[ks][0], db[ks][1]);
     }
 #pragma unroll
     for (int ds = 0; ds < DS; ++ds) {
-      const i16x8 ot = lds_frag_tr(os_, LD, r0, 16 * ds, g, li);
-      const i16x8 qtr = frag_to_f16<T>(lds_frag_tr(qs_, LD, r0, 16 * ds, g, li));
+      const i16x8 ot = frag_tr<D>(os_, r0, 16 * ds, g, li);
+      const i16x8 qt = frag_tr<D>(qs_, r0, 16 * ds, g, li);
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         dvacc[ds][ks] = M::mma(ot, pf[ks], dvacc[ds][ks]);
-        dkacc[ds][ks] = mma_f16(qtr, dsf[ks], dkacc[ds][ks]);
+        dkacc[ds][ks] = mma_f16(qt, dsf[ks], dkacc[ds][ks]);
       }
     }
   };
-
-  const int qstart = k0;  // causal: queries >= first key of the block
-  const int n_qt = qstart < T_ ? (T_ - qstart + KBQ - 1) / KBQ : 0;
-  i16x8 qst[LOADS], ost[LOADS];
-  float cst = 0.f, dst = 0.f;
-  auto load_tile = [&](int it) {
-    const int q0 = qstart + it * KBQ;
-#pragma unroll
-    for (int u = 0; u < LOADS; ++u) {
-      const int c = tid + 256 * u;
-      const int row = c / CPR, col = (c % CPR) * 8;
-      const int qr = q0 + row;
-      if (qr < T_) {
-        qst[u] = *reinterpret_cast<const i16x8*>(qp + (int64_t)qr * a.sq[2] + col);
-        ost[u] = *reinterpret_cast<const i16x8*>(dop + (int64_t)qr * a.sdo[2] + col);
-      } else {
-        qst[u] = i16x8{0, 0, 0, 0, 0, 0, 0, 0};
-        ost[u] = i16x8{0, 0, 0, 0, 0, 0, 0, 0};
-      }
-    }
-    if (tid < KBQ) {
-      const int qr = q0 + tid;
-      const float c = qr < T_ ? 4.f * ci[qr] : 0.f;
-      cst = c;
-      dst = qr < T_ ? -c * dl[qr] : 0.f;
-    }
-  };
-  auto store_tile = [&](int buf) {
-#pragma unroll
-    for (int u = 0; u < LOADS; ++u) {
-      const int c = tid + 256 * u;
-      const int row = c / CPR, col = (c % CPR) * 8;
-      *reinterpret_cast<i16x8*>(&sm.q[buf][row * LD + col]) = qst[u];
-      *reinterpret_cast<i16x8*>(&sm.o[buf][row * LD + col]) = ost[u];
-    }
-    if (tid < KBQ) {
-      sm.c4[buf][tid] = cst;
-      sm.nc4d[buf][tid] = dst;
-    }
+  // 32 queries starting at qc (tile rows r0 .. r0 + 31)
+  auto chunk = [&](auto mask_tag, int qc, int r0, const short* qs_, const short* os_, const float2* st_) {
+    f32x4 sA[2], pA[2], sB[2], pB[2];
+    uint32_t pa[2][2], pb[2][2], da[2][2], db[2][2];
+    m1(r0, sA, pA, qs_, os_);
+    m1(r0 + 16, sB, pB, qs_, os_);
+    vh(mask_tag, qc, r0, sA, pA, st_, pa, da);
+    vh(mask_tag, qc + 16, r0 + 16, sB, pB, st_, pb, db);
+    m2(r0, pa, pb, da, db, qs_, os_);
   };
 
-  if (n_qt > 0) {
-    load_tile(0);
-    store_tile(0);
-  }
+  const int n_it = k0 < T_ ? (T_ - k0 + kBN - 1) / kBN : 0;  // causal: queries >= k0
+  if (n_it > 0) issue(0, k0);
+  dma_wait();
   __syncthreads();
-  for (int it = 0; it < n_qt; ++it) {
+  for (int it = 0; it < n_it; ++it) {
     const int buf = it & 1;
-    const bool more = it + 1 < n_qt;
-    if (more) load_tile(it + 1);
-    const int q0 = qstart + it * KBQ;
-    const short* qs_ = sm.q[buf];
-    const short* os_ = sm.o[buf];
-    const float* c4s = sm.c4[buf];
-    const float* nds = sm.nc4d[buf];
-    if (q0 >= kw + 31) {  // every pair of the tile has key <= q
-      half(std::false_type{}, q0, 0, qs_, os_, c4s, nds);
-      half(std::false_type{}, q0 + 32, 32, qs_, os_, c4s, nds);
-    } else {
+    if (it + 1 < n_it) issue(buf ^ 1, k0 + (it + 1) * kBN);
+    const int q0 = k0 + it * kBN;
 #pragma unroll
-      for (int h2 = 0; h2 < 2; ++h2) {
-        const int qh = q0 + 32 * h2;
-        if (qh + 31 < kw) continue;  // every pair of the half has key > q
-        if (qh >= kw + 31)
-          half(std::false_type{}, qh, 32 * h2, qs_, os_, c4s, nds);
-        else
-          half(std::true_type{}, qh, 32 * h2, qs_, os_, c4s, nds);
-      }
+    for (int c = 0; c < 2; ++c) {
+      const int qc = q0 + 32 * c;
+      if (qc >= kw + kRows - 1)
+        chunk(std::false_type{}, qc, 32 * c, sq[buf], so[buf], sst[buf]);
+      else if (qc + 31 >= kw)
+        chunk(std::true_type{}, qc, 32 * c, sq[buf], so[buf], sst[buf]);
     }
-    if (more) store_tile(buf ^ 1);
+    dma_wait();
     __syncthreads();
   }
 
@@ -764,56 +609,83 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_mfma_k(AttnArgs a,
       T* rv = dvp + (int64_t)key * a.sdv[2];
 #pragma unroll
       for (int ds = 0; ds < DS; ++ds) {
-        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
         const f32x4 kq = dkacc[ds][ks];
         const f32x4 vq = dvacc[ds][ks];
-        u32x2 uk = {M::pack2(kq[0] * scale, kq[1] * scale), M::pack2(kq[2] * scale, kq[3] * scale)};
-        u32x2 uv = {M::pack2(vq[0], vq[1]), M::pack2(vq[2], vq[3])};
-        *reinterpret_cast<u32x2*>(rk + 16 * ds + 4 * g) = uk;
-        *reinterpret_cast<u32x2*>(rv + 16 * ds + 4 * g) = uv;
+        *reinterpret_cast<u32x2*>(rk + 16 * ds + 4 * g) =
+            u32x2{M::pack2(kq[0] * scale, kq[1] * scale), M::pack2(kq[2] * scale, kq[3] * scale)};
+        *reinterpret_cast<u32x2*>(rv + 16 * ds + 4 * g) = u32x2{M::pack2(vq[0], vq[1]), M::pack2(vq[2], vq[3])};
       }
     }
   }
 }
 
+// ============================================================================
+// Launchers
+// ============================================================================
 bool attn_mfma_supported(int D) { return D == 64 || D == 128; }
 
-template <typename T> int attn_fwd_mfma(const AttnArgs& a, hipStream_t st) {
-  const int64_t nb = (int64_t)((a.T + FBM - 1) / FBM) * a.B * a.H;
-  if (nb > 0x7fffffffLL) return KAT_EUNSUPPORTED;
-  dim3 grid((unsigned)nb);
-  if (a.D == 128)
-    hipLaunchKernelGGL((attn_fwd_mfma_k<T, 128>), grid, dim3(256), 0, st, a);
-  else if (a.D == 64)
-    hipLaunchKernelGGL((attn_fwd_mfma_k<T, 64>), grid, dim3(256), 0, st, a);
-  else
-    return KAT_EUNSUPPORTED;
+size_t attn_mfma_workspace(int64_t B, int64_t H, int64_t T, int64_t D) {
+  const size_t rows = (size_t)(B * H * T);
+  auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
+  return al(rows * sizeof(float2)) + 2 * al(rows * (size_t)D * sizeof(f16));
+}
+
+namespace {
+
+// every tensor the kernels read through a buffer resource (q, k, v, and dO in
+// the backward) must fit 31-bit byte offsets per (b, h) slice and have
+// non-overlapping rows
+bool offsets_ok(const AttnArgs& a, bool bwd) {
+  const int64_t lim = 0x7fffffffLL;
+  const int64_t* s2[4] = {&a.sq[2], &a.sk[2], &a.sv[2], &a.sdo[2]};
+  for (int t = 0; t < (bwd ? 4 : 3); ++t)
+    if (*s2[t] < a.D || ((int64_t)a.T + kBM) * *s2[t] * 2 > lim) return false;
+  return (int64_t)a.T * a.D * 2 < lim && (int64_t)a.T * 8 < lim;
+}
+
+template <typename T, int D> int launch_fwd(const AttnArgs& a, hipStream_t st) {
+  const int64_t nb = (int64_t)((a.T + kBM - 1) / kBM) * a.B * a.H;
+  hipLaunchKernelGGL((attn_fwd_k<T, D>), dim3((unsigned)nb), dim3(256), 0, st, a);
   return check_launch("kat_attn_fwd (mfma)");
 }
 
-template <typename T>
-int attn_bwd_mfma(const AttnArgs& a, const float* delta, const float* cinv, hipStream_t st) {
-  const int64_t nk = (int64_t)((a.T + KBN - 1) / KBN) * a.B * a.H;
-  const int64_t nq = (int64_t)((a.T + FBM - 1) / FBM) * a.B * a.H;
-  if (nk > 0x7fffffffLL || nq > 0x7fffffffLL) return KAT_EUNSUPPORTED;
-  dim3 gk((unsigned)nk), gq((unsigned)nq);
-  if (a.D == 128) {
-    hipLaunchKernelGGL((attn_bwd_dkv_mfma_k<T, 128>), gk, dim3(256), 0, st, a, delta, cinv);
-    if (int rc = check_launch("kat_attn_bwd (dkv, mfma)")) return rc;
-    hipLaunchKernelGGL((attn_bwd_dq_mfma_k<T, 128>), gq, dim3(256), 0, st, a, delta, cinv);
-  } else if (a.D == 64) {
-    hipLaunchKernelGGL((attn_bwd_dkv_mfma_k<T, 64>), gk, dim3(256), 0, st, a, delta, cinv);
-    if (int rc = check_launch("kat_attn_bwd (dkv, mfma)")) return rc;
-    hipLaunchKernelGGL((attn_bwd_dq_mfma_k<T, 64>), gq, dim3(256), 0, st, a, delta, cinv);
-  } else {
-    return KAT_EUNSUPPORTED;
-  }
+template <typename T, int D>
+int launch_bwd(const AttnArgs& a, void* ws, hipStream_t st) {
+  const int64_t rows = (int64_t)a.B * a.H * a.T;
+  auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
+  float2* stats = reinterpret_cast<float2*>(ws);
+  f16* q16 = reinterpret_cast<f16*>(reinterpret_cast<char*>(ws) + al(rows * sizeof(float2)));
+  f16* k16 = reinterpret_cast<f16*>(reinterpret_cast<char*>(q16) + al(rows * D * sizeof(f16)));
+  constexpr int rpb = 256 / (D / 8);
+  hipLaunchKernelGGL((attn_bwd_prep_k<T, D>), dim3((unsigned)((rows + rpb - 1) / rpb)), dim3(256), 0, st, a,
+                     stats, q16, k16);
+  if (int rc = check_launch("kat_attn_bwd (prep)")) return rc;
+  const int64_t nt = (int64_t)((a.T + kBM - 1) / kBM) * a.B * a.H;
+  hipLaunchKernelGGL((attn_bwd_dkv_k<T, D>), dim3((unsigned)nt), dim3(256), 0, st, a, stats, q16);
+  if (int rc = check_launch("kat_attn_bwd (dkv, mfma)")) return rc;
+  hipLaunchKernelGGL((attn_bwd_dq_k<T, D>), dim3((unsigned)nt), dim3(256), 0, st, a, stats, k16);
   return check_launch("kat_attn_bwd (dq, mfma)");
+}
+
+}  // namespace
+
+template <typename T> int attn_fwd_mfma(const AttnArgs& a, hipStream_t st) {
+  if ((int64_t)((a.T + kBM - 1) / kBM) * a.B * a.H > 0x7fffffffLL || !offsets_ok(a, false)) return KAT_EUNSUPPORTED;
+  if (a.D == 128) return launch_fwd<T, 128>(a, st);
+  if (a.D == 64) return launch_fwd<T, 64>(a, st);
+  return KAT_EUNSUPPORTED;
+}
+
+template <typename T> int attn_bwd_mfma(const AttnArgs& a, void* ws, hipStream_t st) {
+  if ((int64_t)((a.T + kBM - 1) / kBM) * a.B * a.H > 0x7fffffffLL || !offsets_ok(a, true)) return KAT_EUNSUPPORTED;
+  if (a.D == 128) return launch_bwd<T, 128>(a, ws, st);
+  if (a.D == 64) return launch_bwd<T, 64>(a, ws, st);
+  return KAT_EUNSUPPORTED;
 }
 
 template int attn_fwd_mfma<bf16>(const AttnArgs&, hipStream_t);
 template int attn_fwd_mfma<f16>(const AttnArgs&, hipStream_t);
-template int attn_bwd_mfma<bf16>(const AttnArgs&, const float*, const float*, hipStream_t);
-template int attn_bwd_mfma<f16>(const AttnArgs&, const float*, const float*, hipStream_t);
+template int attn_bwd_mfma<bf16>(const AttnArgs&, void*, hipStream_t);
+template int attn_bwd_mfma<f16>(const AttnArgs&, void*, hipStream_t);
 
 }  // namespace kat

@@ -1,0 +1,199 @@
+// Device building blocks of the gfx950 (CDNA4) MFMA attention kernels:
+// MFMA wrappers, LDS fragment reads, LDS-DMA tile staging, block ordering.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "kat_common.h"
+
+namespace kat {
+namespace mfma {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+// v_mfma_f32_16x16x32_{bf16,f16}. Operand layout (lane l, g = l / 16, li = l % 16):
+// A[m = li][k-set g], B[k-set g][n = li], C[4 g + j][li] (j = 0..3). A and B only
+// have to agree on which 8 k-indices form k-set g.
+template <typename T> struct Mfma;
+template <> struct Mfma<bf16> {
+  static __device__ __forceinline__ f32x4 mma(const i16x8& a, const i16x8& b, const f32x4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16((bf16x8)a, (bf16x8)b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint32_t pack2(float x, float y) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{x, y}), bf16x2));
+  }
+};
+template <> struct Mfma<f16> {
+  static __device__ __forceinline__ f32x4 mma(const i16x8& a, const i16x8& b, const f32x4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16((f16x8)a, (f16x8)b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint32_t pack2(float x, float y) {
+    typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{x, y}), f16x2));
+  }
+};
+
+// fp16 operands for the dS products: dS = p g (dP - Delta) is rounded to fp16
+// (11-bit significand) rather than bf16 before dQ = dS K and dK = dS^T Q, so its
+// rounding error is 4x smaller. K and Q enter those products (and S itself) as
+// fp16 copies; bf16 -> fp16 is exact for |x| in [2^-14, 65504], magnitudes
+// above 65504 are clamped and smaller ones keep fp16's subnormal spacing 2^-24.
+__device__ __forceinline__ f32x4 mma_f16(const i16x8& a, const i16x8& b, const f32x4& c) {
+  return Mfma<f16>::mma(a, b, c);
+}
+__device__ __forceinline__ uint32_t pack2_f16(float x, float y) { return Mfma<f16>::pack2(x, y); }
+
+template <typename T> __device__ __forceinline__ i16x8 to_f16x8(const i16x8& v);
+template <> __device__ __forceinline__ i16x8 to_f16x8<f16>(const i16x8& v) { return v; }
+template <> __device__ __forceinline__ i16x8 to_f16x8<bf16>(const i16x8& v) {
+  const u32x4 w = __builtin_bit_cast(u32x4, v);
+  u32x4 o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float lo = __builtin_bit_cast(float, w[e] << 16);
+    const float hi = __builtin_bit_cast(float, w[e] & 0xffff0000u);
+    o[e] = pack2_f16(fminf(fmaxf(lo, -65504.f), 65504.f), fminf(fmaxf(hi, -65504.f), 65504.f));
+  }
+  return __builtin_bit_cast(i16x8, o);
+}
+
+__device__ __forceinline__ i16x8 pack_frag(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  return __builtin_bit_cast(i16x8, (u32x4{a, b, c, d}));
+}
+
+// ---------------------------------------------------------------------------
+// Buffer resources. Loads through a raw buffer resource (stride 0) return zero
+// for bytes at or beyond num_records, which zero-fills rows past the sequence
+// end without branches.
+// ---------------------------------------------------------------------------
+constexpr int kRsrcWord3 = 0x00020000;  // gfx9 raw buffer: 32-bit data format
+
+// resource for kernel-side loads through the compiler builtin
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, kRsrcWord3);
+}
+__device__ __forceinline__ i16x8 load16(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
+  return __builtin_bit_cast(i16x8, __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0));
+}
+
+// resource as four SGPRs, for the LDS-DMA below
+__device__ __forceinline__ i32x4 rsrc_words(const void* base, uint32_t bytes) {
+  const uint64_t p = (uint64_t)base;
+  i32x4 r;
+  r[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)p);
+  r[1] = __builtin_amdgcn_readfirstlane((int)((uint32_t)(p >> 32) & 0xffffu));
+  r[2] = __builtin_amdgcn_readfirstlane((int)bytes);
+  r[3] = kRsrcWord3;
+  return r;
+}
+
+// LDS-DMA: every active lane l copies 16 bytes at buffer offset voff into LDS at
+// lds + 16 l (buffer_load_dwordx4 ... lds, M0 = LDS base). Issued through inline
+// asm so that the compiler adds no wait for it before unrelated LDS reads; the
+// kernel waits with dma_wait() before the barrier that publishes the tile.
+// dma_wait() is the s_waitcnt builtin (vmcnt(0), expcnt and lgkmcnt left at
+// their maxima: 0x0F70 in the gfx9 encoding) rather than asm, so the compiler's
+// wait tracking also sees every earlier vector-memory load as complete.
+__device__ __forceinline__ void dma16(const i32x4& r, const void* lds, uint32_t voff) {
+  const uint32_t la = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)(lds));
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(la), "v"(voff),
+               "s"(r)
+               : "memory");
+}
+__device__ __forceinline__ void dma_wait() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// ---------------------------------------------------------------------------
+// LDS tiles: rows of D 16-bit elements, 16-byte chunks XOR-swizzled by row so
+// that the row-fragment reads (16 rows, one chunk) and the transposing reads (8
+// rows, two chunks per 32 lanes) touch distinct bank groups.
+// ---------------------------------------------------------------------------
+template <int D> __device__ __forceinline__ int swz(int row) {
+  if constexpr (D == 128) return ((row & 7) << 1) | ((row >> 3) & 1);
+  else return (((row >> 1) & 3) << 1) | ((row >> 3) & 1);
+}
+template <int D> __device__ __forceinline__ int soff(int row, int col) {
+  return row * D + (((col >> 3) ^ swz<D>(row)) << 3) + (col & 7);
+}
+
+__device__ __forceinline__ i16x8 lds16(const short* p) { return *reinterpret_cast<const i16x8*>(p); }
+
+// Transposing LDS read (ds_read_b64_tr_b16): within each 16-lane group, result
+// lane i element j is element i % 4 of the 8 bytes addressed by lane i / 4 + 4 j.
+__device__ __forceinline__ i16x4 lds_tr(const short* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
+}
+
+// A-operand fragment of a row-major swizzled tile read transposed: lane (g, li)
+// gets column c0 + li of rows r0 + 4 g + {0..3} (elements 0-3) and
+// r0 + 16 + 4 g + {0..3} (elements 4-7).
+template <int D>
+__device__ __forceinline__ i16x8 frag_tr(const short* tile, int r0, int c0, int g, int li) {
+  const int row = r0 + 4 * g + (li >> 2), col = c0 + 4 * (li & 3);
+  const i16x4 lo = lds_tr(tile + soff<D>(row, col));
+  const i16x4 hi = lds_tr(tile + soff<D>(row + 16, col));
+  return i16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+// Stage a 64-row tile (rows row0 .. row0 + 63 of a [rows][stride] matrix, D
+// columns) into a swizzled LDS tile with the NW waves of the block: each wave
+// issues 64 / RPS / NW DMA segments of RPS rows.
+template <int D, int NW> struct TileDma {
+  static constexpr int CPR = D / 8;           // 16-byte chunks per row
+  static constexpr int RPS = 64 / CPR;        // rows per 1 KB segment
+  static constexpr int SEGS = 64 / RPS / NW;  // segments per wave
+  uint32_t off[SEGS];
+  __device__ __forceinline__ void init(int w, int lane, uint32_t stride) {
+#pragma unroll
+    for (int u = 0; u < SEGS; ++u) {
+      const int row = (w * SEGS + u) * RPS + lane / CPR;
+      const int c = (lane % CPR) ^ swz<D>(row);
+      off[u] = (row * stride + 8 * c) * 2;
+    }
+  }
+  // base: first row of the matrix; bytes: its extent; row0: first tile row
+  __device__ __forceinline__ void issue(short* tile, const void* base, uint32_t bytes, int row0,
+                                        uint32_t stride, int w) const {
+    const uint32_t skip = (uint32_t)row0 * stride * 2;
+    const i32x4 r = rsrc_words((const char*)base + skip, bytes > skip ? bytes - skip : 0u);
+#pragma unroll
+    for (int u = 0; u < SEGS; ++u) dma16(r, tile + (w * SEGS + u) * RPS * D, off[u]);
+  }
+};
+
+// Block order. Workgroups are dispatched round-robin over the 8 XCDs (block id
+// i runs on XCD i % 8), and each XCD has its own L2. Heads are assigned to XCDs
+// (head h on XCD h % 8 when B*H is a multiple of 8) and each XCD takes the
+// tiles of its heads longest (most causal work) first across all its heads,
+// which balances the causal triangle over the XCD's CUs.
+// Returns the (b*H + h) index and the tile rank (0 = most work).
+__device__ __forceinline__ void block_order(int id, int BH, int& bh, int& rank) {
+  if ((BH & 7) == 0) {
+    const int xcd = id & 7, slot = id >> 3, hpx = BH >> 3;
+    rank = slot / hpx;
+    bh = xcd + 8 * (slot - rank * hpx);
+  } else {
+    rank = id / BH;
+    bh = id - rank * BH;
+  }
+}
+
+// extent in bytes of T rows of D 16-bit elements at a row stride (elements)
+__device__ __forceinline__ uint32_t row_bytes(int T, uint32_t stride, int D) {
+  return ((uint32_t)(T - 1) * stride + (uint32_t)D) * 2u;
+}
+
+}  // namespace mfma
+}  // namespace kat

@@ -44,6 +44,12 @@ def test_load_and_version():
 def test_workspace_sizes():
     lib = _lib.load()
     assert lib.kat_attn_bwd_workspace_size(4, 16, 4096, 128, 1) >= 4 * 16 * 4096 * 4
+    # bf16 / fp16 with an MFMA head dim: per-row stats (8 B) plus fp16 copies of
+    # Q and K; fp32 only needs Delta and cinv
+    rows = 4 * 16 * 4096
+    assert lib.kat_attn_bwd_workspace_size(4, 16, 4096, 128, 1) >= rows * 8 + 2 * rows * 128 * 2
+    assert lib.kat_attn_bwd_workspace_size(4, 16, 4096, 64, 2) >= rows * 8 + 2 * rows * 64 * 2
+    assert lib.kat_attn_bwd_workspace_size(4, 16, 4096, 128, 0) < rows * 16
     assert lib.kat_attn_bwd_workspace_size(0, 16, 4096, 128, 1) == 0
     n = lib.kat_men_bwd_workspace_size(16384, 4096, 1)
     assert n > 0 and n % (4096 * 4) == 0

@@ -127,9 +127,17 @@ def _check_lowp(o, L, dq, dk, dv, q, k, v, do, slopes, scale, sel=None):
         assert_lowp(got, ref, dt, name)
 
 
+def _pin_mfma(monkeypatch, D):
+    # bf16 / fp16 calls whose head dim the MFMA kernels cover must run on them:
+    # with KAT_ATTN_IMPL=mfma a fallback to the tiled kernels is an error
+    if D in (64, 128):
+        monkeypatch.setenv("KAT_ATTN_IMPL", "mfma")
+
+
 @pytest.mark.parametrize("name", ["attn_bf16_d64", "attn_bf16_d128"])
-def test_golden_bf16(gpu, name):
+def test_golden_bf16(gpu, name, monkeypatch):
     z = golden(name)
+    _pin_mfma(monkeypatch, z["q"].shape[-1])
     q, k, v, do = (_t(z[n], torch.bfloat16) for n in ("q", "k", "v", "do"))
     o, L, dq, dk, dv = _run(q, k, v, do, _t(z["slopes"]), float(z["scale"]))
     assert_lowp(o, torch.from_numpy(z["o"]), torch.bfloat16, "o (fixture)")
@@ -139,7 +147,8 @@ def test_golden_bf16(gpu, name):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("B,H,T,D", [(1, 2, 64, 64), (1, 3, 200, 128), (2, 2, 333, 64),
                                      (1, 2, 257, 32), (1, 1, 1, 128), (1, 2, 1000, 128)])
-def test_lowp_shapes(gpu, dtype, B, H, T, D):
+def test_lowp_shapes(gpu, dtype, B, H, T, D, monkeypatch):
+    _pin_mfma(monkeypatch, D)
     q, k, v, do = _inputs(7 * T + D, B, H, T, D, dtype)
     slopes = F.compute_alibi_slopes(H)
     scale = 1.0 / math.sqrt(D)
@@ -147,11 +156,12 @@ def test_lowp_shapes(gpu, dtype, B, H, T, D):
     _check_lowp(o, L, dq, dk, dv, q, k, v, do, slopes, scale)
 
 
-def test_config3_bf16_sampled_heads(gpu):
+def test_config3_bf16_sampled_heads(gpu, monkeypatch):
     # B=4, H=16, S=4096, D=128 bf16; slopes 2^(-(i+1)/2); heads are independent,
     # so the oracle checks three (b, h) pairs, including the smallest and
     # largest slope
     B, H, T, D = 4, 16, 4096, 128
+    _pin_mfma(monkeypatch, D)
     q, k, v, do = _inputs(3, B, H, T, D, torch.bfloat16)
     slopes = torch.tensor([2.0 ** (-(i + 1) / 2) for i in range(H)], dtype=torch.float32)
     scale = 1.0 / math.sqrt(D)
@@ -169,6 +179,7 @@ def test_mfma_matches_tiled_kernel(gpu, monkeypatch):
     B, H, T, D = 1, 4, 384, 128
     q, k, v, do = _inputs(11, B, H, T, D, torch.bfloat16)
     slopes = F.compute_alibi_slopes(H).to(dev)
+    _pin_mfma(monkeypatch, D)
     o_m, L_m = F.rational_attention_forward(q, k, v, slopes, 0.09)
     g_m = F.rational_attention_backward(q, k, v, o_m, L_m, do, slopes, 0.09)
     monkeypatch.setenv("KAT_ATTN_IMPL", "tiled")
@@ -182,9 +193,10 @@ def test_mfma_matches_tiled_kernel(gpu, monkeypatch):
         assert bool((err <= bound).all()), (n, float(err.max()))
 
 
-def test_strided_qkv_views_match_contiguous(gpu):
+def test_strided_qkv_views_match_contiguous(gpu, monkeypatch):
     # the model's layout: one [B, T, 3, H, D] buffer permuted to three views
     B, T, H, D = 2, 150, 4, 64
+    _pin_mfma(monkeypatch, D)
     g = torch.Generator().manual_seed(5)
     qkv = torch.randn(B, T, 3, H, D, generator=g).to(torch.bfloat16).to(dev)
     q, k, v = qkv.permute(2, 0, 3, 1, 4)
@@ -196,7 +208,8 @@ def test_strided_qkv_views_match_contiguous(gpu):
         assert torch.equal(x, y)
 
 
-def test_backward_is_deterministic(gpu):
+def test_backward_is_deterministic(gpu, monkeypatch):
+    _pin_mfma(monkeypatch, 128)
     q, k, v, do = _inputs(9, 1, 2, 512, 128, torch.bfloat16)
     slopes = F.compute_alibi_slopes(2).to(dev)
     a = _run(q, k, v, do, slopes, 0.088)
