@@ -15,6 +15,8 @@ throughput 7*B*H*S^2*D / step time in TFLOP/s. The same JSON line carries:
                  workload (one (b, h) head), on this host's cores.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-fused]
+       python bench.py --copy-calibration   (one plain 1 GiB device copy, for
+                                             scaling HBM byte counters)
 """
 
 import argparse
@@ -30,6 +32,13 @@ sys.path.insert(0, ROOT)
 METRIC = "attn fwd+bwd TFLOP/s (% MFMA peak) at S=4096; fused-op HBM GB/s (% peak)"
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+
+# HBM bytes per call at the benchmark shape, from rocprofv3 FETCH_SIZE and
+# WRITE_SIZE passes (sum over the call's kernels), each scaled by what the same
+# counter reads for a plain 1 GiB copy (python bench.py --copy-calibration:
+# FETCH_SIZE x 2.0, WRITE_SIZE x 1.0). Summary and commands:
+# profiles/attention_bench_hbm_traffic.md
+MEASURED_TRAFFIC_BYTES = {"kat_attn_fwd": 756.6 * 2 ** 20, "kat_attn_bwd": 2003.0 * 2 ** 20}
 
 
 def attention_inputs(torch, B, H, T, D, dev, seed=0):
@@ -174,6 +183,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-fused", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only a plain device-to-device copy of 1 GiB (3 times): the "
+                         "reference for scaling the FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -182,6 +194,17 @@ def main():
         sys.exit(2)
 
     import torch
+    if args.copy_calibration:
+        assert torch.cuda.is_available(), "bench.py needs a GPU"
+        n = 1 << 29  # bf16 elements: 1 GiB read + 1 GiB written per copy
+        x = torch.ones(n, dtype=torch.bfloat16, device="cuda:0")
+        y = torch.empty_like(x)
+        for _ in range(3):
+            y.copy_(x)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes_read": 2 * n, "copy_calibration_bytes_written": 2 * n,
+                          "copies": 3}), flush=True)
+        return
     import fastalgebraictransformer_amd as F
     from fastalgebraictransformer_amd import _lib
     _lib.load()
@@ -211,7 +234,8 @@ def main():
                    "slopes": "2^(-(i+1)/2)", "scale": "1/sqrt(128)"},
         "roofline": {"bound": "mfma", "call": dom, "achieved": round(ach, 2),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": None},
+                     "frac": round(ach / PEAK_BF16_TFLOPS, 4),
+                     "traffic": round(MEASURED_TRAFFIC_BYTES[dom])},
         "kernels": {"kat_attn_fwd": {"ms": round(att["fwd_ms"], 4), "TFLOPs": round(fwd_tf, 2),
                                      "algorithmic_flops": att["flops_fwd"]},
                     "kat_attn_bwd": {"ms": round(att["bwd_ms"], 4), "TFLOPs": round(bwd_tf, 2),
