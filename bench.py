@@ -12,7 +12,12 @@ throughput 7*B*H*S^2*D / step time in TFLOP/s. The same JSON line carries:
                  rational_softmax fwd+bwd at their benchmark shapes (bf16),
                  with the 256 MB last-level cache flushed before each rep;
   * cpu_baseline -- the CPU oracle (fp32) on a bounded sample of the same
-                 workload (one (b, h) head), on this host's cores.
+                 workload (one (b, h) head), on this host's cores;
+  * device     -- CU count, a measured bf16 MFMA loop rate (beside the 2.5 PF
+                 spec peak) and a measured 1 GiB device-copy bandwidth;
+  * model_step -- one training step (bf16 autocast forward + loss + backward,
+                 no optimizer) of the 109.5 M-parameter model at batch 16 x 2048
+                 (reported, not the metric): tokens/s and MFU.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-fused]
        python bench.py --copy-calibration   (one plain 1 GiB device copy, for
@@ -81,11 +86,93 @@ def bench_attention(torch, F, steps, warmup, B=4, H=16, T=4096, D=128):
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms = start.elapsed_time(end) / steps
-    fwd_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / steps
-    bwd_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / steps
+    fwd = sorted(e[0].elapsed_time(e[1]) for e in evs)
+    bwd = sorted(e[1].elapsed_time(e[2]) for e in evs)
     unit = B * H * T * T * D  # one causal S x S x D matmul = 2 * (S^2 / 2) * D flops
-    return dict(ms=ms, wall_ms=wall * 1e3 / steps, fwd_ms=fwd_ms, bwd_ms=bwd_ms,
+    return dict(ms=ms, wall_ms=wall * 1e3 / steps, fwd_ms=sum(fwd) / steps, bwd_ms=sum(bwd) / steps,
+                fwd_median_ms=fwd[steps // 2], bwd_median_ms=bwd[steps // 2],
                 flops_step=7 * unit, flops_fwd=2 * unit, flops_bwd=5 * unit)
+
+
+def device_info(torch, lib):
+    """CU count, measured MFMA loop rate and device-copy bandwidth."""
+    import ctypes
+    dev = torch.device("cuda:0")
+    props = torch.cuda.get_device_properties(dev)
+    cus = props.multi_processor_count
+    blocks, iters = 8 * cus, 20000
+    out = torch.empty(blocks * 256, dtype=torch.float32, device=dev)
+    flops = ctypes.c_double(0.0)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    best = 0.0
+    for _ in range(3):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        rc = lib.kat_probe_mfma_bf16(ctypes.c_void_p(out.data_ptr()), blocks, iters, ctypes.byref(flops), stream)
+        e1.record()
+        torch.cuda.synchronize()
+        if rc != 0:
+            raise RuntimeError("kat_probe_mfma_bf16 failed")
+        best = max(best, flops.value / (e0.elapsed_time(e1) * 1e-3) / 1e12)
+    n = 1 << 29
+    x = torch.ones(n, dtype=torch.bfloat16, device=dev)
+    y = torch.empty_like(x)
+    y.copy_(x)
+    ts = []
+    for _ in range(5):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        y.copy_(x)
+        e1.record()
+        torch.cuda.synchronize()
+        ts.append(e0.elapsed_time(e1))
+    copy_gbs = 4 * n / (min(ts) * 1e-3) / 1e9  # 2 bytes read + 2 written per element
+    del x, y, out
+    return {"name": props.name, "arch": getattr(props, "gcnArchName", ""), "cus": cus,
+            "mfma_bf16_loop_tflops": round(best, 1),
+            "mfma_bf16_spec_tflops": PEAK_BF16_TFLOPS, "copy_1GiB_GBs": round(copy_gbs, 1),
+            "hbm_spec_GBs": PEAK_HBM_GBS}
+
+
+def bench_model_step(torch, steps=5, warmup=2):
+    """Config-4 training step: AlgebraicTransformerLM(32000, 768, 12, 12), batch
+    16 x 2048, bf16 autocast forward + cross-entropy, backward (no optimizer)."""
+    from fastalgebraictransformer_amd.algebraic_model import AlgebraicTransformerLM
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    model = AlgebraicTransformerLM(32000, 768, 12, 12).to(dev)
+    model.train()
+    g = torch.Generator().manual_seed(0)
+    ids = torch.randint(0, 32000, (16, 2048), generator=g).to(dev)
+    labels = torch.randint(0, 32000, (16, 2048), generator=g).to(dev)
+
+    def step():
+        model.zero_grad(set_to_none=True)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            _, loss = model(ids, labels)
+        loss.backward()
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    params = sum(p.numel() for p in model.parameters())
+    # 6 N per token for the dense layers, plus causal attention fwd+bwd = 7 B H S^2 D
+    # per layer (12 layers): 25.86 TFLOP per step at this shape
+    flops = 6 * params * 16 * 2048 + 12 * 7 * 16 * 12 * 2048 * 2048 * 64
+    del model
+    torch.cuda.empty_cache()
+    return {"model": "AlgebraicTransformerLM(32000, 768, 12, 12)", "params": params,
+            "batch": [16, 2048], "ms_per_step": round(ms, 3),
+            "tokens_per_s": round(16 * 2048 / (ms * 1e-3), 1),
+            "tflops_step": round(flops / 1e12, 2), "mfu": round(flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+            "note": "reported, not the metric; dropout 0.1 (model default)"}
 
 
 def bench_fused(torch, F, reps=10):
@@ -154,10 +241,23 @@ def bench_fused(torch, F, reps=10):
     return res
 
 
-def cpu_baseline(torch, S=4096, D=128, reps=2):
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(torch, S=4096, D=128, reps=3):
     """CPU oracle (fp32) forward + backward of one (b, h) head of the workload
-    (heads are independent, so this is an exact 1/64 slice)."""
+    (heads are independent, so this is an exact 1/64 slice), on every core this
+    process may run on."""
     import oracle as O
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
     g = torch.Generator().manual_seed(0)
     q, k, v, do = (torch.randn(1, 1, S, D, generator=g).to(torch.bfloat16) for _ in range(4))
     slopes = torch.tensor([2.0 ** -0.5])
@@ -168,21 +268,24 @@ def cpu_baseline(torch, S=4096, D=128, reps=2):
         o, L = O.attention_fwd(q, k, v, slopes, scale, dtype=torch.float32)
         O.attention_bwd(q, k, v, o, L, do, slopes, scale, dtype=torch.float32)
         ts.append(time.perf_counter() - t0)
-    t = min(ts)
+    t = sorted(ts)[len(ts) // 2]
     flops = 7 * S * S * D
     return {"value": flops / t / 1e12, "unit": "TFLOP/s", "cores": torch.get_num_threads(),
             "kind": "port",
             "sample": f"1 of 64 (b,h) heads at S={S}, D={D}: oracle fp32 fwd+bwd, "
-                      f"best of {reps} ({t:.2f} s per head)"}
+                      f"median of {reps} ({t:.2f} s per head); {cpu_model()}, "
+                      f"affinity {cores} of os.cpu_count() {os.cpu_count()}"}
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-fused", action="store_true")
+    ap.add_argument("--no-model", action="store_true", help="skip the model training step")
+    ap.add_argument("--no-device", action="store_true", help="skip the MFMA / copy probes")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain device-to-device copy of 1 GiB (3 times): the "
                          "reference for scaling the FETCH_SIZE / WRITE_SIZE counters")
@@ -236,16 +339,20 @@ def main():
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(ach / PEAK_BF16_TFLOPS, 4),
                      "traffic": round(MEASURED_TRAFFIC_BYTES[dom])},
-        "kernels": {"kat_attn_fwd": {"ms": round(att["fwd_ms"], 4), "TFLOPs": round(fwd_tf, 2),
-                                     "algorithmic_flops": att["flops_fwd"]},
-                    "kat_attn_bwd": {"ms": round(att["bwd_ms"], 4), "TFLOPs": round(bwd_tf, 2),
-                                     "algorithmic_flops": att["flops_bwd"]}},
+        "kernels": {"kat_attn_fwd": {"ms": round(att["fwd_ms"], 4), "median_ms": round(att["fwd_median_ms"], 4),
+                                     "TFLOPs": round(fwd_tf, 2), "algorithmic_flops": att["flops_fwd"]},
+                    "kat_attn_bwd": {"ms": round(att["bwd_ms"], 4), "median_ms": round(att["bwd_median_ms"], 4),
+                                     "TFLOPs": round(bwd_tf, 2), "algorithmic_flops": att["flops_bwd"]}},
         "frac_mfma_peak_step": round(value / PEAK_BF16_TFLOPS, 4),
     }
     if not args.no_fused:
         fused = bench_fused(torch, F)
         line["fused_ops"] = {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv)
                                  for kk, vv in r.items()} for k, r in fused.items()}
+    if not args.no_device:
+        line["device"] = device_info(torch, _lib.load())
+    if not args.no_model:
+        line["model_step"] = bench_model_step(torch)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(torch)
         line["cpu_baseline"]["value"] = round(line["cpu_baseline"]["value"], 5)

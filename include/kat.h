@@ -119,8 +119,8 @@ int kat_men_bwd(const void* dy, const void* x, const void* w, const float* mu, v
  * l_strides: 3 int64 = (b, h, t) strides of L. slopes: fp32 [H].
  * Replaces the host wrapper + rational_attention_fwd_kernel[(B,H,T)] launch at
  * forward.py:267-319 (kernel forward.py:49-159). dtype KAT_BF16/KAT_F16 use
- * the MFMA kernel (D in {32, 64, 128}); KAT_F32 and other D (<= 256) use the
- * fp32 tiled kernel.
+ * the MFMA kernels (D in {64, 128}, 16-byte aligned rows); KAT_F32 and other
+ * D (<= 256) use the fp32 tiled kernels.
  * ---------------------------------------------------------------------- */
 int kat_attn_fwd(const void* q, const void* k, const void* v, void* out, float* L,
                  const float* slopes, int64_t B, int64_t H, int64_t T, int64_t D,
@@ -143,6 +143,15 @@ int kat_attn_bwd(const void* q, const void* k, const void* v, const void* out,
                  int64_t H, int64_t T, int64_t D, const int64_t* strides,
                  const int64_t* l_strides, float scale, float eps, int causal, int dtype,
                  void* stream);
+
+/* ----------------------------------------------------------------------
+ * Measurement helper (no counterpart in the reference; used by bench.py to
+ * report a measured MFMA rate beside the spec peak). `blocks` x 256 threads
+ * each run `iters` rounds of 16 independent v_mfma_f32_16x16x32_bf16 chains
+ * and write one float per thread to `out` (blocks * 256 floats). *flops
+ * receives the flops the launch executes.
+ * ---------------------------------------------------------------------- */
+int kat_probe_mfma_bf16(float* out, int blocks, int iters, double* flops, void* stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,29 @@
+"""The MFMA throughput probe bench.py uses (kat_probe_mfma_bf16)."""
+
+import ctypes
+
+import pytest
+import torch
+
+from fastalgebraictransformer_amd import _lib
+
+pytestmark = pytest.mark.gpu
+
+
+def test_probe_mfma_runs_and_counts_flops(gpu):
+    lib = _lib.load()
+    out = torch.empty(4 * 256, dtype=torch.float32, device="cuda")
+    flops = ctypes.c_double(0.0)
+    rc = lib.kat_probe_mfma_bf16(ctypes.c_void_p(out.data_ptr()), 4, 10, ctypes.byref(flops),
+                                 ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    assert rc == 0
+    # 4 blocks x 4 waves x 10 iterations x 16 MFMAs x (16 x 16 x 32 x 2) flops
+    assert flops.value == 4 * 4 * 10 * 16 * 16 * 16 * 32 * 2
+    assert bool(torch.isfinite(out).all())
+
+
+def test_probe_rejects_bad_arguments():
+    lib = _lib.load()
+    flops = ctypes.c_double(0.0)
+    assert lib.kat_probe_mfma_bf16(None, 4, 10, ctypes.byref(flops), None) != 0
