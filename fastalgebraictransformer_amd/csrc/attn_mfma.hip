@@ -109,7 +109,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_k(AttnArgs a) {
   dv.init(w, lane, sv2);
 
   // S^T of the 16 keys at tile rows hr .. hr + 15
-  auto m1 = [&](int hr, f32x4 (&s_)[2], const short* ks_) {
+  auto m1 = [&](int hr, f32x4 (&s_)[2], const short* ks_) __attribute__((always_inline)) {
 #pragma unroll
     for (int qs = 0; qs < 2; ++qs) s_[qs] = cb;
 #pragma unroll
@@ -120,7 +120,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_k(AttnArgs a) {
     }
   };
   // f' of those scores, packed as P^T; row sums into lsum
-  auto vh = [&](auto mask_tag, int kh, const f32x4 (&s_)[2], uint32_t (&pk)[2][2]) {
+  auto vh = [&](auto mask_tag, int kh, const f32x4 (&s_)[2], uint32_t (&pk)[2][2]) __attribute__((always_inline)) {
     constexpr bool MASK = decltype(mask_tag)::value;
 #pragma unroll
     for (int qs = 0; qs < 2; ++qs) {
@@ -141,7 +141,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_k(AttnArgs a) {
     }
   };
   // O^T += V^T P^T over the 32 keys at tile rows r0 .. r0 + 31
-  auto m2 = [&](int r0, const uint32_t (&pa)[2][2], const uint32_t (&pb)[2][2], const short* vs_) {
+  auto m2 = [&](int r0, const uint32_t (&pa)[2][2], const uint32_t (&pb)[2][2], const short* vs_) __attribute__((always_inline)) {
     i16x8 pf[2];
 #pragma unroll
     for (int qs = 0; qs < 2; ++qs) pf[qs] = pack_frag(pa[qs][0], pa[qs][1], pb[qs][0], pb[qs][1]);
@@ -152,7 +152,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_k(AttnArgs a) {
       for (int qs = 0; qs < 2; ++qs) oacc[ds][qs] = M::mma(vt, pf[qs], oacc[ds][qs]);
     }
   };
-  auto tile = [&](auto mask_tag, int k0, const short* ks_, const short* vs_) {
+  auto tile = [&](auto mask_tag, int k0, const short* ks_, const short* vs_) __attribute__((always_inline)) {
     f32x4 sA[2], sB[2];
     uint32_t pa0[2][2], pb0[2][2], pa1[2][2], pb1[2][2];
     m1(0, sA, ks_);
@@ -172,8 +172,11 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_k(AttnArgs a) {
   dv.issue(sv[0], vp, vbytes, 0, sv2, w);
   dma_wait();
   __syncthreads();
-  for (int kt = 0; kt < n_kt; ++kt) {
-    const int buf = kt & 1;
+  // tile kt sits in buffer kt & 1; the loop is unrolled by two so that the
+  // buffer, and with it every LDS address, is a compile-time constant plus a
+  // per-lane offset kept in a register
+  auto step = [&](int kt, auto buf_tag) __attribute__((always_inline)) {
+    constexpr int buf = decltype(buf_tag)::value;
     if (kt + 1 < n_kt) {
       dk.issue(sk[buf ^ 1], kp, kbytes, (kt + 1) * kBN, sk2, w);
       dv.issue(sv[buf ^ 1], vp, vbytes, (kt + 1) * kBN, sv2, w);
@@ -185,6 +188,10 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_k(AttnArgs a) {
       tile(std::true_type{}, k0, sk[buf], sv[buf]);
     dma_wait();
     __syncthreads();
+  };
+  for (int kt = 0; kt < n_kt; kt += 2) {
+    step(kt, std::integral_constant<int, 0>{});
+    if (kt + 1 < n_kt) step(kt + 1, std::integral_constant<int, 1>{});
   }
 
   // epilogue: L' across the 4 lane groups, normalise, store
@@ -314,7 +321,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_k(AttnArgs a, const float2
   dv.init(w, lane, sv2);
 
   // S^T and dP^T of the 16 keys at tile rows hr .. hr + 15
-  auto m1 = [&](int hr, f32x4 (&s_)[2], f32x4 (&p_)[2], const short* ks_, const short* vs_) {
+  auto m1 = [&](int hr, f32x4 (&s_)[2], f32x4 (&p_)[2], const short* ks_, const short* vs_) __attribute__((always_inline)) {
 #pragma unroll
     for (int qs = 0; qs < 2; ++qs) {
       s_[qs] = cb;
@@ -332,7 +339,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_k(AttnArgs a, const float2
     }
   };
   // dS of those scores, packed fp16 as dS^T
-  auto vh = [&](auto mask_tag, int kh, const f32x4 (&s_)[2], const f32x4 (&p_)[2], uint32_t (&pk)[2][2]) {
+  auto vh = [&](auto mask_tag, int kh, const f32x4 (&s_)[2], const f32x4 (&p_)[2], uint32_t (&pk)[2][2]) __attribute__((always_inline)) {
     constexpr bool MASK = decltype(mask_tag)::value;
 #pragma unroll
     for (int qs = 0; qs < 2; ++qs) {
@@ -352,7 +359,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_k(AttnArgs a, const float2
     }
   };
   // dQ^T += K16^T dS^T over the 32 keys at tile rows r0 .. r0 + 31
-  auto m2 = [&](int r0, const uint32_t (&pa)[2][2], const uint32_t (&pb)[2][2], const short* ks_) {
+  auto m2 = [&](int r0, const uint32_t (&pa)[2][2], const uint32_t (&pb)[2][2], const short* ks_) __attribute__((always_inline)) {
     i16x8 dsf[2];
 #pragma unroll
     for (int qs = 0; qs < 2; ++qs) dsf[qs] = pack_frag(pa[qs][0], pa[qs][1], pb[qs][0], pb[qs][1]);
@@ -363,7 +370,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_k(AttnArgs a, const float2
       for (int qs = 0; qs < 2; ++qs) dqacc[ds][qs] = mma_f16(kt, dsf[qs], dqacc[ds][qs]);
     }
   };
-  auto tile = [&](auto mask_tag, int k0, const short* ks_, const short* vs_) {
+  auto tile = [&](auto mask_tag, int k0, const short* ks_, const short* vs_) __attribute__((always_inline)) {
     f32x4 sA[2], pA[2], sB[2], pB[2];
     uint32_t da0[2][2], db0[2][2], da1[2][2], db1[2][2];
     m1(0, sA, pA, ks_, vs_);
@@ -383,8 +390,9 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_k(AttnArgs a, const float2
   dv.issue(sv[0], vp, vbytes, 0, sv2, w);
   dma_wait();
   __syncthreads();
-  for (int kt = 0; kt < n_kt; ++kt) {
-    const int buf = kt & 1;
+  // unrolled by two: static buffers (see the forward)
+  auto step = [&](int kt, auto buf_tag) __attribute__((always_inline)) {
+    constexpr int buf = decltype(buf_tag)::value;
     if (kt + 1 < n_kt) {
       dk.issue(sk[buf ^ 1], kp, kbytes, (kt + 1) * kBN, D, w);
       dv.issue(sv[buf ^ 1], vp, vbytes, (kt + 1) * kBN, sv2, w);
@@ -396,6 +404,10 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_k(AttnArgs a, const float2
       tile(std::true_type{}, k0, sk[buf], sv[buf]);
     dma_wait();
     __syncthreads();
+  };
+  for (int kt = 0; kt < n_kt; kt += 2) {
+    step(kt, std::integral_constant<int, 0>{});
+    if (kt + 1 < n_kt) step(kt + 1, std::integral_constant<int, 1>{});
   }
 
   T* __restrict__ dqp = (T*)a.dq + b * a.sdq[0] + h * a.sdq[1];
@@ -488,7 +500,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkv_k(AttnArgs a, const float
   do_.init(w, lane, sdo2);
   // stats of a 64-query tile: 512 bytes, lanes 0..31 of wave 0
   const uint32_t st_off = (uint32_t)lane * 16u;
-  auto issue = [&](int buf, int qrow0) {
+  auto issue = [&](int buf, int qrow0) __attribute__((always_inline)) {
     dq_.issue(sq[buf], qp, qbytes, qrow0, D, w);
     do_.issue(so[buf], dop, obytes, qrow0, sdo2, w);
     if (w == 0 && lane < 32) {
@@ -498,7 +510,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkv_k(AttnArgs a, const float
   };
 
   // S and dP of the 16 queries at tile rows hr .. hr + 15
-  auto m1 = [&](int hr, f32x4 (&s_)[2], f32x4 (&p_)[2], const short* qs_, const short* os_) {
+  auto m1 = [&](int hr, f32x4 (&s_)[2], f32x4 (&p_)[2], const short* qs_, const short* os_) __attribute__((always_inline)) {
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       s_[ks] = cb;
@@ -517,7 +529,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkv_k(AttnArgs a, const float
   };
   // P (input dtype) and dS (fp16) of those scores
   auto vh = [&](auto mask_tag, int qh, int hr, const f32x4 (&s_)[2], const f32x4 (&p_)[2],
-                const float2* st_, uint32_t (&pp)[2][2], uint32_t (&dp)[2][2]) {
+                const float2* st_, uint32_t (&pp)[2][2], uint32_t (&dp)[2][2]) __attribute__((always_inline)) {
     constexpr bool MASK = decltype(mask_tag)::value;
     const f32x4 s01 = *reinterpret_cast<const f32x4*>(st_ + hr + 4 * g);
     const f32x4 s23 = *reinterpret_cast<const f32x4*>(st_ + hr + 4 * g + 2);
@@ -550,7 +562,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkv_k(AttnArgs a, const float
   // dV^T += dO^T P and dK^T += Q16^T dS over the 32 queries at tile rows r0 .. r0 + 31
   auto m2 = [&](int r0, const uint32_t (&pa)[2][2], const uint32_t (&pb)[2][2],
                 const uint32_t (&da)[2][2], const uint32_t (&db)[2][2], const short* qs_,
-                const short* os_) {
+                const short* os_) __attribute__((always_inline)) {
     i16x8 pf[2], dsf[2];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
@@ -569,7 +581,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkv_k(AttnArgs a, const float
     }
   };
   // 32 queries starting at qc (tile rows r0 .. r0 + 31)
-  auto chunk = [&](auto mask_tag, int qc, int r0, const short* qs_, const short* os_, const float2* st_) {
+  auto chunk = [&](auto mask_tag, int qc, int r0, const short* qs_, const short* os_, const float2* st_) __attribute__((always_inline)) {
     f32x4 sA[2], pA[2], sB[2], pB[2];
     uint32_t pa[2][2], pb[2][2], da[2][2], db[2][2];
     m1(r0, sA, pA, qs_, os_);
@@ -583,8 +595,9 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkv_k(AttnArgs a, const float
   if (n_it > 0) issue(0, k0);
   dma_wait();
   __syncthreads();
-  for (int it = 0; it < n_it; ++it) {
-    const int buf = it & 1;
+  // unrolled by two: static buffers (see the forward)
+  auto step = [&](int it, auto buf_tag) __attribute__((always_inline)) {
+    constexpr int buf = decltype(buf_tag)::value;
     if (it + 1 < n_it) issue(buf ^ 1, k0 + (it + 1) * kBN);
     const int q0 = k0 + it * kBN;
 #pragma unroll
@@ -597,6 +610,10 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkv_k(AttnArgs a, const float
     }
     dma_wait();
     __syncthreads();
+  };
+  for (int it = 0; it < n_it; it += 2) {
+    step(it, std::integral_constant<int, 0>{});
+    if (it + 1 < n_it) step(it + 1, std::integral_constant<int, 1>{});
   }
 
   T* __restrict__ dkp = (T*)a.dk + b * a.sdk[0] + h * a.sdk[1];
