@@ -4,7 +4,8 @@
 //   attn_fwd_k      O, L      query-tile blocks; K, V tiles stream through LDS
 //   attn_bwd_prep_k Delta, stats, fp16 copies of Q and K (row-parallel)
 //   attn_bwd_dq_k   dQ        query-tile blocks; fp16 K and V tiles stream
-//   attn_bwd_dkv_k  dK, dV    key-tile blocks; fp16 Q and dO tiles stream
+//   attn_bwd_dkv_k  dK, dV    key-tile blocks; fp16 Q and dO tiles stream; the
+//                             waves split into a dV role and a dK role
 // No atomics: every output element is written by one wave, so results are
 // deterministic.
 //
@@ -427,23 +428,39 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_k(AttnArgs a, const float2
 }
 
 // ============================================================================
-// dK, dV: 128 keys per block (4 waves x 32 keys, one block per CU: the K / V
-// fragments and the dK / dV accumulators of 32 keys take ~200 VGPRs); 64-query
-// Q16 / dO tiles and their stats stream through LDS.
-//   S  = Q16 K16^T (+bias)   A = Q16 (LDS rows)          B = K16^T (VGPRs)
-//   dP = dO V^T              A = dO  (LDS rows)          B = V^T   (VGPRs)
-//   dV^T += dO^T P           A = dO^T (LDS transposed)   B = P     (from S)
-//   dK^T += Q16^T dS         A = Q16^T (LDS transposed)  B = dS    (from S, dP)
+// dK, dV: 128 keys per block, 8 waves in two roles. Waves w and w + 4 share the
+// 32 keys kw = k0 + 32 (w % 4) and one SIMD; each role holds one B-operand set
+// and one accumulator set (~200 VGPRs, two waves per SIMD):
+//   P role (w < 4)   S  = Q16 K16^T (+bias)  A = Q16 (LDS rows)         B = K16^T (VGPRs)
+//                    dV^T += dO^T P          A = dO^T (LDS transposed)  B = P (from S)
+//   D role (w >= 4)  dP = dO V^T             A = dO  (LDS rows)         B = V^T   (VGPRs)
+//                    dK^T += Q16^T dS        A = Q16^T (LDS transposed) B = dS
+// The P role also forms w = (t r)^2 t of every score and passes it to the D role
+// through LDS, lane to lane (both roles hold the scores of a 16-query half in
+// the same MFMA C layout), so dS = w (4 cinv dP - 4 cinv Delta) costs the D role
+// one FMA and one multiply. 64-query Q16 / dO tiles and their stats stream
+// through LDS; a tile is worked in two 32-query chunks with one barrier each:
+//   phase 1: P role S, P, w of chunk c                    | barrier
+//   phase 2: P role dV(c); D role dP(c + 1), dS(c), dK(c)
+// The D role computes dP one chunk ahead so that the reads of w issued after
+// the barrier overlap with MFMAs.
 // ============================================================================
+template <int D>
+struct DkvSmem {
+  short q[2][kBN * D];      // Q16 tiles
+  short o[2][kBN * D];      // dO tiles
+  float2 st[2][kBN];        // (4 cinv, -4 cinv Delta) of the tile's queries
+  f32x4 x[2][kNW][4][64];   // w: [chunk parity][key group][16-query half x ks][lane]
+};
+
 template <typename T, int D>
-__global__ __launch_bounds__(256, 1) void attn_bwd_dkv_k(AttnArgs a, const float2* __restrict__ stats,
+__global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float2* __restrict__ stats,
                                                          const f16* __restrict__ q16) {
   typedef Mfma<T> M;
   constexpr int KK = D / 32;
   constexpr int DS = D / 16;
-  __shared__ short sq[2][kBN * D];
-  __shared__ short so[2][kBN * D];
-  __shared__ float2 sst[2][kBN];
+  constexpr int NW = 2 * kNW;
+  __shared__ DkvSmem<D> sm;
 
   const int T_ = a.T, H = a.H;
   int bh, rank;
@@ -451,8 +468,10 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkv_k(AttnArgs a, const float
   const int k0 = rank * kBM;
   const int b = bh / H, h = bh - b * H;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int grp = w % kNW;
+  const bool prole = w < kNW;
   const int g = lane >> 4, li = lane & 15;
-  const int kw = k0 + kRows * w;
+  const int kw = k0 + kRows * grp;
 
   const f16* qp = q16 + (int64_t)bh * T_ * D;
   const T* kp = (const T*)a.k + b * a.sk[0] + h * a.sk[1];
@@ -465,9 +484,9 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkv_k(AttnArgs a, const float
   const float slope = a.slopes[h];
   const float scale = a.scale;
 
-  // K16^T / V^T fragments (B operands): lane (g, li) holds row kw + 16 ks + li,
-  // columns 32 kk + 8 g .. +7
-  i16x8 kf[2][KK], vf[2][KK];
+  // B operands: K16^T (P role) or V^T (D role) fragments; lane (g, li) holds row
+  // kw + 16 ks + li, columns 32 kk + 8 g .. +7
+  i16x8 bfr[2][KK];
   {
     const __amdgpu_buffer_rsrc_t rk = rsrc(kp, row_bytes(T_, sk2, D));
     const __amdgpu_buffer_rsrc_t rv = rsrc(vp, row_bytes(T_, sv2, D));
@@ -476,8 +495,8 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkv_k(AttnArgs a, const float
       const uint32_t key = (uint32_t)(kw + 16 * ks + li);
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk) {
-        kf[ks][kk] = to_f16x8<T>(load16(rk, (key * sk2 + 32 * kk + 8 * g) * 2));
-        vf[ks][kk] = load16(rv, (key * sv2 + 32 * kk + 8 * g) * 2);
+        if (prole) bfr[ks][kk] = to_f16x8<T>(load16(rk, (key * sk2 + 32 * kk + 8 * g) * 2));
+        else bfr[ks][kk] = load16(rv, (key * sv2 + 32 * kk + 8 * g) * 2);
       }
     }
   }
@@ -486,59 +505,53 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkv_k(AttnArgs a, const float
 #pragma unroll
   for (int j = 0; j < 4; ++j) cb[j] = (slope / scale) * (float)(li - 4 * g - j);
 
-  f32x4 dkacc[DS][2], dvacc[DS][2];
+  f32x4 acc[DS][2];  // dV^T (P role) or dK^T (D role)
 #pragma unroll
   for (int ds = 0; ds < DS; ++ds)
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      dkacc[ds][ks] = f32x4{0.f, 0.f, 0.f, 0.f};
-      dvacc[ds][ks] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
+    for (int ks = 0; ks < 2; ++ks) acc[ds][ks] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  TileDma<D, kNW> dq_, do_;
+  TileDma<D, NW> dq_, do_;
   dq_.init(w, lane, D);
   do_.init(w, lane, sdo2);
   // stats of a 64-query tile: 512 bytes, lanes 0..31 of wave 0
   const uint32_t st_off = (uint32_t)lane * 16u;
   auto issue = [&](int buf, int qrow0) __attribute__((always_inline)) {
-    dq_.issue(sq[buf], qp, qbytes, qrow0, D, w);
-    do_.issue(so[buf], dop, obytes, qrow0, sdo2, w);
+    dq_.issue(sm.q[buf], qp, qbytes, qrow0, D, w);
+    do_.issue(sm.o[buf], dop, obytes, qrow0, sdo2, w);
     if (w == 0 && lane < 32) {
       const uint32_t skip = (uint32_t)qrow0 * 8u;
-      dma16(rsrc_words((const char*)stp + skip, stbytes > skip ? stbytes - skip : 0u), sst[buf], st_off);
+      dma16(rsrc_words((const char*)stp + skip, stbytes > skip ? stbytes - skip : 0u), sm.st[buf], st_off);
     }
   };
 
-  // S and dP of the 16 queries at tile rows hr .. hr + 15
-  auto m1 = [&](int hr, f32x4 (&s_)[2], f32x4 (&p_)[2], const short* qs_, const short* os_) __attribute__((always_inline)) {
+  // S (P role) or dP (D role) of the 16 queries at tile rows hr .. hr + 15
+  auto m1 = [&](auto role, int hr, f32x4 (&s_)[2], const short* as_) __attribute__((always_inline)) {
+    constexpr bool P = decltype(role)::value;
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      s_[ks] = cb;
-      p_[ks] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
+    for (int ks = 0; ks < 2; ++ks) s_[ks] = P ? cb : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {
-      const i16x8 qa = lds16(qs_ + soff<D>(hr + li, 32 * kk + 8 * g));
-      const i16x8 oa = lds16(os_ + soff<D>(hr + li, 32 * kk + 8 * g));
+      const i16x8 fa = lds16(as_ + soff<D>(hr + li, 32 * kk + 8 * g));
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        s_[ks] = mma_f16(qa, kf[ks][kk], s_[ks]);
-        p_[ks] = M::mma(oa, vf[ks][kk], p_[ks]);
+        if constexpr (P) s_[ks] = mma_f16(fa, bfr[ks][kk], s_[ks]);
+        else s_[ks] = M::mma(fa, bfr[ks][kk], s_[ks]);
       }
     }
   };
-  // P (input dtype) and dS (fp16) of those scores
-  auto vh = [&](auto mask_tag, int qh, int hr, const f32x4 (&s_)[2], const f32x4 (&p_)[2],
-                const float2* st_, uint32_t (&pp)[2][2], uint32_t (&dp)[2][2]) __attribute__((always_inline)) {
+  // P role: P (input dtype) of a 16-query half, and w into the exchange buffer
+  auto vp_ = [&](auto mask_tag, int qh, int hr, const f32x4 (&s_)[2], const float2* st_, f32x4 (*xw)[64],
+                 int xg, uint32_t (&pp)[2][2]) __attribute__((always_inline)) {
     constexpr bool MASK = decltype(mask_tag)::value;
     const f32x4 s01 = *reinterpret_cast<const f32x4*>(st_ + hr + 4 * g);
     const f32x4 s23 = *reinterpret_cast<const f32x4*>(st_ + hr + 4 * g + 2);
     const float c4v[4] = {s01[0], s01[2], s23[0], s23[2]};
-    const float ndv[4] = {s01[1], s01[3], s23[1], s23[3]};
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       const float tterm = slope * (float)(kw + 16 * ks - qh);
-      float pv[4], dv[4];
+      float pv[4];
+      f32x4 wv;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const float s = fmaf(s_[ks][j], scale, tterm);
@@ -547,90 +560,130 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkv_k(AttnArgs a, const float
         const float t2 = t * t;
         const float u = t * r;
         pv[j] = (t2 * t2) * (0.25f * c4v[j]);
-        dv[j] = (u * u * t) * fmaf(p_[ks][j], c4v[j], ndv[j]);
+        wv[j] = u * u * t;
         if (MASK && kw + 16 * ks + li > qh + 4 * g + j) {
           pv[j] = 0.f;
-          dv[j] = 0.f;
+          wv[j] = 0.f;
         }
       }
+      xw[xg + ks][lane] = wv;
       pp[ks][0] = M::pack2(pv[0], pv[1]);
       pp[ks][1] = M::pack2(pv[2], pv[3]);
-      dp[ks][0] = pack2_f16(dv[0], dv[1]);
-      dp[ks][1] = pack2_f16(dv[2], dv[3]);
     }
   };
-  // dV^T += dO^T P and dK^T += Q16^T dS over the 32 queries at tile rows r0 .. r0 + 31
-  auto m2 = [&](int r0, const uint32_t (&pa)[2][2], const uint32_t (&pb)[2][2],
-                const uint32_t (&da)[2][2], const uint32_t (&db)[2][2], const short* qs_,
-                const short* os_) __attribute__((always_inline)) {
-    i16x8 pf[2], dsf[2];
+  // acc^T += A^T B over the 32 queries at tile rows r0 .. r0 + 31, A = dO (P role)
+  // or Q16 (D role) read transposed, B = P or dS
+  auto m2 = [&](auto role, int r0, const uint32_t (&pa)[2][2], const uint32_t (&pb)[2][2],
+                const short* as_) __attribute__((always_inline)) {
+    constexpr bool P = decltype(role)::value;
+    i16x8 bf2[2];
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      pf[ks] = pack_frag(pa[ks][0], pa[ks][1], pb[ks][0], pb[ks][1]);
-      dsf[ks] = pack_frag(da[ks][0], da[ks][1], db[ks][0], db[ks][1]);
-    }
+    for (int ks = 0; ks < 2; ++ks) bf2[ks] = pack_frag(pa[ks][0], pa[ks][1], pb[ks][0], pb[ks][1]);
 #pragma unroll
     for (int ds = 0; ds < DS; ++ds) {
-      const i16x8 ot = frag_tr<D>(os_, r0, 16 * ds, g, li);
-      const i16x8 qt = frag_tr<D>(qs_, r0, 16 * ds, g, li);
+      const i16x8 at = frag_tr<D>(as_, r0, 16 * ds, g, li);
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        dvacc[ds][ks] = M::mma(ot, pf[ks], dvacc[ds][ks]);
-        dkacc[ds][ks] = mma_f16(qt, dsf[ks], dkacc[ds][ks]);
+        if constexpr (P) acc[ds][ks] = M::mma(at, bf2[ks], acc[ds][ks]);
+        else acc[ds][ks] = mma_f16(at, bf2[ks], acc[ds][ks]);
       }
     }
   };
-  // 32 queries starting at qc (tile rows r0 .. r0 + 31)
-  auto chunk = [&](auto mask_tag, int qc, int r0, const short* qs_, const short* os_, const float2* st_) __attribute__((always_inline)) {
-    f32x4 sA[2], pA[2], sB[2], pB[2];
-    uint32_t pa[2][2], pb[2][2], da[2][2], db[2][2];
-    m1(r0, sA, pA, qs_, os_);
-    m1(r0 + 16, sB, pB, qs_, os_);
-    vh(mask_tag, qc, r0, sA, pA, st_, pa, da);
-    vh(mask_tag, qc + 16, r0 + 16, sB, pB, st_, pb, db);
-    m2(r0, pa, pb, da, db, qs_, os_);
-  };
 
+  // chunk c: queries k0 + 32 c .. +31, tile (c / 2) in buffer (c / 2) & 1, rows 32 (c & 1)
   const int n_it = k0 < T_ ? (T_ - k0 + kBN - 1) / kBN : 0;  // causal: queries >= k0
+  const int n_ch = 2 * n_it;
+  auto needc = [&](int c) __attribute__((always_inline)) { return c < n_ch && k0 + 32 * c + 31 >= kw; };
+  auto fullc = [&](int c) __attribute__((always_inline)) { return k0 + 32 * c >= kw + kRows - 1; };
   if (n_it > 0) issue(0, k0);
   dma_wait();
   __syncthreads();
-  // unrolled by two: static buffers (see the forward)
-  auto step = [&](int it, auto buf_tag) __attribute__((always_inline)) {
-    constexpr int buf = decltype(buf_tag)::value;
-    if (it + 1 < n_it) issue(buf ^ 1, k0 + (it + 1) * kBN);
-    const int q0 = k0 + it * kBN;
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      const int qc = q0 + 32 * c;
-      if (qc >= kw + kRows - 1)
-        chunk(std::false_type{}, qc, 32 * c, sq[buf], so[buf], sst[buf]);
-      else if (qc + 31 >= kw)
-        chunk(std::true_type{}, qc, 32 * c, sq[buf], so[buf], sst[buf]);
+  f32x4 dpA[2][2], dpB[2][2];  // D role: dP of the current and the next chunk
+  if (!prole && needc(0)) {
+    m1(std::false_type{}, 0, dpA[0], sm.o[0]);
+    m1(std::false_type{}, 16, dpA[1], sm.o[0]);
+  }
+  auto step = [&](int c, f32x4 (&pcur)[2][2], f32x4 (&pnext)[2][2]) __attribute__((always_inline)) {
+    const int it = c >> 1, buf = it & 1, r0 = 32 * (c & 1);
+    const int qc = k0 + 32 * c;
+    const bool need = needc(c), full = need && fullc(c);
+    f32x4 (*xw)[64] = sm.x[c & 1][grp];
+    uint32_t pa[2][2], pb[2][2];
+    if (prole && need) {
+      f32x4 sA[2], sB[2];
+      m1(std::true_type{}, r0, sA, sm.q[buf]);
+      m1(std::true_type{}, r0 + 16, sB, sm.q[buf]);
+      if (full) {
+        vp_(std::false_type{}, qc, r0, sA, sm.st[buf], xw, 0, pa);
+        vp_(std::false_type{}, qc + 16, r0 + 16, sB, sm.st[buf], xw, 2, pb);
+      } else {
+        vp_(std::true_type{}, qc, r0, sA, sm.st[buf], xw, 0, pa);
+        vp_(std::true_type{}, qc + 16, r0 + 16, sB, sm.st[buf], xw, 2, pb);
+      }
     }
-    dma_wait();
-    __syncthreads();
+    if ((c & 1) == 0) {
+      // every wave has left the previous tile: its buffer takes the next one
+      __syncthreads();
+      if (it + 1 < n_it) issue(buf ^ 1, k0 + (it + 1) * kBN);
+    } else {
+      // the next tile has landed (each wave waits for its own DMA)
+      dma_wait();
+      __syncthreads();
+    }
+    if (prole) {
+      if (need) m2(std::true_type{}, r0, pa, pb, sm.o[buf]);
+    } else {
+      f32x4 wv[4];
+      if (need) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) wv[u] = xw[u][lane];
+      }
+      if (needc(c + 1)) {
+        const int c1 = c + 1, r1 = 32 * (c1 & 1);
+        const short* os1 = sm.o[(c1 >> 1) & 1];
+        m1(std::false_type{}, r1, pnext[0], os1);
+        m1(std::false_type{}, r1 + 16, pnext[1], os1);
+      }
+      if (need) {
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          const f32x4 s01 = *reinterpret_cast<const f32x4*>(sm.st[buf] + r0 + 16 * hh + 4 * g);
+          const f32x4 s23 = *reinterpret_cast<const f32x4*>(sm.st[buf] + r0 + 16 * hh + 4 * g + 2);
+          const float c4v[4] = {s01[0], s01[2], s23[0], s23[2]};
+          const float ndv[4] = {s01[1], s01[3], s23[1], s23[3]};
+          uint32_t (&dp)[2][2] = hh ? pb : pa;
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks) {
+            float dv[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) dv[j] = wv[2 * hh + ks][j] * fmaf(pcur[hh][ks][j], c4v[j], ndv[j]);
+            dp[ks][0] = pack2_f16(dv[0], dv[1]);
+            dp[ks][1] = pack2_f16(dv[2], dv[3]);
+          }
+        }
+        m2(std::false_type{}, r0, pa, pb, sm.q[buf]);
+      }
+    }
   };
-  for (int it = 0; it < n_it; it += 2) {
-    step(it, std::integral_constant<int, 0>{});
-    if (it + 1 < n_it) step(it + 1, std::integral_constant<int, 1>{});
+  // unrolled by two: the D role's dP registers alternate
+  for (int c = 0; c < n_ch; c += 2) {
+    step(c, dpA, dpB);
+    if (c + 1 < n_ch) step(c + 1, dpB, dpA);
   }
 
-  T* __restrict__ dkp = (T*)a.dk + b * a.sdk[0] + h * a.sdk[1];
-  T* __restrict__ dvp = (T*)a.dv + b * a.sdv[0] + h * a.sdv[1];
+  T* __restrict__ outp = prole ? (T*)a.dv + b * a.sdv[0] + h * a.sdv[1] : (T*)a.dk + b * a.sdk[0] + h * a.sdk[1];
+  const int64_t ostr = prole ? a.sdv[2] : a.sdk[2];
+  const float osc = prole ? 1.f : scale;
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
     const int key = kw + 16 * ks + li;
     if (key < T_) {
-      T* rk = dkp + (int64_t)key * a.sdk[2];
-      T* rv = dvp + (int64_t)key * a.sdv[2];
+      T* row = outp + (int64_t)key * ostr;
 #pragma unroll
       for (int ds = 0; ds < DS; ++ds) {
-        const f32x4 kq = dkacc[ds][ks];
-        const f32x4 vq = dvacc[ds][ks];
-        *reinterpret_cast<u32x2*>(rk + 16 * ds + 4 * g) =
-            u32x2{M::pack2(kq[0] * scale, kq[1] * scale), M::pack2(kq[2] * scale, kq[3] * scale)};
-        *reinterpret_cast<u32x2*>(rv + 16 * ds + 4 * g) = u32x2{M::pack2(vq[0], vq[1]), M::pack2(vq[2], vq[3])};
+        const f32x4 v = acc[ds][ks];
+        *reinterpret_cast<u32x2*>(row + 16 * ds + 4 * g) =
+            u32x2{M::pack2(v[0] * osc, v[1] * osc), M::pack2(v[2] * osc, v[3] * osc)};
       }
     }
   }
@@ -678,7 +731,7 @@ int launch_bwd(const AttnArgs& a, void* ws, hipStream_t st) {
                      stats, q16, k16);
   if (int rc = check_launch("kat_attn_bwd (prep)")) return rc;
   const int64_t nt = (int64_t)((a.T + kBM - 1) / kBM) * a.B * a.H;
-  hipLaunchKernelGGL((attn_bwd_dkv_k<T, D>), dim3((unsigned)nt), dim3(256), 0, st, a, stats, q16);
+  hipLaunchKernelGGL((attn_bwd_dkv_k<T, D>), dim3((unsigned)nt), dim3(512), 0, st, a, stats, q16);
   if (int rc = check_launch("kat_attn_bwd (dkv, mfma)")) return rc;
   hipLaunchKernelGGL((attn_bwd_dq_k<T, D>), dim3((unsigned)nt), dim3(256), 0, st, a, stats, k16);
   return check_launch("kat_attn_bwd (dq, mfma)");
