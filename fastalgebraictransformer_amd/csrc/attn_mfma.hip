@@ -2,8 +2,9 @@
 //
 // Three kernels carry the attention math, plus a streaming prep pass:
 //   attn_fwd_k      O, L      query-tile blocks; K, V tiles stream through LDS
-//   attn_bwd_prep_k Delta, stats, fp16 copies of Q and K (row-parallel)
-//   attn_bwd_dq_k   dQ        query-tile blocks; fp16 K and V tiles stream
+//   attn_bwd_prep_k fp16 copy of K (row-parallel)
+//   attn_bwd_dq_k   dQ        query-tile blocks; fp16 K and V tiles stream; also
+//                             Delta, the row stats and the fp16 copy of Q
 //   attn_bwd_dkv_k  dK, dV    key-tile blocks; fp16 Q and dO tiles stream; the
 //                             waves split into a dV role and a dK role
 // No atomics: every output element is written by one wave, so results are
@@ -219,13 +220,11 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_k(AttnArgs a) {
 }
 
 // ============================================================================
-// Backward prep (row-parallel, D / 8 lanes per row, 8 elements per lane):
-//   Delta_i = <dO_i, O_i>,  stats_i = (4 cinv_i, -4 cinv_i Delta_i),
-//   q16 / k16 = Q / K rounded to fp16 (clamped to +-65504), [B*H][T][D].
+// Backward prep (row-parallel, 8 elements per thread): k16 = K rounded to fp16
+// (clamped to +-65504), [B*H][T][D].
 // ============================================================================
 template <typename T, int D>
-__global__ __launch_bounds__(256) void attn_bwd_prep_k(AttnArgs a, float2* __restrict__ stats,
-                                                       f16* __restrict__ q16, f16* __restrict__ k16) {
+__global__ __launch_bounds__(256) void attn_bwd_prep_k(AttnArgs a, f16* __restrict__ k16) {
   constexpr int LPR = D / 8;
   const int sub = threadIdx.x % LPR;
   const int64_t row = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / LPR;
@@ -235,23 +234,8 @@ __global__ __launch_bounds__(256) void attn_bwd_prep_k(AttnArgs a, float2* __res
   const int64_t bh = row / a.T;
   const int b = (int)(bh / a.H), h = (int)(bh % a.H);
   const int d = 8 * sub;
-  const i16x8 ov = *reinterpret_cast<const i16x8*>((const T*)a.o + b * a.so[0] + h * a.so[1] + (int64_t)i * a.so[2] + d);
-  const i16x8 gv = *reinterpret_cast<const i16x8*>((const T*)a.dout + b * a.sdo[0] + h * a.sdo[1] + (int64_t)i * a.sdo[2] + d);
-  const i16x8 qv = *reinterpret_cast<const i16x8*>((const T*)a.q + b * a.sq[0] + h * a.sq[1] + (int64_t)i * a.sq[2] + d);
   const i16x8 kv = *reinterpret_cast<const i16x8*>((const T*)a.k + b * a.sk[0] + h * a.sk[1] + (int64_t)i * a.sk[2] + d);
-  const VecT<T, 8> o8 = __builtin_bit_cast(VecT<T, 8>, ov), g8 = __builtin_bit_cast(VecT<T, 8>, gv);
-  float s = 0.f;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) s = fmaf((float)g8.v[e], (float)o8.v[e], s);
-#pragma unroll
-  for (int off = LPR / 2; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
-  *reinterpret_cast<i16x8*>(q16 + row * D + d) = to_f16x8<T>(qv);
   *reinterpret_cast<i16x8*>(k16 + row * D + d) = to_f16x8<T>(kv);
-  if (sub == 0) {
-    const float l = a.L[b * a.sl[0] + h * a.sl[1] + (int64_t)i * a.sl[2]];
-    const float c4 = 4.f / (16.f * (l + a.eps));
-    stats[row] = make_float2(c4, -c4 * s);
-  }
 }
 
 // ============================================================================
@@ -259,10 +243,13 @@ __global__ __launch_bounds__(256) void attn_bwd_prep_k(AttnArgs a, float2* __res
 //   S^T  = K16 Q16^T (+bias)  A = K16 (LDS rows)         B = Q16^T (VGPRs)
 //   dP^T = V dO^T             A = V   (LDS rows)         B = dO^T  (VGPRs)
 //   dQ^T += K16^T dS^T        A = K16^T (LDS transposed) B = dS^T  (from S^T, dP^T)
+// Each block also forms, for its own query rows, Delta_i = <dO_i, O_i> and
+// stats_i = (4 cinv_i, -4 cinv_i Delta_i), and writes stats and the fp16 copy
+// of Q (clamped to +-65504) for the dK / dV kernel, which runs after it.
 // ============================================================================
 template <typename T, int D>
-__global__ __launch_bounds__(256, 2) void attn_bwd_dq_k(AttnArgs a, const float2* __restrict__ stats,
-                                                        const f16* __restrict__ k16) {
+__global__ __launch_bounds__(256, 2) void attn_bwd_dq_k(AttnArgs a, float2* __restrict__ stats,
+                                                        f16* __restrict__ q16, const f16* __restrict__ k16) {
   typedef Mfma<T> M;
   constexpr int KK = D / 32;
   constexpr int DS = D / 16;
@@ -283,7 +270,9 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_k(AttnArgs a, const float2
   const f16* kp = k16 + (int64_t)bh * T_ * D;
   const T* vp = (const T*)a.v + b * a.sv[0] + h * a.sv[1];
   const T* dop = (const T*)a.dout + b * a.sdo[0] + h * a.sdo[1];
+  const T* op = (const T*)a.o + b * a.so[0] + h * a.so[1];
   const uint32_t sq2 = (uint32_t)a.sq[2], sv2 = (uint32_t)a.sv[2], sdo2 = (uint32_t)a.sdo[2];
+  const uint32_t so2 = (uint32_t)a.so[2];
   const uint32_t kbytes = row_bytes(T_, D, D), vbytes = row_bytes(T_, sv2, D);
   const float slope = a.slopes[h];
   const float scale = a.scale;
@@ -292,19 +281,35 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_k(AttnArgs a, const float2
   float c4[2], nc4d[2];  // 4 cinv_q and -4 cinv_q Delta_q for q = qw + 16 qs + li
   {
     const __amdgpu_buffer_rsrc_t rq = rsrc(qp, row_bytes(T_, sq2, D));
-    const __amdgpu_buffer_rsrc_t ro = rsrc(dop, row_bytes(T_, sdo2, D));
+    const __amdgpu_buffer_rsrc_t rd = rsrc(dop, row_bytes(T_, sdo2, D));
+    const __amdgpu_buffer_rsrc_t ro = rsrc(op, row_bytes(T_, so2, D));
+    const float* Lp = a.L + b * a.sl[0] + h * a.sl[1];
 #pragma unroll
     for (int qs = 0; qs < 2; ++qs) {
       const int qrow = qw + 16 * qs + li;
+      // Delta: lane (g, li) sums 32 of the row's D products, then across g
+      float dsum = 0.f;
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk) {
         qf[qs][kk] = to_f16x8<T>(load16(rq, ((uint32_t)qrow * sq2 + 32 * kk + 8 * g) * 2));
-        dof[qs][kk] = load16(ro, ((uint32_t)qrow * sdo2 + 32 * kk + 8 * g) * 2);
+        dof[qs][kk] = load16(rd, ((uint32_t)qrow * sdo2 + 32 * kk + 8 * g) * 2);
+        const i16x8 ov = load16(ro, ((uint32_t)qrow * so2 + 32 * kk + 8 * g) * 2);
+        const VecT<T, 8> o8 = __builtin_bit_cast(VecT<T, 8>, ov), g8 = __builtin_bit_cast(VecT<T, 8>, dof[qs][kk]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dsum = fmaf((float)g8.v[e], (float)o8.v[e], dsum);
       }
+      dsum += __shfl_xor(dsum, 16, 64);
+      dsum += __shfl_xor(dsum, 32, 64);
       const bool ok = qrow < T_;
-      const float2 st = stats[(int64_t)bh * T_ + (ok ? qrow : 0)];
-      c4[qs] = ok ? st.x : 0.f;
-      nc4d[qs] = ok ? st.y : 0.f;
+      const float l = ok ? Lp[(int64_t)qrow * a.sl[2]] : 0.f;
+      c4[qs] = ok ? 4.f / (16.f * (l + a.eps)) : 0.f;
+      nc4d[qs] = -c4[qs] * dsum;
+      if (ok) {
+        const int64_t r = (int64_t)bh * T_ + qrow;
+        if (g == 0) stats[r] = make_float2(c4[qs], nc4d[qs]);
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) *reinterpret_cast<i16x8*>(q16 + r * D + 32 * kk + 8 * g) = qf[qs][kk];
+      }
     }
   }
   f32x4 cb;
@@ -702,13 +707,13 @@ size_t attn_mfma_workspace(int64_t B, int64_t H, int64_t T, int64_t D) {
 
 namespace {
 
-// every tensor the kernels read through a buffer resource (q, k, v, and dO in
-// the backward) must fit 31-bit byte offsets per (b, h) slice and have
+// every tensor the kernels read through a buffer resource (q, k, v, and dO and
+// O in the backward) must fit 31-bit byte offsets per (b, h) slice and have
 // non-overlapping rows
 bool offsets_ok(const AttnArgs& a, bool bwd) {
   const int64_t lim = 0x7fffffffLL;
-  const int64_t* s2[4] = {&a.sq[2], &a.sk[2], &a.sv[2], &a.sdo[2]};
-  for (int t = 0; t < (bwd ? 4 : 3); ++t)
+  const int64_t* s2[5] = {&a.sq[2], &a.sk[2], &a.sv[2], &a.sdo[2], &a.so[2]};
+  for (int t = 0; t < (bwd ? 5 : 3); ++t)
     if (*s2[t] < a.D || ((int64_t)a.T + kBM) * *s2[t] * 2 > lim) return false;
   return (int64_t)a.T * a.D * 2 < lim && (int64_t)a.T * 8 < lim;
 }
@@ -728,13 +733,14 @@ int launch_bwd(const AttnArgs& a, void* ws, hipStream_t st) {
   f16* k16 = reinterpret_cast<f16*>(reinterpret_cast<char*>(q16) + al(rows * D * sizeof(f16)));
   constexpr int rpb = 256 / (D / 8);
   hipLaunchKernelGGL((attn_bwd_prep_k<T, D>), dim3((unsigned)((rows + rpb - 1) / rpb)), dim3(256), 0, st, a,
-                     stats, q16, k16);
+                     k16);
   if (int rc = check_launch("kat_attn_bwd (prep)")) return rc;
+  // dq also writes stats and q16, which the dK / dV kernel reads
   const int64_t nt = (int64_t)((a.T + kBM - 1) / kBM) * a.B * a.H;
+  hipLaunchKernelGGL((attn_bwd_dq_k<T, D>), dim3((unsigned)nt), dim3(256), 0, st, a, stats, q16, k16);
+  if (int rc = check_launch("kat_attn_bwd (dq, mfma)")) return rc;
   hipLaunchKernelGGL((attn_bwd_dkv_k<T, D>), dim3((unsigned)nt), dim3(512), 0, st, a, stats, q16);
-  if (int rc = check_launch("kat_attn_bwd (dkv, mfma)")) return rc;
-  hipLaunchKernelGGL((attn_bwd_dq_k<T, D>), dim3((unsigned)nt), dim3(256), 0, st, a, stats, k16);
-  return check_launch("kat_attn_bwd (dq, mfma)");
+  return check_launch("kat_attn_bwd (dkv, mfma)");
 }
 
 }  // namespace
