@@ -10,7 +10,9 @@ throughput 7*B*H*S^2*D / step time in TFLOP/s. The same JSON line carries:
                  inside the timed region, against the dense bf16 MFMA peak;
   * fused_ops -- HBM GB/s of mean_error_norm, rational_swiglu and
                  rational_softmax fwd+bwd at their benchmark shapes (bf16),
-                 with the 256 MB last-level cache flushed before each rep;
+                 with the 256 MB last-level cache flushed before each rep
+                 by reading (not writing) a 512 MB buffer, so no dirty lines
+                 of the flush are written back inside the timed region;
   * cpu_baseline -- the CPU oracle (fp32) on a bounded sample of the same
                  workload (one (b, h) head), on this host's cores;
   * device     -- CU count, a measured bf16 MFMA loop rate (beside the 2.5 PF
@@ -181,13 +183,13 @@ def bench_fused(torch, F, reps=10):
     dev = torch.device("cuda:0")
     bf = torch.bfloat16
     g = torch.Generator().manual_seed(1)
-    flush = torch.empty(512 * 1024 * 1024 // 4, dtype=torch.float32, device=dev)
+    flush = torch.ones(512 * 1024 * 1024 // 4, dtype=torch.float32, device=dev)
     res = {}
 
     def timed(fn):
         ts = []
         for _ in range(reps + 2):
-            flush.fill_(1.0)
+            flush.sum()
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record()
             fn()
