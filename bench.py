@@ -19,9 +19,11 @@ throughput 7*B*H*S^2*D / step time in TFLOP/s. The same JSON line carries:
                  spec peak) and a measured 1 GiB device-copy bandwidth;
   * model_step -- one training step (bf16 autocast forward + loss + backward,
                  no optimizer) of the 109.5 M-parameter model at batch 16 x 2048
-                 (reported, not the metric): tokens/s and MFU.
+                 (reported, not the metric): tokens/s and MFU; with --model-large
+                 also the 1.3 B-parameter model at batch 2 x 8192.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-fused]
+                       [--no-model] [--model-large]
        python bench.py --copy-calibration   (one plain 1 GiB device copy, for
                                              scaling HBM byte counters)
 """
@@ -136,17 +138,29 @@ def device_info(torch, lib):
             "hbm_spec_GBs": PEAK_HBM_GBS}
 
 
-def bench_model_step(torch, steps=5, warmup=2):
-    """Config-4 training step: AlgebraicTransformerLM(32000, 768, 12, 12), batch
-    16 x 2048, bf16 autocast forward + cross-entropy, backward (no optimizer)."""
+MODEL_CONFIGS = {
+    # config 4: the ~125M model, batch 16 x 2048 (default bench)
+    "small": dict(vocab=32000, d_model=768, n_head=12, n_layers=12, d_ffn=None, batch=16, seq=2048),
+    # config 5: the ~1.3B decoder at long context, batch 2 x 8192 (--model-large)
+    "large": dict(vocab=50000, d_model=2048, n_head=16, n_layers=24, d_ffn=5632, batch=2, seq=8192),
+}
+
+
+def bench_model_step(torch, which="small", steps=5, warmup=2):
+    """Training step of AlgebraicTransformerLM at a model config: bf16 autocast
+    forward + cross-entropy, backward (no optimizer); random init from seed 0,
+    token ids and labels uniform in [0, vocab)."""
     from fastalgebraictransformer_amd.algebraic_model import AlgebraicTransformerLM
+    c = MODEL_CONFIGS[which]
     dev = torch.device("cuda:0")
     torch.manual_seed(0)
-    model = AlgebraicTransformerLM(32000, 768, 12, 12).to(dev)
+    model = AlgebraicTransformerLM(c["vocab"], c["d_model"], c["n_head"], c["n_layers"], d_ffn=c["d_ffn"],
+                                   block_size=c["seq"]).to(dev)
     model.train()
     g = torch.Generator().manual_seed(0)
-    ids = torch.randint(0, 32000, (16, 2048), generator=g).to(dev)
-    labels = torch.randint(0, 32000, (16, 2048), generator=g).to(dev)
+    B, S = c["batch"], c["seq"]
+    ids = torch.randint(0, c["vocab"], (B, S), generator=g).to(dev)
+    labels = torch.randint(0, c["vocab"], (B, S), generator=g).to(dev)
 
     def step():
         model.zero_grad(set_to_none=True)
@@ -165,15 +179,19 @@ def bench_model_step(torch, steps=5, warmup=2):
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
     params = sum(p.numel() for p in model.parameters())
-    # 6 N per token for the dense layers, plus causal attention fwd+bwd = 7 B H S^2 D
-    # per layer (12 layers): 25.86 TFLOP per step at this shape
-    flops = 6 * params * 16 * 2048 + 12 * 7 * 16 * 12 * 2048 * 2048 * 64
-    del model
+    peak_gib = torch.cuda.max_memory_allocated() / 2 ** 30
+    # 6 N per token for the dense layers, plus causal attention fwd+bwd =
+    # 7 B H S^2 D per layer (config 4: 25.86 TFLOP per step)
+    D = c["d_model"] // c["n_head"]
+    flops = 6 * params * B * S + c["n_layers"] * 7 * B * c["n_head"] * S * S * D
+    del model, ids, labels
     torch.cuda.empty_cache()
-    return {"model": "AlgebraicTransformerLM(32000, 768, 12, 12)", "params": params,
-            "batch": [16, 2048], "ms_per_step": round(ms, 3),
-            "tokens_per_s": round(16 * 2048 / (ms * 1e-3), 1),
+    name = f"AlgebraicTransformerLM({c['vocab']}, {c['d_model']}, {c['n_head']}, {c['n_layers']}" + (
+        f", d_ffn={c['d_ffn']})" if c["d_ffn"] else ")")
+    return {"model": name, "params": params, "batch": [B, S], "ms_per_step": round(ms, 3),
+            "tokens_per_s": round(B * S / (ms * 1e-3), 1),
             "tflops_step": round(flops / 1e12, 2), "mfu": round(flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+            "peak_mem_gib": round(peak_gib, 1),
             "note": "reported, not the metric; dropout 0.1 (model default)"}
 
 
@@ -287,6 +305,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-fused", action="store_true")
     ap.add_argument("--no-model", action="store_true", help="skip the model training step")
+    ap.add_argument("--model-large", action="store_true",
+                    help="also time the ~1.3B model step (batch 2 x 8192, ~55 GB; reported only)")
     ap.add_argument("--no-device", action="store_true", help="skip the MFMA / copy probes")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain device-to-device copy of 1 GiB (3 times): the "
@@ -354,7 +374,9 @@ def main():
     if not args.no_device:
         line["device"] = device_info(torch, _lib.load())
     if not args.no_model:
-        line["model_step"] = bench_model_step(torch)
+        line["model_step"] = bench_model_step(torch, "small")
+    if args.model_large:
+        line["model_step_large"] = bench_model_step(torch, "large", steps=3, warmup=1)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(torch)
         line["cpu_baseline"]["value"] = round(line["cpu_baseline"]["value"], 5)

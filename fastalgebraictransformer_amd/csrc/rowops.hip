@@ -4,10 +4,11 @@
 // Design (MI355X): these ops do a handful of flops per byte, so the only
 // roofline that matters is HBM (8 TB/s). Every kernel touches each tensor
 // exactly once:
-//   * row-resident kernels (softmax, norm): one 64-lane wavefront owns a row,
-//     holds it in registers as packed 16-byte vectors, reduces with cross-lane
-//     shuffles and writes the result -- one HBM pass where the reference makes
-//     two (fused_ops.py:74-106, 319-342, 395-423);
+//   * row-resident kernels (softmax, norm): a 256-thread block owns a row at a
+//     time, holds it in registers as packed 16-byte vectors, reduces with
+//     wavefront shuffles plus a 4-entry LDS exchange and writes the result --
+//     one HBM pass where the reference makes two (fused_ops.py:74-106,
+//     319-342, 395-423);
 //   * SwiGLU is a flat elementwise stream of 16-byte vectors with row strides,
 //     so gate/value can be the two halves of one packed buffer;
 //   * the norm backward folds the weight gradient (torch ops at
