@@ -20,12 +20,20 @@ from .fused_ops import (
     MeanErrorNorm,
     RationalSoftmax,
     RationalSwiGLU,
+    PackedRationalSwiGLU,
     mean_error_norm,
     rational_softmax,
     rational_swiglu,
+    rational_swiglu_packed,
 )
 from .forward import compute_alibi_slopes, rational_attention_forward
-from .backward import RationalAttentionFunction, rational_attention, rational_attention_backward
+from .backward import (
+    PackedRationalAttention,
+    RationalAttentionFunction,
+    rational_attention,
+    rational_attention_backward,
+    rational_attention_packed,
+)
 from .algebraic_model import (
     AlgebraicAttention,
     AlgebraicBlock,
@@ -58,6 +66,10 @@ __all__ = [
     "create_medium_model",
     "create_large_model",
 ]
+# Importable extensions beyond the reference surface (kept out of __all__):
+# rational_attention_packed / PackedRationalAttention on a packed [B, T, 3, H, D]
+# projection and rational_swiglu_packed / PackedRationalSwiGLU on a packed
+# [..., 2F] gate|value buffer -- the model's layouts, same kernels.
 
 
 def install_as(name="kernels"):

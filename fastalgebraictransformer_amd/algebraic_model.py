@@ -17,9 +17,9 @@ import torch.nn as nn
 import torch.nn.functional as F
 from torch.utils.checkpoint import checkpoint
 
-from .backward import rational_attention
+from .backward import rational_attention_packed
 from .forward import compute_alibi_slopes
-from .fused_ops import EPS, mean_error_norm, rational_softmax, rational_swiglu
+from .fused_ops import EPS, mean_error_norm, rational_softmax, rational_swiglu_packed
 
 
 class RationalMR(nn.Module):
@@ -46,8 +46,9 @@ class RationalSwiGLU(nn.Module):
         self.dropout = nn.Dropout(dropout)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        gate, value = self.w_gate_val(x).chunk(2, dim=-1)
-        return self.dropout(self.w_out(rational_swiglu(gate, value)))
+        # gate, value = w_gate_val(x).chunk(2, dim=-1), read in place from the
+        # packed projection (its gradient is written as one buffer as well)
+        return self.dropout(self.w_out(rational_swiglu_packed(self.w_gate_val(x))))
 
 
 class AlgebraicAttention(nn.Module):
@@ -68,16 +69,16 @@ class AlgebraicAttention(nn.Module):
 
     def forward(self, x: torch.Tensor, mask: Optional[torch.Tensor] = None) -> torch.Tensor:
         B, T, C = x.shape
-        # [B, T, 3, H, D] -> three strided [B, H, T, D] views (no copies: the
-        # kernels take (b, h, t) strides)
-        q, k, v = self.qkv(x).view(B, T, 3, self.n_head, self.d_head).permute(2, 0, 3, 1, 4)
+        qkv = self.qkv(x).view(B, T, 3, self.n_head, self.d_head)
         if x.is_cuda:
             # like the reference GPU path (algebraic_model.py:93-101) the
-            # padding mask is not applied here; attention is always causal
-            y = rational_attention(q, k, v, self.alibi_slopes, self.scale, causal=True, eps=EPS)
+            # padding mask is not applied here; attention is always causal.
+            # The kernels read q, k, v in place from the packed projection and
+            # write the output as [B, T, H, D], so no layout copies are made.
+            y = rational_attention_packed(qkv, self.alibi_slopes, self.scale, eps=EPS).view(B, T, C)
         else:
-            y = self._cpu_attention(q, k, v, mask)
-        y = y.transpose(1, 2).contiguous().view(B, T, C)
+            q, k, v = qkv.permute(2, 0, 3, 1, 4)
+            y = self._cpu_attention(q, k, v, mask).transpose(1, 2).contiguous().view(B, T, C)
         return self.dropout(self.out(y))
 
     def _cpu_attention(self, q, k, v, mask):

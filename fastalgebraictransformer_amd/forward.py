@@ -40,6 +40,22 @@ def _unit_d(t):
     return t if t.stride(-1) == 1 or t.shape[-1] == 1 else t.contiguous()
 
 
+def _attn_fwd_into(q, k, v, out, L, alibi_slopes, scale, causal, eps):
+    """Launch kat_attn_fwd on [B,H,T,D] q, k, v and out (any (b, h, t) strides,
+    unit d-stride) and L [B,H,T] fp32."""
+    lib = _lib.load()
+    B, H, T, D = q.shape
+    slopes = alibi_slopes.to(device=q.device, dtype=torch.float32).contiguous()
+    assert slopes.numel() == H, "alibi_slopes must have n_heads entries"
+    strides = _lib.i64_array(_bht_strides(q) + _bht_strides(k) + _bht_strides(v) +
+                             _bht_strides(out))
+    lstr = _lib.i64_array(_bht_strides(L))
+    _lib.check(lib.kat_attn_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                                L.data_ptr(), slopes.data_ptr(), B, H, T, D, strides, lstr,
+                                float(scale), float(eps), int(bool(causal)),
+                                _lib.dtype_code(q), _lib.stream(q)), "kat_attn_fwd")
+
+
 def rational_attention_forward(q, k, v, alibi_slopes, scale, causal=True, eps=EPS):
     """Returns (output [B,H,T,D] in q's dtype, L [B,H,T] fp32 without eps).
 
@@ -48,20 +64,11 @@ def rational_attention_forward(q, k, v, alibi_slopes, scale, causal=True, eps=EP
     stride (no copies are made for them)."""
     assert q.is_cuda and k.is_cuda and v.is_cuda
     assert q.shape == k.shape == v.shape
-    lib = _lib.load()
     B, H, T, D = q.shape
     k = k.to(q.dtype)
     v = v.to(q.dtype)
     q, k, v = _unit_d(q), _unit_d(k), _unit_d(v)
-    slopes = alibi_slopes.to(device=q.device, dtype=torch.float32).contiguous()
-    assert slopes.numel() == H, "alibi_slopes must have n_heads entries"
     out = torch.empty((B, H, T, D), dtype=q.dtype, device=q.device)
     L = torch.empty((B, H, T), dtype=torch.float32, device=q.device)
-    strides = _lib.i64_array(_bht_strides(q) + _bht_strides(k) + _bht_strides(v) +
-                             _bht_strides(out))
-    lstr = _lib.i64_array(_bht_strides(L))
-    _lib.check(lib.kat_attn_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
-                                L.data_ptr(), slopes.data_ptr(), B, H, T, D, strides, lstr,
-                                float(scale), float(eps), int(bool(causal)),
-                                _lib.dtype_code(q), _lib.stream(q)), "kat_attn_fwd")
+    _attn_fwd_into(q, k, v, out, L, alibi_slopes, scale, causal, eps)
     return out, L

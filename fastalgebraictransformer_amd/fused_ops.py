@@ -96,6 +96,46 @@ class RationalSwiGLU(torch.autograd.Function):
         return dgate.view(gate.shape), dvalue.view(gate.shape)
 
 
+class PackedRationalSwiGLU(torch.autograd.Function):
+    """SwiGLU on a packed [..., 2F] buffer whose halves are (gate | value): the
+    model's single gate/value projection. An extension beyond the reference
+    API, used by the model's FFN. The forward reads both halves in place; the
+    backward writes d(gate | value) into one [..., 2F] gradient, so autograd
+    does not concatenate two separate gradients (the reference's chunk path,
+    algebraic_model.py:52-53 with fused_ops.py:498-499,522-528, copies both).
+    Same kernels and results as RationalSwiGLU on the two halves."""
+
+    @staticmethod
+    def forward(ctx, gv):
+        assert gv.is_cuda, "Input must be on CUDA"
+        assert gv.shape[-1] % 2 == 0, "the last dim holds gate and value halves"
+        lib = _lib.load()
+        g2, ld = _lib.rows2d(gv)
+        rows, two_f = g2.shape
+        f = two_f // 2
+        out = torch.empty((rows, f), dtype=gv.dtype, device=gv.device)
+        vptr = _ptr(g2) + f * g2.element_size()
+        _lib.check(lib.kat_rswiglu_fwd(_ptr(g2), vptr, _ptr(out), rows, f, ld, ld, f,
+                                       _lib.dtype_code(gv), _lib.stream(gv)), "kat_rswiglu_fwd")
+        ctx.save_for_backward(gv)
+        return out.view(*gv.shape[:-1], f)
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        (gv,) = ctx.saved_tensors
+        lib = _lib.load()
+        g2, ld = _lib.rows2d(gv)
+        rows, two_f = g2.shape
+        f = two_f // 2
+        y2, ldy = _lib.rows2d(grad_output.to(gv.dtype))
+        dgv = torch.empty((rows, two_f), dtype=gv.dtype, device=gv.device)
+        es = g2.element_size()
+        _lib.check(lib.kat_rswiglu_bwd(_ptr(y2), _ptr(g2), _ptr(g2) + f * es, _ptr(dgv),
+                                       _ptr(dgv) + f * es, rows, f, ldy, ld, ld, two_f, two_f,
+                                       _lib.dtype_code(gv), _lib.stream(gv)), "kat_rswiglu_bwd")
+        return dgv.view(gv.shape)
+
+
 def _weight_for(x, weight):
     """The kernels take the weight as fp32 or in x's dtype, contiguous."""
     if weight.dtype != x.dtype and not (weight.dtype == torch.float32 and x.dtype != torch.float64):
@@ -168,3 +208,12 @@ def mean_error_norm(x, weight, eps=EPS):
         return MeanErrorNorm.apply(x, weight, eps)
     m = x.abs().mean(dim=-1, keepdim=True)
     return (x / (m + eps)) * weight
+
+
+def rational_swiglu_packed(gv):
+    """gate * sigma(gate) * value with gate, value = gv.chunk(2, dim=-1)
+    (see PackedRationalSwiGLU); CPU tensors use the reference formula."""
+    if gv.is_cuda:
+        return PackedRationalSwiGLU.apply(gv)
+    gate, value = gv.chunk(2, dim=-1)
+    return rational_swiglu(gate, value)
