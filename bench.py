@@ -229,7 +229,32 @@ def bench_fused(torch, F, reps=10):
     nbytes = (2 * N * C * 2 + C * 4 + N * 4) + (3 * N * C * 2 + 2 * C * 4 + N * 4)
     t = timed(norm_step)
     res["mean_error_norm"] = dict(shape=[N, C], ms=t, bytes=nbytes, GBs=nbytes / t / 1e6)
-    del x, w, dy
+    del x, dy
+
+    # residual add fused with the norm: fp32 stream x [16384, 4096] plus a
+    # bf16 branch r (the model under autocast); beside it the unfused pair
+    # (torch add, then the norm) it replaces
+    xs = torch.randn(N, C, generator=g).to(dev).requires_grad_(True)
+    rb = torch.randn(N, C, generator=g).to(bf).to(dev).requires_grad_(True)
+    dh = torch.randn(N, C, generator=g).to(dev)
+    dy = torch.randn(N, C, generator=g).to(dev)
+
+    def add_norm_step():
+        xs.grad = rb.grad = w.grad = None
+        h, y = F.add_mean_error_norm(xs, rb, w)
+        torch.autograd.backward([h, y], [dh, dy])
+
+    def add_then_norm_step():
+        xs.grad = rb.grad = w.grad = None
+        h = xs + rb
+        torch.autograd.backward([h, F.mean_error_norm(h, w)], [dh, dy])
+    # fwd: x, r read, h, y written; bwd: dy, dh, h read, dx, dr written
+    nbytes = N * C * (4 + 2 + 4 + 4) + N * C * (4 + 4 + 4 + 4 + 2) + 3 * C * 4 + 2 * N * 4
+    t = timed(add_norm_step)
+    t_unfused = timed(add_then_norm_step)
+    res["add_mean_error_norm"] = dict(shape=[N, C], ms=t, bytes=nbytes, GBs=nbytes / t / 1e6,
+                                      unfused_ms=t_unfused)
+    del xs, rb, dh, dy, w
 
     # rational_swiglu: gate, value [16384, 11008] bf16
     N, C = 16384, 11008

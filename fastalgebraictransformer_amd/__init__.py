@@ -21,6 +21,8 @@ from .fused_ops import (
     RationalSoftmax,
     RationalSwiGLU,
     PackedRationalSwiGLU,
+    ResidualMeanErrorNorm,
+    add_mean_error_norm,
     mean_error_norm,
     rational_softmax,
     rational_swiglu,
@@ -69,7 +71,9 @@ __all__ = [
 # Importable extensions beyond the reference surface (kept out of __all__):
 # rational_attention_packed / PackedRationalAttention on a packed [B, T, 3, H, D]
 # projection and rational_swiglu_packed / PackedRationalSwiGLU on a packed
-# [..., 2F] gate|value buffer -- the model's layouts, same kernels.
+# [..., 2F] gate|value buffer -- the model's layouts, same kernels; and
+# add_mean_error_norm / ResidualMeanErrorNorm, the residual add fused with the
+# norm that reads it.
 
 
 def install_as(name="kernels"):

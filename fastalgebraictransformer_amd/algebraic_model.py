@@ -19,7 +19,8 @@ from torch.utils.checkpoint import checkpoint
 
 from .backward import rational_attention_packed
 from .forward import compute_alibi_slopes
-from .fused_ops import EPS, mean_error_norm, rational_softmax, rational_swiglu_packed
+from .fused_ops import (EPS, add_mean_error_norm, mean_error_norm, rational_softmax,
+                        rational_swiglu_packed)
 
 
 class RationalMR(nn.Module):
@@ -107,8 +108,21 @@ class AlgebraicBlock(nn.Module):
         self.norm2 = RationalMR(d_model)
 
     def forward(self, x: torch.Tensor, mask: Optional[torch.Tensor] = None) -> torch.Tensor:
-        h = x + self.attn(self.norm1(x), mask)
-        return h + self.ffn(self.norm2(h))
+        h, f = self.forward_pending(x, None, mask)
+        return h + f
+
+    def forward_pending(self, x: torch.Tensor, r: Optional[torch.Tensor],
+                        mask: Optional[torch.Tensor] = None):
+        """The block on the stream ``x + r`` (``r`` None: just ``x``), returning
+        ``(h, f)`` with the block's output being ``h + f``. Each residual add
+        is left to the norm that reads its result, which fuses the two
+        (add_mean_error_norm), so the stream is read and written once per add."""
+        if r is None:
+            h0, n1 = x, self.norm1(x)
+        else:
+            h0, n1 = add_mean_error_norm(x, r, self.norm1.weight, self.norm1.eps)
+        h, n2 = add_mean_error_norm(h0, self.attn(n1, mask), self.norm2.weight, self.norm2.eps)
+        return h, self.ffn(n2)
 
 
 class AlgebraicTransformerLM(nn.Module):
@@ -160,12 +174,19 @@ class AlgebraicTransformerLM(nn.Module):
         attention_mask: Optional[torch.Tensor] = None,
     ) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
         x = self.embed(input_ids)
+        # the stream is carried as (x, r), x + r being the reference's x after
+        # each block, so that every residual add fuses into the next norm
+        r = None
         for block in self.blocks:
             if self.gradient_checkpointing and self.training:
-                x = checkpoint(block, x, attention_mask, use_reentrant=False)
+                x, r = checkpoint(block.forward_pending, x, r, attention_mask, use_reentrant=False)
             else:
-                x = block(x, attention_mask)
-        logits = self.head(self.norm(x))
+                x, r = block.forward_pending(x, r, attention_mask)
+        if r is None:
+            normed = self.norm(x)
+        else:
+            _, normed = add_mean_error_norm(x, r, self.norm.weight, self.norm.eps)
+        logits = self.head(normed)
         loss = None
         if labels is not None:
             # next-token loss: position t predicts token t+1

@@ -428,13 +428,55 @@ __global__ __launch_bounds__(256) void rsoftmax_bwd_mp_k(const T* __restrict__ d
 // mean-error norm -- fused_ops.py:295-423 (+ dgamma, fused_ops.py:593-597)
 // ============================================================================
 
-template <typename T, typename W, int NCH>
+// Vectors of V elements of type R (the residual branch may be narrower than
+// the residual stream: 8-byte loads of 4 bf16 beside 16-byte loads of 4 fp32).
+template <typename R, int V>
+__device__ __forceinline__ VecT<R, V> ld_vec_any(const R* __restrict__ p) {
+  if constexpr (sizeof(VecT<R, V>) == 16) {
+    return ld_vec<R, V>(p);
+  } else {
+    static_assert(sizeof(VecT<R, V>) == 8, "8- or 16-byte vectors");
+    typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+    const u32x2_t r = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(p));
+    return __builtin_bit_cast(VecT<R, V>, r);
+  }
+}
+template <typename R, int V>
+__device__ __forceinline__ void st_vec_any(R* __restrict__ p, const VecT<R, V>& v) {
+  if constexpr (sizeof(VecT<R, V>) == 16) {
+    st_vec<R, V>(p, v);
+  } else {
+    static_assert(sizeof(VecT<R, V>) == 8, "8- or 16-byte vectors");
+    typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+    __builtin_nontemporal_store(__builtin_bit_cast(u32x2_t, v), reinterpret_cast<u32x2_t*>(p));
+  }
+}
+template <typename R, int V, int NCH>
+__device__ __forceinline__ void load_row_any(const R* __restrict__ base, int n_cols,
+                                             VecT<R, V> (&r)[NCH]) {
+#pragma unroll
+  for (int k = 0; k < NCH; ++k) {
+    const int col = ((int)threadIdx.x + 256 * k) * V;
+    r[k] = ld_vec_any<R, V>(base + (col < n_cols ? col : 0));
+  }
+}
+
+// R = void: y = norm(x). Otherwise the residual add in front of the norm is
+// fused in (the block's `x = x + branch(...)` followed by norm2 / the next
+// norm1, algebraic_model.py:150-151): h = x + r is rounded to T exactly as
+// torch's promoted add rounds it, written once, and normalised from registers,
+// so (h, y, mu) are bit-identical to the add followed by the plain norm.
+template <typename T, typename W, int NCH, typename R = void>
 __global__ __launch_bounds__(256) void men_fwd_k(const T* __restrict__ x, const W* __restrict__ w,
                                                  T* __restrict__ y, float* __restrict__ mu,
                                                  int64_t n_rows, int n_cols, int64_t ldx,
-                                                 int64_t ldy, float eps) {
+                                                 int64_t ldy, float eps, const void* __restrict__ rp,
+                                                 T* __restrict__ h, int64_t ldr, int64_t ldh) {
   typedef typename AccT<T>::type A;
   constexpr int V = Raw<T>::V;
+  constexpr bool kAdd = !std::is_void<R>::value;
+  typedef std::conditional_t<kAdd, R, T> RT;
+  const RT* r = reinterpret_cast<const RT*>(rp);
   __shared__ A red[2][kRowWaves];
   A wv[NCH][V];
   load_weight<T, W, NCH>(w, n_cols, wv);
@@ -442,11 +484,26 @@ __global__ __launch_bounds__(256) void men_fwd_k(const T* __restrict__ x, const 
   int64_t row = blockIdx.x;
   const int64_t last = n_rows - 1;
   VecT<T, V> cur[NCH], nx1[NCH];
+  VecT<RT, V> rc[NCH], r1[NCH];
   load_row<T, NCH>(x + std::min(row, last) * ldx, n_cols, cur);
+  if constexpr (kAdd) load_row_any<RT, V, NCH>(r + std::min(row, last) * ldr, n_cols, rc);
   load_row<T, NCH>(x + std::min(row + G, last) * ldx, n_cols, nx1);
+  if constexpr (kAdd) load_row_any<RT, V, NCH>(r + std::min(row + G, last) * ldr, n_cols, r1);
   for (int par = 0; row < n_rows; row += G, par ^= 1) {
     VecT<T, V> nx2[NCH];
+    VecT<RT, V> r2[NCH];
     load_row<T, NCH>(x + std::min(row + 2 * G, last) * ldx, n_cols, nx2);
+    if constexpr (kAdd) {
+      load_row_any<RT, V, NCH>(r + std::min(row + 2 * G, last) * ldr, n_cols, r2);
+#pragma unroll
+      for (int k = 0; k < NCH; ++k) {
+        const int col = ((int)threadIdx.x + 256 * k) * V;
+#pragma unroll
+        for (int i = 0; i < V; ++i)
+          cur[k].v[i] = from_acc<T>(to_acc(cur[k].v[i]) + to_acc(rc[k].v[i]));
+        if (col < n_cols) st_vec<T, V>(h + row * ldh + col, cur[k]);
+      }
+    }
     A s = A(0);
 #pragma unroll
     for (int k = 0; k < NCH; ++k) {
@@ -472,6 +529,10 @@ __global__ __launch_bounds__(256) void men_fwd_k(const T* __restrict__ x, const 
     for (int k = 0; k < NCH; ++k) {
       cur[k] = nx1[k];
       nx1[k] = nx2[k];
+      if constexpr (kAdd) {
+        rc[k] = r1[k];
+        r1[k] = r2[k];
+      }
     }
   }
 }
@@ -481,14 +542,23 @@ __global__ __launch_bounds__(256) void men_fwd_k(const T* __restrict__ x, const 
 // Each block keeps kNormPf rows in flight ahead of the one it is reducing.
 constexpr int kNormPf = 2;
 
-template <typename T, typename W, int NCH>
+// R = void: the norm's backward. Otherwise the backward of the fused
+// residual add + norm: x is then h = x + r, dh the gradient that reaches h
+// through the residual stream, and dx = round_T(norm_bwd) + dh (the sum
+// autograd forms for h, in T), written for x and, cast to R, for r (dr may
+// be null).
+template <typename T, typename W, int NCH, typename R = void>
 __global__ __launch_bounds__(256) void men_bwd_k(
     const T* __restrict__ dy, const T* __restrict__ x, const W* __restrict__ w,
     const float* __restrict__ mu, T* __restrict__ dx, typename AccT<T>::type* __restrict__ partial,
-    int64_t n_rows, int n_cols, int64_t lddy, int64_t ldx, int64_t lddx, float eps) {
+    int64_t n_rows, int n_cols, int64_t lddy, int64_t ldx, int64_t lddx, float eps,
+    const T* __restrict__ dh, int64_t lddh, void* __restrict__ drp, int64_t lddr) {
   typedef typename AccT<T>::type A;
   constexpr int V = Raw<T>::V;
   constexpr int PF = kNormPf;
+  constexpr bool kAdd = !std::is_void<R>::value;
+  typedef std::conditional_t<kAdd, R, T> RT;
+  RT* dr = reinterpret_cast<RT*>(drp);
   __shared__ A red[2][kRowWaves];
   A wv[NCH][V], dg[NCH][V];
   load_weight<T, W, NCH>(w, n_cols, wv);
@@ -500,7 +570,7 @@ __global__ __launch_bounds__(256) void men_bwd_k(
   const int64_t G = gridDim.x;
   int64_t row = blockIdx.x;
   // ring of rows row, row + G, ..., row + PF*G: slot 0 is reduced next
-  VecT<T, V> by[PF + 1][NCH], bx[PF + 1][NCH];
+  VecT<T, V> by[PF + 1][NCH], bx[PF + 1][NCH], bh[PF + 1][NCH];
   float bm[PF + 1];
   // Rows past the end are clamped to the last row (loaded, never used):
   // a conditional load would make the compiler wait for it on the spot.
@@ -510,6 +580,7 @@ __global__ __launch_bounds__(256) void men_bwd_k(
     const int64_t r = std::min(row + j * G, last);
     load_row<T, NCH>(dy + r * lddy, n_cols, by[j]);
     load_row<T, NCH>(x + r * ldx, n_cols, bx[j]);
+    if constexpr (kAdd) load_row<T, NCH>(dh + r * lddh, n_cols, bh[j]);
     bm[j] = mu[r];  // the row statistic travels with its row
   }
   for (int par = 0; row < n_rows; row += G, par ^= 1) {
@@ -517,6 +588,7 @@ __global__ __launch_bounds__(256) void men_bwd_k(
       const int64_t r = std::min(row + PF * G, last);
       load_row<T, NCH>(dy + r * lddy, n_cols, by[PF]);
       load_row<T, NCH>(x + r * ldx, n_cols, bx[PF]);
+      if constexpr (kAdd) load_row<T, NCH>(dh + r * lddh, n_cols, bh[PF]);
       bm[PF] = mu[r];
     }
     const A inv = A(1) / ((A)bm[0] + e);  // fused_ops.py:389-390
@@ -540,9 +612,18 @@ __global__ __launch_bounds__(256) void men_bwd_k(
         const A yy = to_acc(by[0][k].v[i]);
         const A xx = to_acc(bx[0][k].v[i]);
         o.v[i] = from_acc<T>(yy * wv[k][i] * inv - sign_of(xx) * corr * inv);  // :418-421
+        if constexpr (kAdd) o.v[i] = from_acc<T>(to_acc(o.v[i]) + to_acc(bh[0][k].v[i]));
         dg[k][i] += in ? yy * (xx * inv) : A(0);  // fused_ops.py:595-597
       }
       if (in) st_vec<T, V>(dx + row * lddx + col, o);
+      if constexpr (kAdd) {
+        if (in && dr != nullptr) {
+          VecT<RT, V> od;
+#pragma unroll
+          for (int i = 0; i < V; ++i) od.v[i] = from_acc<RT>(to_acc(o.v[i]));
+          st_vec_any<RT, V>(dr + row * lddr + col, od);
+        }
+      }
     }
 #pragma unroll
     for (int j = 0; j < PF; ++j) {
@@ -551,6 +632,7 @@ __global__ __launch_bounds__(256) void men_bwd_k(
       for (int k = 0; k < NCH; ++k) {
         by[j][k] = by[j + 1][k];
         bx[j][k] = bx[j + 1][k];
+        if constexpr (kAdd) bh[j][k] = bh[j + 1][k];
       }
     }
   }
@@ -563,33 +645,51 @@ __global__ __launch_bounds__(256) void men_bwd_k(
   }
 }
 
-template <typename T>
+// h = x + r (R non-void) is formed in the first pass, written, and formed
+// again from x and r in the second (the same rounding, so the same value).
+template <typename T, typename R = void>
 __global__ __launch_bounds__(256) void men_fwd_mp_k(const T* __restrict__ x, const void* __restrict__ wp,
                                                     int w_is_f32, T* __restrict__ y,
                                                     float* __restrict__ mu, int64_t n_rows,
                                                     int n_cols, int64_t ldx, int64_t ldy,
-                                                    float eps) {
+                                                    float eps, const void* __restrict__ rp,
+                                                    T* __restrict__ h, int64_t ldr, int64_t ldh) {
   typedef typename AccT<T>::type A;
+  constexpr bool kAdd = !std::is_void<R>::value;
+  typedef std::conditional_t<kAdd, R, T> RT;
+  const RT* r = reinterpret_cast<const RT*>(rp);
   __shared__ A sh[kRowWaves];
   const int64_t row = blockIdx.x;
+  auto xin = [&](int c) -> T {
+    if constexpr (kAdd) return from_acc<T>(to_acc(x[row * ldx + c]) + to_acc(r[row * ldr + c]));
+    else return x[row * ldx + c];
+  };
   A s = A(0);
-  for (int c = threadIdx.x; c < n_cols; c += blockDim.x) s += fabs(to_acc(x[row * ldx + c]));
+  for (int c = threadIdx.x; c < n_cols; c += blockDim.x) {
+    const T xv = xin(c);
+    if constexpr (kAdd) h[row * ldh + c] = xv;
+    s += fabs(to_acc(xv));
+  }
   s = block_sum(s, sh);
   const A mean = s / A(n_cols);
   const A inv = A(1) / (mean + A(eps));
   if (threadIdx.x == 0) mu[row] = (float)mean;
   for (int c = threadIdx.x; c < n_cols; c += blockDim.x) {
     const A wv = w_is_f32 ? (A)((const float*)wp)[c] : to_acc(((const T*)wp)[c]);
-    y[row * ldy + c] = from_acc<T>(to_acc(x[row * ldx + c]) * inv * wv);
+    y[row * ldy + c] = from_acc<T>(to_acc(xin(c)) * inv * wv);
   }
 }
 
-template <typename T>
+template <typename T, typename R = void>
 __global__ __launch_bounds__(256) void men_bwd_mp_k(
     const T* __restrict__ dy, const T* __restrict__ x, const void* __restrict__ wp, int w_is_f32,
     const float* __restrict__ mu, T* __restrict__ dx, typename AccT<T>::type* __restrict__ partial,
-    int64_t n_rows, int n_cols, int64_t lddy, int64_t ldx, int64_t lddx, float eps) {
+    int64_t n_rows, int n_cols, int64_t lddy, int64_t ldx, int64_t lddx, float eps,
+    const T* __restrict__ dh, int64_t lddh, void* __restrict__ drp, int64_t lddr) {
   typedef typename AccT<T>::type A;
+  constexpr bool kAdd = !std::is_void<R>::value;
+  typedef std::conditional_t<kAdd, R, T> RT;
+  RT* dr = reinterpret_cast<RT*>(drp);
   __shared__ A sh[kRowWaves];
   A* part = partial + (int64_t)blockIdx.x * n_cols;  // owned by this block
   for (int c = threadIdx.x; c < n_cols; c += blockDim.x) part[c] = A(0);
@@ -607,7 +707,12 @@ __global__ __launch_bounds__(256) void men_bwd_mp_k(
       const A wv = w_is_f32 ? (A)((const float*)wp)[c] : to_acc(((const T*)wp)[c]);
       const A yy = to_acc(dy[row * lddy + c]);
       const A xx = to_acc(x[row * ldx + c]);
-      dx[row * lddx + c] = from_acc<T>(yy * wv * inv - sign_of(xx) * corr * inv);
+      T g = from_acc<T>(yy * wv * inv - sign_of(xx) * corr * inv);
+      if constexpr (kAdd) {
+        g = from_acc<T>(to_acc(g) + to_acc(dh[row * lddh + c]));
+        if (dr != nullptr) dr[row * lddr + c] = from_acc<RT>(to_acc(g));
+      }
+      dx[row * lddx + c] = g;
       part[c] += yy * (xx * inv);  // same thread owns column c throughout
     }
   }
@@ -784,23 +889,29 @@ static int rsoftmax_bwd_t(const T* dy, const T* x, const T* p, T* dx, int64_t ro
   return check_launch("kat_rsoftmax_bwd");
 }
 
-template <typename T, typename W>
+template <typename T, typename W, typename R = void>
 static int men_fwd_t(const T* x, const W* w, T* y, float* mu, int64_t rows, int64_t cols,
-                     int64_t ldx, int64_t ldy, float eps, hipStream_t st) {
+                     int64_t ldx, int64_t ldy, float eps, hipStream_t st, const R* r = nullptr,
+                     T* h = nullptr, int64_t ldr = 0, int64_t ldh = 0) {
   constexpr int V = Raw<T>::V;
-  const bool vec = cols % V == 0 && ldx % V == 0 && ldy % V == 0 && aligned16(x) &&
-                   aligned16(y) && aligned16(w);
+  constexpr bool kAdd = !std::is_void<R>::value;
+  bool vec = cols % V == 0 && ldx % V == 0 && ldy % V == 0 && aligned16(x) && aligned16(y) &&
+             aligned16(w);
+  if constexpr (kAdd)
+    vec = vec && ldr % V == 0 && ldh % V == 0 && aligned16(h) &&
+          reinterpret_cast<uintptr_t>(r) % (V * sizeof(R)) == 0;
   const int nch = vec ? pick_nch(cols, 256 * V) : 0;
   if (nch) {
     const int64_t blocks = row_grid(rows, kRowBlocksPerCU);
-    KAT_NCH_SWITCH(nch, hipLaunchKernelGGL((men_fwd_k<T, W, N>), dim3((unsigned)blocks), dim3(256),
-                                           0, st, x, w, y, mu, rows, (int)cols, ldx, ldy, eps));
+    KAT_NCH_SWITCH(nch, hipLaunchKernelGGL((men_fwd_k<T, W, N, R>), dim3((unsigned)blocks),
+                                           dim3(256), 0, st, x, w, y, mu, rows, (int)cols, ldx,
+                                           ldy, eps, (const void*)r, h, ldr, ldh));
   } else {
-    hipLaunchKernelGGL((men_fwd_mp_k<T>), dim3((unsigned)rows), dim3(256), 0, st, x,
+    hipLaunchKernelGGL((men_fwd_mp_k<T, R>), dim3((unsigned)rows), dim3(256), 0, st, x,
                        (const void*)w, (int)std::is_same<W, float>::value, y, mu, rows, (int)cols,
-                       ldx, ldy, eps);
+                       ldx, ldy, eps, (const void*)r, h, ldr, ldh);
   }
-  return check_launch("kat_men_fwd");
+  return check_launch(kAdd ? "kat_add_men_fwd" : "kat_men_fwd");
 }
 
 // dgamma partials cost G x cols x 4 bytes of extra traffic (written here,
@@ -810,34 +921,41 @@ static int men_bwd_grid(int64_t rows, bool resident) {
   return (int)row_grid(rows, 2);
 }
 
-template <typename T, typename W>
+template <typename T, typename W, typename R = void>
 static int men_bwd_t(const T* dy, const T* x, const W* w, const float* mu, T* dx,
                      typename AccT<T>::type* dw, void* ws, size_t ws_bytes, int64_t rows,
                      int64_t cols, int64_t lddy, int64_t ldx, int64_t lddx, float eps,
-                     hipStream_t st) {
+                     hipStream_t st, const T* dh = nullptr, int64_t lddh = 0, R* dr = nullptr,
+                     int64_t lddr = 0) {
   typedef typename AccT<T>::type A;
   constexpr int V = Raw<T>::V;
-  const bool vec = cols % V == 0 && lddy % V == 0 && ldx % V == 0 && lddx % V == 0 &&
-                   aligned16(dy) && aligned16(x) && aligned16(dx) && aligned16(w);
+  constexpr bool kAdd = !std::is_void<R>::value;
+  const char* nm = kAdd ? "kat_add_men_bwd" : "kat_men_bwd";
+  bool vec = cols % V == 0 && lddy % V == 0 && ldx % V == 0 && lddx % V == 0 &&
+             aligned16(dy) && aligned16(x) && aligned16(dx) && aligned16(w);
+  if constexpr (kAdd)
+    vec = vec && lddh % V == 0 && aligned16(dh) &&
+          (dr == nullptr || (lddr % V == 0 && reinterpret_cast<uintptr_t>(dr) % (V * sizeof(R)) == 0));
   const int nch = vec ? pick_nch(cols, 256 * V) : 0;
   const int G = men_bwd_grid(rows, nch != 0);
   const size_t need = (size_t)G * (size_t)cols * sizeof(A);
   if (ws_bytes < need || (need && ws == nullptr))
-    return fail(KAT_EINVAL, "kat_men_bwd: workspace %zu bytes < required %zu", ws_bytes, need);
+    return fail(KAT_EINVAL, "%s: workspace %zu bytes < required %zu", nm, ws_bytes, need);
   A* partial = reinterpret_cast<A*>(ws);
   if (nch) {
-    KAT_NCH_SWITCH(nch, hipLaunchKernelGGL((men_bwd_k<T, W, N>), dim3(G), dim3(256), 0, st, dy, x,
-                                           w, mu, dx, partial, rows, (int)cols, lddy, ldx, lddx,
-                                           eps));
+    KAT_NCH_SWITCH(nch, hipLaunchKernelGGL((men_bwd_k<T, W, N, R>), dim3(G), dim3(256), 0, st, dy,
+                                           x, w, mu, dx, partial, rows, (int)cols, lddy, ldx, lddx,
+                                           eps, dh, lddh, (void*)dr, lddr));
   } else {
-    hipLaunchKernelGGL((men_bwd_mp_k<T>), dim3(G), dim3(256), 0, st, dy, x, (const void*)w,
-                       (int)std::is_same<W, float>::value, mu, dx, partial, rows, (int)cols, lddy, ldx, lddx, eps);
+    hipLaunchKernelGGL((men_bwd_mp_k<T, R>), dim3(G), dim3(256), 0, st, dy, x, (const void*)w,
+                       (int)std::is_same<W, float>::value, mu, dx, partial, rows, (int)cols, lddy,
+                       ldx, lddx, eps, dh, lddh, (void*)dr, lddr);
   }
-  int rc = check_launch("kat_men_bwd");
+  int rc = check_launch(nm);
   if (rc) return rc;
   hipLaunchKernelGGL((colsum_k<A>), dim3((unsigned)((cols + 63) / 64)), dim3(1024), 0, st,
                      partial, G, (int)cols, dw);
-  return check_launch("kat_men_bwd (dw reduction)");
+  return check_launch(kAdd ? "kat_add_men_bwd (dw reduction)" : "kat_men_bwd (dw reduction)");
 }
 
 }  // namespace kat
@@ -987,6 +1105,107 @@ extern "C" int kat_men_bwd(const void* dy, const void* x, const void* w, const f
                    (men_bwd_t<T, float>((const T*)dy, (const T*)x, (const float*)w, mu, (T*)dx,
                                         (typename AccT<T>::type*)dw, workspace, workspace_bytes,
                                         n_rows, n_cols, ld_dy, ld_x, ld_dx, eps, st)));
+  }
+  return fail(KAT_EUNSUPPORTED, "%s: weight dtype %d with input dtype %d", nm, dtype_w, dtype);
+}
+
+// Residual add fused with the norm. The residual branch r (and its gradient
+// dr) has the stream's dtype, or bf16 / fp16 beside an fp32 stream (the
+// branch output of an autocast matmul added to the fp32 residual).
+template <typename T, typename W>
+static int add_men_fwd_d(const char* nm, int dtype, int dtype_r, const void* x, const void* r,
+                         const void* w, void* h, void* y, float* mu, int64_t rows, int64_t cols,
+                         int64_t ldx, int64_t ldr, int64_t ldh, int64_t ldy, float eps,
+                         hipStream_t st) {
+  if (dtype_r == dtype)
+    return men_fwd_t<T, W, T>((const T*)x, (const W*)w, (T*)y, mu, rows, cols, ldx, ldy, eps, st,
+                              (const T*)r, (T*)h, ldr, ldh);
+  if constexpr (std::is_same<T, float>::value) {
+    if (dtype_r == KAT_BF16)
+      return men_fwd_t<T, W, bf16>((const T*)x, (const W*)w, (T*)y, mu, rows, cols, ldx, ldy, eps,
+                                   st, (const bf16*)r, (T*)h, ldr, ldh);
+    if (dtype_r == KAT_F16)
+      return men_fwd_t<T, W, f16>((const T*)x, (const W*)w, (T*)y, mu, rows, cols, ldx, ldy, eps,
+                                  st, (const f16*)r, (T*)h, ldr, ldh);
+  }
+  return fail(KAT_EUNSUPPORTED, "%s: residual dtype %d with stream dtype %d", nm, dtype_r, dtype);
+}
+
+template <typename T, typename W>
+static int add_men_bwd_d(const char* nm, int dtype, int dtype_r, const void* dy, const void* dh,
+                         const void* h, const void* w, const float* mu, void* dx, void* dr,
+                         void* dw, void* ws, size_t ws_bytes, int64_t rows, int64_t cols,
+                         int64_t lddy, int64_t lddh, int64_t ldh, int64_t lddx, int64_t lddr,
+                         float eps, hipStream_t st) {
+  typedef typename AccT<T>::type A;
+  if (dtype_r == dtype)
+    return men_bwd_t<T, W, T>((const T*)dy, (const T*)h, (const W*)w, mu, (T*)dx, (A*)dw, ws,
+                              ws_bytes, rows, cols, lddy, ldh, lddx, eps, st, (const T*)dh, lddh,
+                              (T*)dr, lddr);
+  if constexpr (std::is_same<T, float>::value) {
+    if (dtype_r == KAT_BF16)
+      return men_bwd_t<T, W, bf16>((const T*)dy, (const T*)h, (const W*)w, mu, (T*)dx, (A*)dw, ws,
+                                   ws_bytes, rows, cols, lddy, ldh, lddx, eps, st, (const T*)dh,
+                                   lddh, (bf16*)dr, lddr);
+    if (dtype_r == KAT_F16)
+      return men_bwd_t<T, W, f16>((const T*)dy, (const T*)h, (const W*)w, mu, (T*)dx, (A*)dw, ws,
+                                  ws_bytes, rows, cols, lddy, ldh, lddx, eps, st, (const T*)dh,
+                                  lddh, (f16*)dr, lddr);
+  }
+  return fail(KAT_EUNSUPPORTED, "%s: residual dtype %d with stream dtype %d", nm, dtype_r, dtype);
+}
+
+extern "C" int kat_add_men_fwd(const void* x, const void* r, const void* w, void* h, void* y,
+                               float* mu, int64_t n_rows, int64_t n_cols, int64_t ld_x,
+                               int64_t ld_r, int64_t ld_h, int64_t ld_y, float eps, int dtype,
+                               int dtype_r, int dtype_w, void* stream) {
+  const char* nm = "kat_add_men_fwd";
+  if (int rc = check_rows(nm, n_rows, n_cols)) return rc;
+  if (n_rows == 0 || n_cols == 0) return KAT_OK;
+  if (!x || !r || !w || !h || !y || !mu) return fail(KAT_EINVAL, "%s: null pointer", nm);
+  if (int rc = check_ld(nm, n_cols, {ld_x, ld_r, ld_h, ld_y})) return rc;
+  const hipStream_t st = as_stream(stream);
+  if (dtype_w == dtype) {
+    KAT_DISPATCH_T(dtype, nm,
+                   (add_men_fwd_d<T, T>(nm, dtype, dtype_r, x, r, w, h, y, mu, n_rows, n_cols,
+                                        ld_x, ld_r, ld_h, ld_y, eps, st)));
+  }
+  if (dtype_w == KAT_F32 && dtype != KAT_F64) {
+    KAT_DISPATCH_T(dtype, nm,
+                   (add_men_fwd_d<T, float>(nm, dtype, dtype_r, x, r, w, h, y, mu, n_rows, n_cols,
+                                            ld_x, ld_r, ld_h, ld_y, eps, st)));
+  }
+  return fail(KAT_EUNSUPPORTED, "%s: weight dtype %d with input dtype %d", nm, dtype_w, dtype);
+}
+
+extern "C" int kat_add_men_bwd(const void* dy, const void* dh, const void* h, const void* w,
+                               const float* mu, void* dx, void* dr, void* dw, void* workspace,
+                               size_t workspace_bytes, int64_t n_rows, int64_t n_cols,
+                               int64_t ld_dy, int64_t ld_dh, int64_t ld_h, int64_t ld_dx,
+                               int64_t ld_dr, float eps, int dtype, int dtype_r, int dtype_w,
+                               void* stream) {
+  const char* nm = "kat_add_men_bwd";
+  if (int rc = check_rows(nm, n_rows, n_cols)) return rc;
+  if (n_cols == 0) return KAT_OK;
+  if (n_rows == 0)  // dw = 0, like kat_men_bwd
+    return kat_men_bwd(dy, h, w, mu, dx, dw, workspace, workspace_bytes, 0, n_cols, n_cols,
+                       n_cols, n_cols, eps, dtype, dtype_w, stream);
+  if (!dy || !dh || !h || !w || !mu || !dx || !dw) return fail(KAT_EINVAL, "%s: null pointer", nm);
+  if (int rc = check_ld(nm, n_cols, {ld_dy, ld_dh, ld_h, ld_dx})) return rc;
+  if (dr != nullptr)
+    if (int rc = check_ld(nm, n_cols, {ld_dr})) return rc;
+  const hipStream_t st = as_stream(stream);
+  if (dtype_w == dtype) {
+    KAT_DISPATCH_T(dtype, nm,
+                   (add_men_bwd_d<T, T>(nm, dtype, dtype_r, dy, dh, h, w, mu, dx, dr, dw,
+                                        workspace, workspace_bytes, n_rows, n_cols, ld_dy, ld_dh,
+                                        ld_h, ld_dx, ld_dr, eps, st)));
+  }
+  if (dtype_w == KAT_F32 && dtype != KAT_F64) {
+    KAT_DISPATCH_T(dtype, nm,
+                   (add_men_bwd_d<T, float>(nm, dtype, dtype_r, dy, dh, h, w, mu, dx, dr, dw,
+                                            workspace, workspace_bytes, n_rows, n_cols, ld_dy,
+                                            ld_dh, ld_h, ld_dx, ld_dr, eps, st)));
   }
   return fail(KAT_EUNSUPPORTED, "%s: weight dtype %d with input dtype %d", nm, dtype_w, dtype);
 }

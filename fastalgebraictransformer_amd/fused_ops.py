@@ -185,6 +185,71 @@ class MeanErrorNorm(torch.autograd.Function):
         return dx.view(x.shape), dw, None
 
 
+class ResidualMeanErrorNorm(torch.autograd.Function):
+    """(h, y) = (x + r, mean_error_norm(x + r, weight)) in one pass: the
+    pre-norm block's residual add and the norm that reads it
+    (reference algebraic_model.py:150-151 with fused_ops.py:542-599).
+
+    ``r`` may be narrower than ``x`` (bf16/fp16 branch output beside an fp32
+    residual stream, as under autocast); ``h`` has ``x``'s dtype exactly as
+    torch's promoted add gives it. Outputs and gradients equal those of
+    ``h = x + r; y = MeanErrorNorm.apply(h, weight, eps)`` bit for bit."""
+
+    @staticmethod
+    def forward(ctx, x, r, weight, eps=EPS):
+        assert x.is_cuda and r.is_cuda, "Input must be on CUDA"
+        assert r.shape == x.shape, "residual branch must have the stream's shape"
+        lib = _lib.load()
+        w = _weight_for(x, weight)
+        assert w.numel() == x.shape[-1], "weight must have x.shape[-1] elements"
+        x2, ldx = _lib.rows2d(x)
+        r2, ldr = _lib.rows2d(r)
+        rows, cols = x2.shape
+        h = torch.empty((rows, cols), dtype=x.dtype, device=x.device)
+        y = torch.empty((rows, cols), dtype=x.dtype, device=x.device)
+        mean = torch.empty(rows, dtype=torch.float32, device=x.device)
+        _lib.check(lib.kat_add_men_fwd(_ptr(x2), _ptr(r2), _ptr(w), _ptr(h), _ptr(y), _ptr(mean),
+                                       rows, cols, ldx, ldr, cols, cols, float(eps),
+                                       _lib.dtype_code(x), _lib.dtype_code(r),
+                                       _lib.dtype_code(w), _lib.stream(x)), "kat_add_men_fwd")
+        ctx.save_for_backward(h, w, mean)
+        ctx.eps = eps
+        ctx.r_dtype = r.dtype
+        return h.view(x.shape), y.view(x.shape)
+
+    @staticmethod
+    def backward(ctx, grad_h, grad_y):
+        h, w, mean = ctx.saved_tensors
+        lib = _lib.load()
+        rows, cols = h.shape
+        g2, ldg = _lib.rows2d(grad_y.to(h.dtype))
+        d2, ldd = _lib.rows2d(grad_h.to(h.dtype))
+        code = _lib.dtype_code(h)
+        dx = torch.empty((rows, cols), dtype=h.dtype, device=h.device)
+        # a same-dtype branch gets the stream's gradient itself (as torch's add
+        # backward gives both operands the one tensor); a narrower one its cast
+        dr = None
+        if ctx.r_dtype != h.dtype and ctx.needs_input_grad[1]:
+            dr = torch.empty((rows, cols), dtype=ctx.r_dtype, device=h.device)
+        acc = torch.float64 if h.dtype == torch.float64 else torch.float32
+        dw = torch.empty(cols, dtype=acc, device=h.device)
+        ws_bytes = lib.kat_men_bwd_workspace_size(rows, cols, code)
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=h.device)
+        _lib.check(lib.kat_add_men_bwd(_ptr(g2), _ptr(d2), _ptr(h), _ptr(w), _ptr(mean), _ptr(dx),
+                                       None if dr is None else _ptr(dr), _ptr(dw), _ptr(ws),
+                                       ws_bytes, rows, cols, ldg, ldd, cols, cols, cols,
+                                       float(ctx.eps), code,
+                                       _lib.dtype_code(dr if dr is not None else h),
+                                       _lib.dtype_code(w), _lib.stream(h)), "kat_add_men_bwd")
+        shape = grad_y.shape
+        dx = dx.view(shape)
+        if not ctx.needs_input_grad[1]:
+            d_r = None
+        else:
+            d_r = dx if dr is None else dr.view(shape)
+        return dx, d_r, dw, None
+
+
 def rational_softmax(x, eps=EPS):
     """Rational softmax over the last dim (reference fused_ops.py:606-615)."""
     if x.is_cuda:
@@ -208,6 +273,16 @@ def mean_error_norm(x, weight, eps=EPS):
         return MeanErrorNorm.apply(x, weight, eps)
     m = x.abs().mean(dim=-1, keepdim=True)
     return (x / (m + eps)) * weight
+
+
+def add_mean_error_norm(x, r, weight, eps=EPS):
+    """(x + r, mean_error_norm(x + r, weight, eps)) with the add fused into the
+    norm on CUDA tensors (see ResidualMeanErrorNorm); CPU tensors use the
+    reference formulas."""
+    if x.is_cuda:
+        return ResidualMeanErrorNorm.apply(x, r, weight, eps)
+    h = x + r
+    return h, mean_error_norm(h, weight, eps)
 
 
 def rational_swiglu_packed(gv):

@@ -115,3 +115,34 @@ def test_model_state_dict_names_match_reference_layout():
         assert n in names, n
     assert m.embed.weight is m.head.weight
     assert m.blocks[0].ffn.w_gate_val.weight.shape == (2 * int(768 * 8 / 3), 768)
+
+
+def test_model_residual_stream_matches_reference_block_structure():
+    """The model carries the stream as (x, r) so that each residual add fuses
+    into the next norm; on CPU that must equal the reference block
+    `x = x + attn(norm1(x)); x = x + ffn(norm2(x))` (algebraic_model.py:149-152)
+    followed by the final norm and head (:209-237) exactly."""
+    torch.manual_seed(3)
+    m = F.AlgebraicTransformerLM(vocab_size=40, d_model=32, n_head=4, n_layers=3, dropout=0.0)
+    ids = torch.randint(0, 40, (2, 7))
+    logits, _ = m(ids)
+    x = m.embed(ids)
+    for blk in m.blocks:
+        x = x + blk.attn(blk.norm1(x))
+        x = x + blk.ffn(blk.norm2(x))
+    ref = m.head(m.norm(x))
+    assert torch.equal(logits, ref)
+    # a single block called directly keeps the reference's x -> x contract
+    x0 = torch.randn(2, 7, 32)
+    blk = m.blocks[1]
+    h = x0 + blk.attn(blk.norm1(x0))
+    assert torch.equal(blk(x0), h + blk.ffn(blk.norm2(h)))
+
+
+def test_add_mean_error_norm_cpu_is_add_then_norm():
+    x = torch.randn(5, 24)
+    r = torch.randn(5, 24)
+    w = torch.rand(24) + 0.5
+    h, y = F.add_mean_error_norm(x, r, w)
+    assert torch.equal(h, x + r)
+    assert torch.equal(y, F.mean_error_norm(x + r, w))
