@@ -15,6 +15,9 @@ throughput 7*B*H*S^2*D / step time in TFLOP/s. The same JSON line carries:
                  of the flush are written back inside the timed region;
   * cpu_baseline -- the CPU oracle (fp32) on a bounded sample of the same
                  workload (one (b, h) head), on this host's cores;
+  * attention_variants -- fwd+bwd of the padding-mask / non-causal attention
+                 extension at the same shape (right-padded batch, non-causal,
+                 both), TFLOP/s over the (query, key) pairs each attends;
   * device     -- CU count, a measured bf16 MFMA loop rate (beside the 2.5 PF
                  spec peak) and a measured 1 GiB device-copy bandwidth;
   * model_step -- one training step (bf16 autocast forward + loss + backward,
@@ -23,7 +26,7 @@ throughput 7*B*H*S^2*D / step time in TFLOP/s. The same JSON line carries:
                  also the 1.3 B-parameter model at batch 2 x 8192.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-fused]
-                       [--no-model] [--model-large]
+                       [--no-variants] [--no-model] [--model-large]
        python bench.py --copy-calibration   (one plain 1 GiB device copy, for
                                              scaling HBM byte counters)
 """
@@ -96,6 +99,53 @@ def bench_attention(torch, F, steps, warmup, B=4, H=16, T=4096, D=128):
     return dict(ms=ms, wall_ms=wall * 1e3 / steps, fwd_ms=sum(fwd) / steps, bwd_ms=sum(bwd) / steps,
                 fwd_median_ms=fwd[steps // 2], bwd_median_ms=bwd[steps // 2],
                 flops_step=7 * unit, flops_fwd=2 * unit, flops_bwd=5 * unit)
+
+
+def bench_attention_variants(torch, F, steps=5, warmup=2, B=4, H=16, T=4096, D=128):
+    """fwd+bwd of the masked / non-causal attention extension at the benchmark
+    shape (bf16). TFLOP/s count the (query, key) pairs each variant attends:
+    7 matmuls x 2 D flops per pair, the same accounting as the headline metric
+    (whose causal pairs are ~T^2 / 2 per head)."""
+    dev = torch.device("cuda:0")
+    q, k, v, do = attention_inputs(torch, B, H, T, D, dev)
+    for t in (q, k, v):
+        t.requires_grad_(True)
+    slopes = torch.tensor([2.0 ** (-(i + 1) / 2) for i in range(H)], dtype=torch.float32,
+                          device=dev)
+    scale = 1.0 / math.sqrt(D)
+    lens = [T, T - T // 8, T - T // 4, T - 3 * T // 8]  # right padding, 0-37.5% of keys
+    pad = torch.zeros(B, T, dtype=torch.bool)
+    for b, n in enumerate(lens):
+        pad[b, :n] = True
+    out = {}
+    for name, km, causal in (("causal_padded", pad, True), ("noncausal", None, False),
+                             ("noncausal_padded", pad, False)):
+        kmc = torch.ones(B, T, dtype=torch.bool) if km is None else km
+        if causal:
+            pairs = int(kmc.to(torch.int64).cumsum(1).sum()) * H
+        else:
+            pairs = int(kmc.to(torch.int64).sum(1).sum()) * T * H
+        kmd = None if km is None else km.to(dev)
+
+        def step():
+            for t in (q, k, v):
+                t.grad = None
+            F.rational_attention_masked(q, k, v, slopes, scale, key_mask=kmd,
+                                        causal=causal).backward(do)
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            step()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        flops = 7 * 2 * D * pairs
+        out[name] = dict(ms=round(ms, 4), pairs=pairs, TFLOPs=round(flops / ms / 1e9, 2),
+                         valid_keys=lens if km is not None else [T] * B)
+    return out
 
 
 def device_info(torch, lib):
@@ -329,6 +379,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-fused", action="store_true")
+    ap.add_argument("--no-variants", action="store_true",
+                    help="skip the masked / non-causal attention variants")
     ap.add_argument("--no-model", action="store_true", help="skip the model training step")
     ap.add_argument("--model-large", action="store_true",
                     help="also time the ~1.3B model step (batch 2 x 8192, ~55 GB; reported only)")
@@ -392,6 +444,8 @@ def main():
                                      "TFLOPs": round(bwd_tf, 2), "algorithmic_flops": att["flops_bwd"]}},
         "frac_mfma_peak_step": round(value / PEAK_BF16_TFLOPS, 4),
     }
+    if not args.no_variants:
+        line["attention_variants"] = bench_attention_variants(torch, F)
     if not args.no_fused:
         fused = bench_fused(torch, F)
         line["fused_ops"] = {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv)

@@ -30,10 +30,12 @@ from .fused_ops import (
 )
 from .forward import compute_alibi_slopes, rational_attention_forward
 from .backward import (
+    MaskedRationalAttentionFunction,
     PackedRationalAttention,
     RationalAttentionFunction,
     rational_attention,
     rational_attention_backward,
+    rational_attention_masked,
     rational_attention_packed,
 )
 from .algebraic_model import (
@@ -73,7 +75,8 @@ __all__ = [
 # projection and rational_swiglu_packed / PackedRationalSwiGLU on a packed
 # [..., 2F] gate|value buffer -- the model's layouts, same kernels; and
 # add_mean_error_norm / ResidualMeanErrorNorm, the residual add fused with the
-# norm that reads it.
+# norm that reads it; rational_attention_masked / MaskedRationalAttentionFunction,
+# attention with a key padding mask and a real non-causal mode.
 
 
 def install_as(name="kernels"):

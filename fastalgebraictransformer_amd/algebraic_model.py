@@ -17,7 +17,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 from torch.utils.checkpoint import checkpoint
 
-from .backward import rational_attention_packed
+from .backward import attention_torch, rational_attention_packed
 from .forward import compute_alibi_slopes
 from .fused_ops import (EPS, add_mean_error_norm, mean_error_norm, rational_softmax,
                         rational_swiglu_packed)
@@ -72,11 +72,13 @@ class AlgebraicAttention(nn.Module):
         B, T, C = x.shape
         qkv = self.qkv(x).view(B, T, 3, self.n_head, self.d_head)
         if x.is_cuda:
-            # like the reference GPU path (algebraic_model.py:93-101) the
-            # padding mask is not applied here; attention is always causal.
-            # The kernels read q, k, v in place from the packed projection and
-            # write the output as [B, T, H, D], so no layout copies are made.
-            y = rational_attention_packed(qkv, self.alibi_slopes, self.scale, eps=EPS).view(B, T, C)
+            # causal, with the padding mask applied as the reference's CPU path
+            # applies it (algebraic_model.py:129-131; its GPU path, :93-101,
+            # drops the mask). The kernels read q, k, v in place from the
+            # packed projection and write the output as [B, T, H, D], so no
+            # layout copies are made.
+            y = rational_attention_packed(qkv, self.alibi_slopes, self.scale, eps=EPS,
+                                          key_mask=mask).view(B, T, C)
         else:
             q, k, v = qkv.permute(2, 0, 3, 1, 4)
             y = self._cpu_attention(q, k, v, mask).transpose(1, 2).contiguous().view(B, T, C)
@@ -85,16 +87,7 @@ class AlgebraicAttention(nn.Module):
     def _cpu_attention(self, q, k, v, mask):
         """Reference CPU path (algebraic_model.py:112-136): full score matrix,
         ALiBi, -1e4 causal and padding fill, rational softmax, P @ V."""
-        B, H, T, D = q.shape
-        scores = torch.matmul(q, k.transpose(-2, -1)) * self.scale
-        idx = torch.arange(T, device=q.device)
-        dist = (idx[:, None] - idx[None, :]).abs().float()
-        scores = scores + (-dist * self.alibi_slopes.view(1, H, 1, 1))
-        future = torch.ones(T, T, device=q.device, dtype=torch.bool).triu(1)
-        scores = scores.masked_fill(future[None, None], -1e4)
-        if mask is not None:
-            scores = scores.masked_fill((mask == 0)[:, None, None, :], -1e4)
-        return torch.matmul(rational_softmax(scores, eps=EPS), v)
+        return attention_torch(q, k, v, self.alibi_slopes, self.scale, mask, True, EPS)
 
 
 class AlgebraicBlock(nn.Module):

@@ -15,6 +15,7 @@ from . import _lib
 from .fused_ops import EPS, NEG_INF  # noqa: F401
 from .forward import (  # noqa: F401
     _attn_fwd_into,
+    _key_mask_arg,
     _bht_strides,
     _unit_d,
     compute_alibi_slopes,
@@ -22,9 +23,11 @@ from .forward import (  # noqa: F401
 )
 
 
-def _attn_bwd_into(q, k, v, output, L, grad_output, dq, dk, dv, alibi_slopes, scale, causal, eps):
-    """Launch kat_attn_bwd; every [B,H,T,D] argument may have any (b, h, t)
-    strides with a unit d-stride. The workspace comes from torch's allocator."""
+def _attn_bwd_into(q, k, v, output, L, grad_output, dq, dk, dv, alibi_slopes, scale, causal, eps,
+                   key_mask=None, extended=False):
+    """Launch the attention backward; every [B,H,T,D] argument may have any
+    (b, h, t) strides with a unit d-stride. The workspace comes from torch's
+    allocator. ``extended``: kat_attn_bwd_masked (see _attn_fwd_into)."""
     lib = _lib.load()
     B, H, T, D = q.shape
     slopes = alibi_slopes.to(device=q.device, dtype=torch.float32).contiguous()
@@ -35,11 +38,21 @@ def _attn_bwd_into(q, k, v, output, L, grad_output, dq, dk, dv, alibi_slopes, sc
         _bht_strides(q) + _bht_strides(k) + _bht_strides(v) + _bht_strides(output) +
         _bht_strides(grad_output) + _bht_strides(dq) + _bht_strides(dk) + _bht_strides(dv))
     lstr = _lib.i64_array(_bht_strides(L))
-    _lib.check(lib.kat_attn_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), output.data_ptr(),
-                                L.data_ptr(), grad_output.data_ptr(), dq.data_ptr(),
-                                dk.data_ptr(), dv.data_ptr(), slopes.data_ptr(), ws.data_ptr(),
-                                ws_bytes, B, H, T, D, strides, lstr, float(scale), float(eps),
-                                int(bool(causal)), code, _lib.stream(q)), "kat_attn_bwd")
+    if not extended:
+        _lib.check(lib.kat_attn_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), output.data_ptr(),
+                                    L.data_ptr(), grad_output.data_ptr(), dq.data_ptr(),
+                                    dk.data_ptr(), dv.data_ptr(), slopes.data_ptr(), ws.data_ptr(),
+                                    ws_bytes, B, H, T, D, strides, lstr, float(scale), float(eps),
+                                    int(bool(causal)), code, _lib.stream(q)), "kat_attn_bwd")
+        return
+    km_ptr = None if key_mask is None else key_mask.data_ptr()
+    _lib.check(lib.kat_attn_bwd_masked(q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                       output.data_ptr(), L.data_ptr(), grad_output.data_ptr(),
+                                       dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                                       slopes.data_ptr(), km_ptr, T, ws.data_ptr(), ws_bytes, B,
+                                       H, T, D, strides, lstr, float(scale), float(eps),
+                                       int(bool(causal)), code, _lib.stream(q)),
+               "kat_attn_bwd_masked")
 
 
 def rational_attention_backward(q, k, v, output, L, grad_output, alibi_slopes, scale,
@@ -96,32 +109,103 @@ class PackedRationalAttention(torch.autograd.Function):
     on the three views."""
 
     @staticmethod
-    def forward(ctx, qkv, alibi_slopes, scale, eps):
+    def forward(ctx, qkv, alibi_slopes, scale, eps, key_mask=None):
         assert qkv.is_cuda and qkv.dim() == 5 and qkv.shape[2] == 3, "qkv must be [B, T, 3, H, D]"
         qkv = _unit_d(qkv)
         B, T, _, H, D = qkv.shape
+        km = _key_mask_arg(key_mask, B, T, qkv.device)
         q, k, v = qkv.permute(2, 0, 3, 1, 4)
         y = torch.empty((B, T, H, D), dtype=qkv.dtype, device=qkv.device)
         L = torch.empty((B, H, T), dtype=torch.float32, device=qkv.device)
-        _attn_fwd_into(q, k, v, y.permute(0, 2, 1, 3), L, alibi_slopes, scale, True, eps)
-        ctx.save_for_backward(qkv, y, L, alibi_slopes)
+        _attn_fwd_into(q, k, v, y.permute(0, 2, 1, 3), L, alibi_slopes, scale, True, eps, km,
+                       extended=km is not None)
+        ctx.save_for_backward(qkv, y, L, alibi_slopes, km)
         ctx.scale = scale
         ctx.eps = eps
         return y
 
     @staticmethod
     def backward(ctx, grad_y):
-        qkv, y, L, alibi_slopes = ctx.saved_tensors
+        qkv, y, L, alibi_slopes, km = ctx.saved_tensors
         q, k, v = qkv.permute(2, 0, 3, 1, 4)
         grad_o = _unit_d(grad_y.to(qkv.dtype).permute(0, 2, 1, 3))
         dqkv = torch.empty(qkv.shape, dtype=qkv.dtype, device=qkv.device)
         dq, dk, dv = dqkv.permute(2, 0, 3, 1, 4)
         _attn_bwd_into(q, k, v, y.permute(0, 2, 1, 3), L, grad_o, dq, dk, dv, alibi_slopes,
-                       ctx.scale, True, ctx.eps)
-        return dqkv, None, None, None
+                       ctx.scale, True, ctx.eps, km, extended=km is not None)
+        return dqkv, None, None, None, None
 
 
-def rational_attention_packed(qkv, alibi_slopes, scale, eps=EPS):
+def rational_attention_packed(qkv, alibi_slopes, scale, eps=EPS, key_mask=None):
     """Causal ALiBi rational attention on qkv [B, T, 3, H, D]; returns
-    [B, T, H, D] (see PackedRationalAttention)."""
-    return PackedRationalAttention.apply(qkv, alibi_slopes, scale, eps)
+    [B, T, H, D] (see PackedRationalAttention). ``key_mask`` [B, T]: keys where
+    it is 0 are dropped (see rational_attention_masked)."""
+    return PackedRationalAttention.apply(qkv, alibi_slopes, scale, eps, key_mask)
+
+
+class MaskedRationalAttentionFunction(torch.autograd.Function):
+    """Attention with a key padding mask and a real non-causal mode (see
+    rational_attention_masked); recompute backward as RationalAttentionFunction."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, alibi_slopes, scale, key_mask, causal, eps):
+        assert q.is_cuda and k.is_cuda and v.is_cuda
+        assert q.shape == k.shape == v.shape
+        B, H, T, D = q.shape
+        km = _key_mask_arg(key_mask, B, T, q.device)
+        k, v = k.to(q.dtype), v.to(q.dtype)
+        q, k, v = _unit_d(q), _unit_d(k), _unit_d(v)
+        out = torch.empty((B, H, T, D), dtype=q.dtype, device=q.device)
+        L = torch.empty((B, H, T), dtype=torch.float32, device=q.device)
+        _attn_fwd_into(q, k, v, out, L, alibi_slopes, scale, causal, eps, km, extended=True)
+        ctx.save_for_backward(q, k, v, out, L, alibi_slopes, km)
+        ctx.scale = scale
+        ctx.causal = causal
+        ctx.eps = eps
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        q, k, v, out, L, alibi_slopes, km = ctx.saved_tensors
+        B, H, T, D = q.shape
+        go = _unit_d(grad_output.to(q.dtype))
+        dq, dk, dv = (torch.empty((B, H, T, D), dtype=q.dtype, device=q.device) for _ in range(3))
+        _attn_bwd_into(q, k, v, out, L, go, dq, dk, dv, alibi_slopes, ctx.scale, ctx.causal,
+                       ctx.eps, km, extended=True)
+        return dq, dk, dv, None, None, None, None, None
+
+
+def attention_torch(q, k, v, alibi_slopes, scale, key_mask=None, causal=True, eps=EPS):
+    """The reference model's CPU attention (algebraic_model.py:112-136): full
+    score matrix, ALiBi -slope |i - j|, the -1e4 causal fill (``causal``) and
+    -1e4 padding fill where ``key_mask`` == 0, rational softmax, P @ V."""
+    from .fused_ops import rational_softmax
+    B, H, T, D = q.shape
+    scores = torch.matmul(q, k.transpose(-2, -1)) * scale
+    idx = torch.arange(T, device=q.device)
+    dist = (idx[:, None] - idx[None, :]).abs().float()
+    scores = scores + (-dist * alibi_slopes.to(q.device).view(1, H, 1, 1))
+    if causal:
+        future = torch.ones(T, T, device=q.device, dtype=torch.bool).triu(1)
+        scores = scores.masked_fill(future[None, None], NEG_INF)
+    if key_mask is not None:
+        scores = scores.masked_fill((key_mask == 0)[:, None, None, :], NEG_INF)
+    return torch.matmul(rational_softmax(scores, eps=eps), v)
+
+
+def rational_attention_masked(q, k, v, alibi_slopes, scale, key_mask=None, causal=True, eps=EPS):
+    """ALiBi rational attention with a key padding mask and a real non-causal
+    mode -- an extension beyond the reference API, whose GPU path ignores both
+    (forward.py:273) while its model's CPU path applies the padding mask
+    (algebraic_model.py:129-131).
+
+    key_mask: [B, T] (any dtype); key j of batch b is dropped where it is 0.
+    causal=False: every key is visible, with ALiBi -slope |i - j| (the CPU
+    path's form). A dropped key contributes exactly nothing (the CPU path's
+    -1e4 fill leaves ~6e-18 per key), so a query with no visible key returns 0.
+    CUDA tensors run the libkat kernels; CPU tensors the reference's torch
+    formulation (attention_torch)."""
+    if q.is_cuda:
+        return MaskedRationalAttentionFunction.apply(q, k, v, alibi_slopes, scale, key_mask,
+                                                     causal, eps)
+    return attention_torch(q, k, v, alibi_slopes, scale, key_mask, causal, eps)

@@ -100,16 +100,18 @@ static int attn_bwd_t(const AttnArgs& a, void* ws, hipStream_t st) {
   return attn_bwd_generic<T>(a, delta, st);
 }
 
-extern "C" int kat_attn_fwd(const void* q, const void* k, const void* v, void* out, float* L,
-                            const float* slopes, int64_t B, int64_t H, int64_t T, int64_t D,
-                            const int64_t* strides, const int64_t* l_strides, float scale,
-                            float eps, int causal, int dtype, void* stream) {
-  (void)causal;  // always causal, as the reference (forward.py:110)
-  const char* nm = "kat_attn_fwd";
+static int attn_fwd_impl(const char* nm, const void* q, const void* k, const void* v, void* out,
+                         float* L, const float* slopes, const uint8_t* key_mask,
+                         int64_t mask_stride_b, int64_t B, int64_t H, int64_t T, int64_t D,
+                         const int64_t* strides, const int64_t* l_strides, float scale, float eps,
+                         int causal, int dtype, void* stream) {
   AttnArgs a = {};
   if (int rc = fill_args(nm, a, B, H, T, D, strides, 4, l_strides)) return rc;
   if (B * H * T == 0 || D == 0) return KAT_OK;
   if (!q || !k || !v || !out || !L || !slopes) return fail(KAT_EINVAL, "%s: null pointer", nm);
+  if (key_mask && mask_stride_b < T && B > 1)
+    return fail(KAT_EINVAL, "%s: key-mask batch stride %lld < T %lld", nm, (long long)mask_stride_b,
+                (long long)T);
   a.q = q;
   a.k = k;
   a.v = v;
@@ -118,6 +120,9 @@ extern "C" int kat_attn_fwd(const void* q, const void* k, const void* v, void* o
   a.slopes = slopes;
   a.scale = scale;
   a.eps = eps;
+  a.km = key_mask;
+  a.skm = mask_stride_b;
+  a.causal = causal ? 1 : 0;
   const hipStream_t st = as_stream(stream);
   switch (dtype) {
     case KAT_F32: return attn_fwd_generic<float>(a, st);
@@ -127,25 +132,45 @@ extern "C" int kat_attn_fwd(const void* q, const void* k, const void* v, void* o
   }
 }
 
+extern "C" int kat_attn_fwd(const void* q, const void* k, const void* v, void* out, float* L,
+                            const float* slopes, int64_t B, int64_t H, int64_t T, int64_t D,
+                            const int64_t* strides, const int64_t* l_strides, float scale,
+                            float eps, int causal, int dtype, void* stream) {
+  (void)causal;  // always causal, as the reference (forward.py:110)
+  return attn_fwd_impl("kat_attn_fwd", q, k, v, out, L, slopes, nullptr, 0, B, H, T, D, strides,
+                       l_strides, scale, eps, 1, dtype, stream);
+}
+
+extern "C" int kat_attn_fwd_masked(const void* q, const void* k, const void* v, void* out,
+                                   float* L, const float* slopes, const uint8_t* key_mask,
+                                   int64_t mask_stride_b, int64_t B, int64_t H, int64_t T,
+                                   int64_t D, const int64_t* strides, const int64_t* l_strides,
+                                   float scale, float eps, int causal, int dtype, void* stream) {
+  return attn_fwd_impl("kat_attn_fwd_masked", q, k, v, out, L, slopes, key_mask, mask_stride_b, B,
+                       H, T, D, strides, l_strides, scale, eps, causal, dtype, stream);
+}
+
 extern "C" size_t kat_attn_bwd_workspace_size(int64_t B, int64_t H, int64_t T, int64_t D,
                                               int dtype) {
   if (B <= 0 || H <= 0 || T <= 0 || D < 0) return 0;
   return bwd_workspace(B, H, T, D, dtype);
 }
 
-extern "C" int kat_attn_bwd(const void* q, const void* k, const void* v, const void* out,
-                            const float* L, const void* dout, void* dq, void* dk, void* dv,
-                            const float* slopes, void* workspace, size_t workspace_bytes,
-                            int64_t B, int64_t H, int64_t T, int64_t D, const int64_t* strides,
-                            const int64_t* l_strides, float scale, float eps, int causal,
-                            int dtype, void* stream) {
-  (void)causal;  // always causal, as the reference (backward.py:125,222)
-  const char* nm = "kat_attn_bwd";
+static int attn_bwd_impl(const char* nm, const void* q, const void* k, const void* v,
+                         const void* out, const float* L, const void* dout, void* dq, void* dk,
+                         void* dv, const float* slopes, const uint8_t* key_mask,
+                         int64_t mask_stride_b, void* workspace, size_t workspace_bytes,
+                         int64_t B, int64_t H, int64_t T, int64_t D, const int64_t* strides,
+                         const int64_t* l_strides, float scale, float eps, int causal, int dtype,
+                         void* stream) {
   AttnArgs a = {};
   if (int rc = fill_args(nm, a, B, H, T, D, strides, 8, l_strides)) return rc;
   if (B * H * T == 0 || D == 0) return KAT_OK;
   if (!q || !k || !v || !out || !L || !dout || !dq || !dk || !dv || !slopes)
     return fail(KAT_EINVAL, "%s: null pointer", nm);
+  if (key_mask && mask_stride_b < T && B > 1)
+    return fail(KAT_EINVAL, "%s: key-mask batch stride %lld < T %lld", nm, (long long)mask_stride_b,
+                (long long)T);
   const size_t need = bwd_workspace(B, H, T, D, dtype);
   if (!workspace || workspace_bytes < need)
     return fail(KAT_EINVAL, "%s: workspace %zu bytes < required %zu", nm, workspace_bytes, need);
@@ -161,6 +186,9 @@ extern "C" int kat_attn_bwd(const void* q, const void* k, const void* v, const v
   a.slopes = slopes;
   a.scale = scale;
   a.eps = eps;
+  a.km = key_mask;
+  a.skm = mask_stride_b;
+  a.causal = causal ? 1 : 0;
   float* delta = reinterpret_cast<float*>(workspace);
   float* cinv = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + stat_bytes(B, H, T));
   const hipStream_t st = as_stream(stream);
@@ -172,4 +200,28 @@ extern "C" int kat_attn_bwd(const void* q, const void* k, const void* v, const v
     case KAT_F16: return attn_bwd_t<f16>(a, workspace, st);
     default: return fail(KAT_EUNSUPPORTED, "%s: unsupported dtype %d", nm, dtype);
   }
+}
+
+extern "C" int kat_attn_bwd(const void* q, const void* k, const void* v, const void* out,
+                            const float* L, const void* dout, void* dq, void* dk, void* dv,
+                            const float* slopes, void* workspace, size_t workspace_bytes,
+                            int64_t B, int64_t H, int64_t T, int64_t D, const int64_t* strides,
+                            const int64_t* l_strides, float scale, float eps, int causal,
+                            int dtype, void* stream) {
+  (void)causal;  // always causal, as the reference (backward.py:125,222)
+  return attn_bwd_impl("kat_attn_bwd", q, k, v, out, L, dout, dq, dk, dv, slopes, nullptr, 0,
+                       workspace, workspace_bytes, B, H, T, D, strides, l_strides, scale, eps, 1,
+                       dtype, stream);
+}
+
+extern "C" int kat_attn_bwd_masked(const void* q, const void* k, const void* v, const void* out,
+                                   const float* L, const void* dout, void* dq, void* dk, void* dv,
+                                   const float* slopes, const uint8_t* key_mask,
+                                   int64_t mask_stride_b, void* workspace, size_t workspace_bytes,
+                                   int64_t B, int64_t H, int64_t T, int64_t D,
+                                   const int64_t* strides, const int64_t* l_strides, float scale,
+                                   float eps, int causal, int dtype, void* stream) {
+  return attn_bwd_impl("kat_attn_bwd_masked", q, k, v, out, L, dout, dq, dk, dv, slopes, key_mask,
+                       mask_stride_b, workspace, workspace_bytes, B, H, T, D, strides, l_strides,
+                       scale, eps, causal, dtype, stream);
 }

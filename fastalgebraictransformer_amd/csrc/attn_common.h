@@ -22,7 +22,17 @@ struct AttnArgs {
   int B, H, T, D;
   int64_t sq[3], sk[3], sv[3], so[3], sdo[3], sdq[3], sdk[3], sdv[3], sl[3];
   float scale, eps;
+  // key padding mask: key j of batch b is attended iff km[b * skm + j] != 0
+  // (km == nullptr: every key); causal == 0: every key visible, ALiBi on |i - j|
+  const uint8_t* km;
+  int64_t skm;
+  int causal;
 };
+
+// key j of batch b passes the padding mask (j < T assumed)
+__device__ __forceinline__ bool key_ok(const AttnArgs& a, int b, int j) {
+  return a.km == nullptr || a.km[(int64_t)b * a.skm + j] != 0;
+}
 
 template <typename T> int attn_fwd_generic(const AttnArgs& a, hipStream_t st);
 // Delta_i = <dO_i, O_i> and cinv_i = 1 / (16 (L_i + eps)), both [B*H*T] fp32.

@@ -6,12 +6,14 @@
 // independent on-GPU cross-check of the bf16 MFMA kernels.
 //
 // Math (reference forward.py:110-159, backward.py:116-154, 222-260):
-//   s_ij = (q_i . k_j) * scale - slope_h * (i - j),  j <= i (always causal)
+//   s_ij = (q_i . k_j) * scale - slope_h * |i - j|,  j <= i (causal), every j
+//   (causal == 0); keys the padding mask drops are skipped
 //   f_ij = sigma(s_ij)^4, L_i = sum_j f_ij (stored without eps)
 //   o_i  = sum_j f_ij v_j / (L_i + eps)
 //   p = f / (L + eps), g = 2 / ((|s|+1)^2 (sigma + eps)), dS = p g (dO_i.v_j - Delta_i)
 //   dq = scale * sum_j dS k_j,  dk = scale * sum_i dS q_i,  dv = sum_i p dO_i
-// Keys j > i are never visited, exactly as the reference kernels' loops.
+// In causal mode keys j > i are never visited, exactly as the reference
+// kernels' loops.
 
 #include <algorithm>
 
@@ -63,7 +65,8 @@ __global__ __launch_bounds__(256) void attn_fwd_generic_k(AttnArgs a) {
 #pragma unroll
   for (int m = 0; m < NO; ++m) acc[m] = 0.f;
   float l = 0.f;
-  const int kend = std::min(q0 + GB, T_);  // causal: keys < q0 + GB
+  const bool causal = a.causal != 0;
+  const int kend = causal ? std::min(q0 + GB, T_) : T_;  // causal: keys < q0 + GB
   for (int k0 = 0; k0 < kend; k0 += GB) {
     __syncthreads();
     load_tile<T, DMAX>(sm.b, k, a.sk[2], k0, T_, D);
@@ -74,10 +77,11 @@ __global__ __launch_bounds__(256) void attn_fwd_generic_k(AttnArgs a) {
       const int c = cl + 8 * m, j = k0 + c;
       float dot = 0.f;
       for (int d = 0; d < D; ++d) dot = fmaf(sm.a[r][d], sm.b[c][d], dot);
-      const float s = dot * a.scale - slope * (float)(i - j);  // forward.py:129-133
-      const float sg = rsig(s);                                // forward.py:137-140
+      const float s = dot * a.scale - slope * fabsf((float)(i - j));  // forward.py:129-133
+      const float sg = rsig(s);                                       // forward.py:137-140
       const float s2 = sg * sg;
-      sm.p[r][c] = (j <= i && i < T_) ? s2 * s2 : 0.f;
+      const bool vis = (causal ? j <= i : j < T_) && i < T_ && key_ok(a, b, j);
+      sm.p[r][c] = vis ? s2 * s2 : 0.f;
     }
     __syncthreads();
     for (int c = 0; c < GB; ++c) {
@@ -161,7 +165,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_generic_k(AttnArgs a,
   float acc[NO];
 #pragma unroll
   for (int m = 0; m < NO; ++m) acc[m] = 0.f;
-  const int kend = std::min(q0 + GB, T_);
+  const bool causal = a.causal != 0;
+  const int kend = causal ? std::min(q0 + GB, T_) : T_;
   for (int k0 = 0; k0 < kend; k0 += GB) {
     __syncthreads();
     load_tile<T, DMAX>(sm.b, k, a.sk[2], k0, T_, D);
@@ -177,13 +182,14 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_generic_k(AttnArgs a,
         dp = fmaf(sm.c[r][d], sm.d[c][d], dp);
       }
       // backward.py:133-151
-      const float s = dot * a.scale - slope * (float)(i - j);
+      const float s = dot * a.scale - slope * fabsf((float)(i - j));
       const float den = fabsf(s) + 1.f;
       const float sg = 0.5f * (s / den + 1.f);
       const float s2 = sg * sg;
       const float p = s2 * s2 / (Li + a.eps);
       const float g = 2.f / (den * den * (sg + a.eps));
-      sm.s[r][c] = (j <= i && i < T_) ? p * g * (dp - Di) : 0.f;
+      const bool vis = (causal ? j <= i : j < T_) && i < T_ && key_ok(a, b, j);
+      sm.s[r][c] = vis ? p * g * (dp - Di) : 0.f;
     }
     __syncthreads();
     for (int c = 0; c < GB; ++c) {
@@ -223,7 +229,9 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_generic_k(AttnArgs a,
   float dk[NO], dv[NO];
 #pragma unroll
   for (int m = 0; m < NO; ++m) dk[m] = dv[m] = 0.f;
-  for (int q0 = (k0 / GB) * GB; q0 < T_; q0 += GB) {  // causal: queries >= k0
+  const bool causal = a.causal != 0;
+  const bool jok = j < T_ && key_ok(a, b, j);
+  for (int q0 = causal ? (k0 / GB) * GB : 0; q0 < T_; q0 += GB) {  // causal: queries >= k0
     __syncthreads();
     load_tile<T, DMAX>(sm.c, q, a.sq[2], q0, T_, D);
     load_tile<T, DMAX>(sm.d, dO, a.sdo[2], q0, T_, D);
@@ -242,13 +250,13 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_generic_k(AttnArgs a,
         dp = fmaf(sm.d[c][d], sm.b[r][d], dp);
       }
       // backward.py:233-254
-      const float s = dot * a.scale - slope * (float)(i - j);
+      const float s = dot * a.scale - slope * fabsf((float)(i - j));
       const float den = fabsf(s) + 1.f;
       const float sg = 0.5f * (s / den + 1.f);
       const float s2 = sg * sg;
       const float p = s2 * s2 / (sm.r0[c] + a.eps);
       const float g = 2.f / (den * den * (sg + a.eps));
-      const bool ok = j <= i && i < T_ && j < T_;
+      const bool ok = (!causal || j <= i) && i < T_ && jok;
       sm.p[r][c] = ok ? p : 0.f;
       sm.s[r][c] = ok ? p * g * (dp - sm.r1[c]) : 0.f;
     }

@@ -51,17 +51,23 @@ constexpr int kNW = 4;         // waves per block
 constexpr int kRows = 32;      // rows owned per wave
 constexpr int kBM = kNW * kRows;  // rows owned per block
 constexpr int kBN = 64;        // streamed rows per LDS tile
+// kernel modes: causal (keys j <= i) and a key padding mask; the reference's
+// configuration is kModeCausal alone
+constexpr int kModeCausal = 1;
+constexpr int kModeKeyMask = 2;
 
 // ============================================================================
 // Forward: 128 queries per block, 4 waves x 32 queries, 2 blocks per CU.
 //   S^T[key][q]  = K Q^T (+ bias)   A = K  (LDS rows)         B = Q^T (VGPRs)
 //   O^T[d][q]   += V^T P^T          A = V^T (LDS transposed)  B = P^T (from S^T)
 // ============================================================================
-template <typename T, int D>
+template <typename T, int D, int MODE>
 __global__ __launch_bounds__(256, 2) void attn_fwd_k(AttnArgs a) {
   typedef Mfma<T> M;
   constexpr int KK = D / 32;  // k-steps of QK^T
   constexpr int DS = D / 16;  // 16-wide d subtiles of O^T
+  constexpr bool kCausal = (MODE & kModeCausal) != 0;
+  constexpr bool kKM = (MODE & kModeKeyMask) != 0;
   __shared__ short sk[2][kBN * D];
   __shared__ short sv[2][kBN * D];
 
@@ -98,6 +104,15 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_k(AttnArgs a) {
   f32x4 cb;
 #pragma unroll
   for (int j = 0; j < 4; ++j) cb[j] = (slope / scale) * (float)(4 * g + j - li);
+  // the bias in use, sgn slope (key - q): sgn = +1 gives -slope |i - j| on and
+  // below the diagonal; non-causal mode switches to sgn = -1 (negating cbx in
+  // place) from the first tile wholly above it on
+  f32x4 cbx = cb;
+  float sgn = 1.f;
+  // key validity of the current tile (bit r: key k0 + r), and its first key
+  uint64_t vm = ~0ull;
+  int kcur = 0;
+  const uint8_t* kmb = kKM ? a.km + (int64_t)b * a.skm : nullptr;
 
   f32x4 oacc[DS][2];
 #pragma unroll
@@ -113,7 +128,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_k(AttnArgs a) {
   // S^T of the 16 keys at tile rows hr .. hr + 15
   auto m1 = [&](int hr, f32x4 (&s_)[2], const short* ks_) __attribute__((always_inline)) {
 #pragma unroll
-    for (int qs = 0; qs < 2; ++qs) s_[qs] = cb;
+    for (int qs = 0; qs < 2; ++qs) s_[qs] = cbx;
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {
       const i16x8 kf = lds16(ks_ + soff<D>(hr + li, 32 * kk + 8 * g));
@@ -121,21 +136,33 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_k(AttnArgs a) {
       for (int qs = 0; qs < 2; ++qs) s_[qs] = M::mma(kf, qf[qs][kk], s_[qs]);
     }
   };
-  // f' of those scores, packed as P^T; row sums into lsum
-  auto vh = [&](auto mask_tag, int kh, const f32x4 (&s_)[2], uint32_t (&pk)[2][2]) __attribute__((always_inline)) {
-    constexpr bool MASK = decltype(mask_tag)::value;
+  // f' of those scores, packed as P^T; row sums into lsum. MASKED: the
+  // per-score work of a tile that straddles the diagonal or holds invalid
+  // keys -- causal: keys past the query get f' = 0; non-causal: scores whose
+  // bias form has the wrong sign for |i - j| are corrected; keys outside the
+  // validity mask (padding mask, or past T) get f' = 0.
+  auto vh = [&](auto masked_tag, int kh, const f32x4 (&s_)[2], uint32_t (&pk)[2][2]) __attribute__((always_inline)) {
+    constexpr bool MASKED = decltype(masked_tag)::value;
+    constexpr bool kVM = kKM || !kCausal;  // a validity mask exists
+    uint32_t nib = 0;
+    if constexpr (MASKED && kVM) nib = (uint32_t)(vm >> (kh - kcur + 4 * g));
 #pragma unroll
     for (int qs = 0; qs < 2; ++qs) {
-      const float tterm = slope * (float)(kh - qw - 16 * qs);
+      const float tterm = (kCausal ? slope : sgn * slope) * (float)(kh - qw - 16 * qs);
       float f[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const float s = fmaf(s_[qs][j], scale, tterm);
+        float s = fmaf(s_[qs][j], scale, tterm);
+        if constexpr (MASKED && !kCausal) {
+          const float sd = sgn * (float)((kh + 4 * g + j) - (qw + 16 * qs + li));
+          if (sd > 0.f) s = fmaf(-2.f * slope, sd, s);
+        }
         const float r = __builtin_amdgcn_rcpf(fabsf(s) + 1.f);
         const float t = fmaf(s, r, 1.f);
         const float t2 = t * t;
         f[j] = t2 * t2;
-        if (MASK && kh + 4 * g + j > qw + 16 * qs + li) f[j] = 0.f;
+        if (MASKED && kCausal && kh + 4 * g + j > qw + 16 * qs + li) f[j] = 0.f;
+        if (MASKED && kVM && !((nib >> j) & 1u)) f[j] = 0.f;
       }
       lsum[qs] += (f[0] + f[1]) + (f[2] + f[3]);
       pk[qs][0] = M::pack2(f[0], f[1]);
@@ -154,22 +181,61 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_k(AttnArgs a) {
       for (int qs = 0; qs < 2; ++qs) oacc[ds][qs] = M::mma(vt, pf[qs], oacc[ds][qs]);
     }
   };
-  auto tile = [&](auto mask_tag, int k0, const short* ks_, const short* vs_) __attribute__((always_inline)) {
+  auto tile = [&](auto masked_tag, int k0, const short* ks_, const short* vs_) __attribute__((always_inline)) {
     f32x4 sA[2], sB[2];
     uint32_t pa0[2][2], pb0[2][2], pa1[2][2], pb1[2][2];
     m1(0, sA, ks_);
     m1(16, sB, ks_);
-    vh(mask_tag, k0, sA, pa0);
+    vh(masked_tag, k0, sA, pa0);
     m1(32, sA, ks_);
-    vh(mask_tag, k0 + 16, sB, pb0);
+    vh(masked_tag, k0 + 16, sB, pb0);
     m2(0, pa0, pb0, vs_);
     m1(48, sB, ks_);
-    vh(mask_tag, k0 + 32, sA, pa1);
-    vh(mask_tag, k0 + 48, sB, pb1);
+    vh(masked_tag, k0 + 32, sA, pa1);
+    vh(masked_tag, k0 + 48, sB, pb1);
     m2(32, pa1, pb1, vs_);
   };
+  // which variant a tile takes. Causal without a padding mask: below the
+  // diagonal plain, straddling it masked, above it skipped. Otherwise a tile
+  // wholly on one side of the diagonal (causal: below it) with every key valid
+  // takes the plain path, a tile with no valid key is skipped, and any other
+  // tile takes the masked one; non-causal mode switches the bias sign at the
+  // first tile wholly above the diagonal.
+  auto tile_step = [&](int k0, const short* ks_, const short* vs_) __attribute__((always_inline)) {
+    if constexpr (kCausal && !kKM) {
+      if (k0 + kBN - 1 <= qw)
+        tile(std::false_type{}, k0, ks_, vs_);
+      else if (k0 <= qw + kRows - 1)
+        tile(std::true_type{}, k0, ks_, vs_);
+    } else {
+      bool plain;
+      if constexpr (kCausal) {
+        plain = k0 + kBN - 1 <= qw;
+      } else {
+        const bool above = k0 > qw + kRows - 1;
+        if (above && sgn > 0.f) {
+          cbx = -cbx;
+          sgn = -1.f;
+        }
+        plain = above || k0 + kBN - 1 <= qw;
+      }
+      plain = plain && vm == ~0ull;
+      if (vm == 0ull || (kCausal && k0 > qw + kRows - 1)) {
+      } else if (plain) {
+        tile(std::false_type{}, k0, ks_, vs_);
+      } else {
+        tile(std::true_type{}, k0, ks_, vs_);
+      }
+    }
+  };
 
-  const int n_kt = (std::min(q0 + kBM, T_) + kBN - 1) / kBN;
+  const int n_kt = kCausal ? (std::min(q0 + kBM, T_) + kBN - 1) / kBN : (T_ + kBN - 1) / kBN;
+  // this lane's padding-mask byte of key tile kt (0 past the end)
+  auto kmbyte = [&](int kt) __attribute__((always_inline)) {
+    const int j = kt * kBN + lane;
+    return (kKM && j < T_) ? (uint32_t)kmb[j] : 0u;
+  };
+  uint32_t kmn = kmbyte(0);  // loaded one tile ahead of its use
   dk.issue(sk[0], kp, kbytes, 0, sk2, w);
   dv.issue(sv[0], vp, vbytes, 0, sv2, w);
   dma_wait();
@@ -184,10 +250,14 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_k(AttnArgs a) {
       dv.issue(sv[buf ^ 1], vp, vbytes, (kt + 1) * kBN, sv2, w);
     }
     const int k0 = kt * kBN;
-    if (k0 + kBN - 1 <= qw)
-      tile(std::false_type{}, k0, sk[buf], sv[buf]);
-    else if (k0 <= qw + kRows - 1)
-      tile(std::true_type{}, k0, sk[buf], sv[buf]);
+    kcur = k0;
+    if constexpr (kKM) {
+      vm = __builtin_amdgcn_ballot_w64(kmn != 0u);
+      if (kt + 1 < n_kt) kmn = kmbyte(kt + 1);
+    } else if constexpr (!kCausal) {
+      vm = T_ - k0 >= kBN ? ~0ull : (1ull << (T_ - k0)) - 1ull;
+    }
+    tile_step(k0, sk[buf], sv[buf]);
     dma_wait();
     __syncthreads();
   };
@@ -247,12 +317,14 @@ __global__ __launch_bounds__(256) void attn_bwd_prep_k(AttnArgs a, f16* __restri
 // stats_i = (4 cinv_i, -4 cinv_i Delta_i), and writes stats and the fp16 copy
 // of Q (clamped to +-65504) for the dK / dV kernel, which runs after it.
 // ============================================================================
-template <typename T, int D>
+template <typename T, int D, int MODE>
 __global__ __launch_bounds__(256, 2) void attn_bwd_dq_k(AttnArgs a, float2* __restrict__ stats,
                                                         f16* __restrict__ q16, const f16* __restrict__ k16) {
   typedef Mfma<T> M;
   constexpr int KK = D / 32;
   constexpr int DS = D / 16;
+  constexpr bool kCausal = (MODE & kModeCausal) != 0;
+  constexpr bool kKM = (MODE & kModeKeyMask) != 0;
   __shared__ short sk[2][kBN * D];
   __shared__ short sv[2][kBN * D];
 
@@ -315,6 +387,12 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_k(AttnArgs a, float2* __re
   f32x4 cb;
 #pragma unroll
   for (int j = 0; j < 4; ++j) cb[j] = (slope / scale) * (float)(4 * g + j - li);
+  // bias in use and key validity of the current tile, as in the forward
+  f32x4 cbx = cb;
+  float sgn = 1.f;
+  uint64_t vm = ~0ull;
+  int kcur = 0;
+  const uint8_t* kmb = kKM ? a.km + (int64_t)b * a.skm : nullptr;
 
   f32x4 dqacc[DS][2];
 #pragma unroll
@@ -330,7 +408,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_k(AttnArgs a, float2* __re
   auto m1 = [&](int hr, f32x4 (&s_)[2], f32x4 (&p_)[2], const short* ks_, const short* vs_) __attribute__((always_inline)) {
 #pragma unroll
     for (int qs = 0; qs < 2; ++qs) {
-      s_[qs] = cb;
+      s_[qs] = cbx;
       p_[qs] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 #pragma unroll
@@ -344,21 +422,29 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_k(AttnArgs a, float2* __re
       }
     }
   };
-  // dS of those scores, packed fp16 as dS^T
-  auto vh = [&](auto mask_tag, int kh, const f32x4 (&s_)[2], const f32x4 (&p_)[2], uint32_t (&pk)[2][2]) __attribute__((always_inline)) {
-    constexpr bool MASK = decltype(mask_tag)::value;
+  // dS of those scores, packed fp16 as dS^T (MASKED as in the forward)
+  auto vh = [&](auto masked_tag, int kh, const f32x4 (&s_)[2], const f32x4 (&p_)[2], uint32_t (&pk)[2][2]) __attribute__((always_inline)) {
+    constexpr bool MASKED = decltype(masked_tag)::value;
+    constexpr bool kVM = kKM || !kCausal;
+    uint32_t nib = 0;
+    if constexpr (MASKED && kVM) nib = (uint32_t)(vm >> (kh - kcur + 4 * g));
 #pragma unroll
     for (int qs = 0; qs < 2; ++qs) {
-      const float tterm = slope * (float)(kh - qw - 16 * qs);
+      const float tterm = (kCausal ? slope : sgn * slope) * (float)(kh - qw - 16 * qs);
       float d[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const float s = fmaf(s_[qs][j], scale, tterm);
+        float s = fmaf(s_[qs][j], scale, tterm);
+        if constexpr (MASKED && !kCausal) {
+          const float sd = sgn * (float)((kh + 4 * g + j) - (qw + 16 * qs + li));
+          if (sd > 0.f) s = fmaf(-2.f * slope, sd, s);
+        }
         const float r = __builtin_amdgcn_rcpf(fabsf(s) + 1.f);
         const float t = fmaf(s, r, 1.f);
         const float u = t * r;
         d[j] = (u * u * t) * fmaf(p_[qs][j], c4[qs], nc4d[qs]);
-        if (MASK && kh + 4 * g + j > qw + 16 * qs + li) d[j] = 0.f;
+        if (MASKED && kCausal && kh + 4 * g + j > qw + 16 * qs + li) d[j] = 0.f;
+        if (MASKED && kVM && !((nib >> j) & 1u)) d[j] = 0.f;
       }
       pk[qs][0] = pack2_f16(d[0], d[1]);
       pk[qs][1] = pack2_f16(d[2], d[3]);
@@ -376,22 +462,60 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_k(AttnArgs a, float2* __re
       for (int qs = 0; qs < 2; ++qs) dqacc[ds][qs] = mma_f16(kt, dsf[qs], dqacc[ds][qs]);
     }
   };
-  auto tile = [&](auto mask_tag, int k0, const short* ks_, const short* vs_) __attribute__((always_inline)) {
+  auto tile = [&](auto masked_tag, int k0, const short* ks_, const short* vs_) __attribute__((always_inline)) {
     f32x4 sA[2], pA[2], sB[2], pB[2];
     uint32_t da0[2][2], db0[2][2], da1[2][2], db1[2][2];
     m1(0, sA, pA, ks_, vs_);
     m1(16, sB, pB, ks_, vs_);
-    vh(mask_tag, k0, sA, pA, da0);
+    vh(masked_tag, k0, sA, pA, da0);
     m1(32, sA, pA, ks_, vs_);
-    vh(mask_tag, k0 + 16, sB, pB, db0);
+    vh(masked_tag, k0 + 16, sB, pB, db0);
     m2(0, da0, db0, ks_);
     m1(48, sB, pB, ks_, vs_);
-    vh(mask_tag, k0 + 32, sA, pA, da1);
-    vh(mask_tag, k0 + 48, sB, pB, db1);
+    vh(masked_tag, k0 + 32, sA, pA, da1);
+    vh(masked_tag, k0 + 48, sB, pB, db1);
     m2(32, da1, db1, ks_);
   };
+  // which variant a tile takes. Causal without a padding mask: below the
+  // diagonal plain, straddling it masked, above it skipped. Otherwise a tile
+  // wholly on one side of the diagonal (causal: below it) with every key valid
+  // takes the plain path, a tile with no valid key is skipped, and any other
+  // tile takes the masked one; non-causal mode switches the bias sign at the
+  // first tile wholly above the diagonal.
+  auto tile_step = [&](int k0, const short* ks_, const short* vs_) __attribute__((always_inline)) {
+    if constexpr (kCausal && !kKM) {
+      if (k0 + kBN - 1 <= qw)
+        tile(std::false_type{}, k0, ks_, vs_);
+      else if (k0 <= qw + kRows - 1)
+        tile(std::true_type{}, k0, ks_, vs_);
+    } else {
+      bool plain;
+      if constexpr (kCausal) {
+        plain = k0 + kBN - 1 <= qw;
+      } else {
+        const bool above = k0 > qw + kRows - 1;
+        if (above && sgn > 0.f) {
+          cbx = -cbx;
+          sgn = -1.f;
+        }
+        plain = above || k0 + kBN - 1 <= qw;
+      }
+      plain = plain && vm == ~0ull;
+      if (vm == 0ull || (kCausal && k0 > qw + kRows - 1)) {
+      } else if (plain) {
+        tile(std::false_type{}, k0, ks_, vs_);
+      } else {
+        tile(std::true_type{}, k0, ks_, vs_);
+      }
+    }
+  };
 
-  const int n_kt = (std::min(q0 + kBM, T_) + kBN - 1) / kBN;
+  const int n_kt = kCausal ? (std::min(q0 + kBM, T_) + kBN - 1) / kBN : (T_ + kBN - 1) / kBN;
+  auto kmbyte = [&](int kt) __attribute__((always_inline)) {
+    const int j = kt * kBN + lane;
+    return (kKM && j < T_) ? (uint32_t)kmb[j] : 0u;
+  };
+  uint32_t kmn = kmbyte(0);
   dk.issue(sk[0], kp, kbytes, 0, D, w);
   dv.issue(sv[0], vp, vbytes, 0, sv2, w);
   dma_wait();
@@ -404,10 +528,14 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_k(AttnArgs a, float2* __re
       dv.issue(sv[buf ^ 1], vp, vbytes, (kt + 1) * kBN, sv2, w);
     }
     const int k0 = kt * kBN;
-    if (k0 + kBN - 1 <= qw)
-      tile(std::false_type{}, k0, sk[buf], sv[buf]);
-    else if (k0 <= qw + kRows - 1)
-      tile(std::true_type{}, k0, sk[buf], sv[buf]);
+    kcur = k0;
+    if constexpr (kKM) {
+      vm = __builtin_amdgcn_ballot_w64(kmn != 0u);
+      if (kt + 1 < n_kt) kmn = kmbyte(kt + 1);
+    } else if constexpr (!kCausal) {
+      vm = T_ - k0 >= kBN ? ~0ull : (1ull << (T_ - k0)) - 1ull;
+    }
+    tile_step(k0, sk[buf], sv[buf]);
     dma_wait();
     __syncthreads();
   };
@@ -458,13 +586,15 @@ struct DkvSmem {
   f32x4 x[2][kNW][4][64];   // w: [chunk parity][key group][16-query half x ks][lane]
 };
 
-template <typename T, int D>
+template <typename T, int D, int MODE>
 __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float2* __restrict__ stats,
                                                          const f16* __restrict__ q16) {
   typedef Mfma<T> M;
   constexpr int KK = D / 32;
   constexpr int DS = D / 16;
   constexpr int NW = 2 * kNW;
+  constexpr bool kCausal = (MODE & kModeCausal) != 0;
+  constexpr bool kKM = (MODE & kModeKeyMask) != 0;
   __shared__ DkvSmem<D> sm;
 
   const int T_ = a.T, H = a.H;
@@ -509,6 +639,25 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
   f32x4 cb;
 #pragma unroll
   for (int j = 0; j < 4; ++j) cb[j] = (slope / scale) * (float)(li - 4 * g - j);
+  // bias in use (negated for query chunks wholly below this wave's keys in
+  // non-causal mode)
+  f32x4 cbx = cb;
+  float slx = slope;
+  // Padding mask: a dropped key's P and dS column is zero, so its dK / dV
+  // rows are zero and the other keys' rows do not depend on it. The kernel
+  // computes every key and stores zeros for dropped ones; a wave group whose
+  // 32 keys are all dropped skips the work.
+  bool kval[2] = {true, true};
+  bool gany = true;
+  if constexpr (kKM) {
+    const uint8_t* kmb = a.km + (int64_t)b * a.skm;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int key = kw + 16 * ks + li;
+      kval[ks] = key < T_ && kmb[key] != 0;
+    }
+    gany = __builtin_amdgcn_ballot_w64(kval[0] || kval[1]) != 0ull;
+  }
 
   f32x4 acc[DS][2];  // dV^T (P role) or dK^T (D role)
 #pragma unroll
@@ -534,7 +683,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
   auto m1 = [&](auto role, int hr, f32x4 (&s_)[2], const short* as_) __attribute__((always_inline)) {
     constexpr bool P = decltype(role)::value;
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) s_[ks] = P ? cb : f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int ks = 0; ks < 2; ++ks) s_[ks] = P ? cbx : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {
       const i16x8 fa = lds16(as_ + soff<D>(hr + li, 32 * kk + 8 * g));
@@ -545,28 +694,34 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
       }
     }
   };
-  // P role: P (input dtype) of a 16-query half, and w into the exchange buffer
-  auto vp_ = [&](auto mask_tag, int qh, int hr, const f32x4 (&s_)[2], const float2* st_, f32x4 (*xw)[64],
+  // P role: P (input dtype) of a 16-query half, and w into the exchange buffer.
+  // DIAG: a chunk that straddles the diagonal (causal: keys past the query get
+  // P = w = 0; non-causal: their bias becomes -slope (key - q)).
+  auto vp_ = [&](auto diag_tag, int qh, int hr, const f32x4 (&s_)[2], const float2* st_, f32x4 (*xw)[64],
                  int xg, uint32_t (&pp)[2][2]) __attribute__((always_inline)) {
-    constexpr bool MASK = decltype(mask_tag)::value;
+    constexpr bool DIAG = decltype(diag_tag)::value;
     const f32x4 s01 = *reinterpret_cast<const f32x4*>(st_ + hr + 4 * g);
     const f32x4 s23 = *reinterpret_cast<const f32x4*>(st_ + hr + 4 * g + 2);
     const float c4v[4] = {s01[0], s01[2], s23[0], s23[2]};
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      const float tterm = slope * (float)(kw + 16 * ks - qh);
+      const float tterm = slx * (float)(kw + 16 * ks - qh);
       float pv[4];
       f32x4 wv;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const float s = fmaf(s_[ks][j], scale, tterm);
+        float s = fmaf(s_[ks][j], scale, tterm);
+        if constexpr (DIAG && !kCausal) {
+          const int dkq = (kw + 16 * ks + li) - (qh + 4 * g + j);
+          if (dkq > 0) s = fmaf(-2.f * slope, (float)dkq, s);
+        }
         const float r = __builtin_amdgcn_rcpf(fabsf(s) + 1.f);
         const float t = fmaf(s, r, 1.f);
         const float t2 = t * t;
         const float u = t * r;
         pv[j] = (t2 * t2) * (0.25f * c4v[j]);
         wv[j] = u * u * t;
-        if (MASK && kw + 16 * ks + li > qh + 4 * g + j) {
+        if (DIAG && kCausal && kw + 16 * ks + li > qh + 4 * g + j) {
           pv[j] = 0.f;
           wv[j] = 0.f;
         }
@@ -595,12 +750,19 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
     }
   };
 
-  // chunk c: queries k0 + 32 c .. +31, tile (c / 2) in buffer (c / 2) & 1, rows 32 (c & 1)
-  const int n_it = k0 < T_ ? (T_ - k0 + kBN - 1) / kBN : 0;  // causal: queries >= k0
+  // chunk c: queries qbase + 32 c .. +31, tile (c / 2) in buffer (c / 2) & 1,
+  // rows 32 (c & 1); causal: queries from k0 on, non-causal: every query
+  const int qbase = kCausal ? k0 : 0;
+  const int n_it = qbase < T_ ? (T_ - qbase + kBN - 1) / kBN : 0;
   const int n_ch = 2 * n_it;
-  auto needc = [&](int c) __attribute__((always_inline)) { return c < n_ch && k0 + 32 * c + 31 >= kw; };
-  auto fullc = [&](int c) __attribute__((always_inline)) { return k0 + 32 * c >= kw + kRows - 1; };
-  if (n_it > 0) issue(0, k0);
+  auto needc = [&](int c) __attribute__((always_inline)) {
+    return c < n_ch && gany && (!kCausal || qbase + 32 * c + 31 >= kw);
+  };
+  // no key of the wave lies past a query of the chunk (non-causal: or every key does)
+  auto fullc = [&](int c) __attribute__((always_inline)) {
+    return qbase + 32 * c >= kw + kRows - 1 || (!kCausal && kw > qbase + 32 * c + 31);
+  };
+  if (n_it > 0) issue(0, qbase);
   dma_wait();
   __syncthreads();
   f32x4 dpA[2][2], dpB[2][2];  // D role: dP of the current and the next chunk
@@ -610,10 +772,15 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
   }
   auto step = [&](int c, f32x4 (&pcur)[2][2], f32x4 (&pnext)[2][2]) __attribute__((always_inline)) {
     const int it = c >> 1, buf = it & 1, r0 = 32 * (c & 1);
-    const int qc = k0 + 32 * c;
+    const int qc = qbase + 32 * c;
     const bool need = needc(c), full = need && fullc(c);
     f32x4 (*xw)[64] = sm.x[c & 1][grp];
     uint32_t pa[2][2], pb[2][2];
+    if constexpr (!kCausal) {
+      const bool above = kw > qc + 31;
+      cbx = above ? -cb : cb;
+      slx = above ? -slope : slope;
+    }
     if (prole && need) {
       f32x4 sA[2], sB[2];
       m1(std::true_type{}, r0, sA, sm.q[buf]);
@@ -629,7 +796,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
     if ((c & 1) == 0) {
       // every wave has left the previous tile: its buffer takes the next one
       __syncthreads();
-      if (it + 1 < n_it) issue(buf ^ 1, k0 + (it + 1) * kBN);
+      if (it + 1 < n_it) issue(buf ^ 1, qbase + (it + 1) * kBN);
     } else {
       // the next tile has landed (each wave waits for its own DMA)
       dma_wait();
@@ -686,7 +853,8 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
       T* row = outp + (int64_t)key * ostr;
 #pragma unroll
       for (int ds = 0; ds < DS; ++ds) {
-        const f32x4 v = acc[ds][ks];
+        f32x4 v = acc[ds][ks];
+        if (kKM && !kval[ks]) v = f32x4{0.f, 0.f, 0.f, 0.f};
         *reinterpret_cast<u32x2*>(row + 16 * ds + 4 * g) =
             u32x2{M::pack2(v[0] * osc, v[1] * osc), M::pack2(v[2] * osc, v[3] * osc)};
       }
@@ -718,13 +886,13 @@ bool offsets_ok(const AttnArgs& a, bool bwd) {
   return (int64_t)a.T * a.D * 2 < lim && (int64_t)a.T * 8 < lim;
 }
 
-template <typename T, int D> int launch_fwd(const AttnArgs& a, hipStream_t st) {
+template <typename T, int D, int MODE> int launch_fwd(const AttnArgs& a, hipStream_t st) {
   const int64_t nb = (int64_t)((a.T + kBM - 1) / kBM) * a.B * a.H;
-  hipLaunchKernelGGL((attn_fwd_k<T, D>), dim3((unsigned)nb), dim3(256), 0, st, a);
+  hipLaunchKernelGGL((attn_fwd_k<T, D, MODE>), dim3((unsigned)nb), dim3(256), 0, st, a);
   return check_launch("kat_attn_fwd (mfma)");
 }
 
-template <typename T, int D>
+template <typename T, int D, int MODE>
 int launch_bwd(const AttnArgs& a, void* ws, hipStream_t st) {
   const int64_t rows = (int64_t)a.B * a.H * a.T;
   auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
@@ -737,25 +905,34 @@ int launch_bwd(const AttnArgs& a, void* ws, hipStream_t st) {
   if (int rc = check_launch("kat_attn_bwd (prep)")) return rc;
   // dq also writes stats and q16, which the dK / dV kernel reads
   const int64_t nt = (int64_t)((a.T + kBM - 1) / kBM) * a.B * a.H;
-  hipLaunchKernelGGL((attn_bwd_dq_k<T, D>), dim3((unsigned)nt), dim3(256), 0, st, a, stats, q16, k16);
+  hipLaunchKernelGGL((attn_bwd_dq_k<T, D, MODE>), dim3((unsigned)nt), dim3(256), 0, st, a, stats, q16, k16);
   if (int rc = check_launch("kat_attn_bwd (dq, mfma)")) return rc;
-  hipLaunchKernelGGL((attn_bwd_dkv_k<T, D>), dim3((unsigned)nt), dim3(512), 0, st, a, stats, q16);
+  hipLaunchKernelGGL((attn_bwd_dkv_k<T, D, MODE>), dim3((unsigned)nt), dim3(512), 0, st, a, stats, q16);
   return check_launch("kat_attn_bwd (dkv, mfma)");
 }
 
 }  // namespace
 
+// the kernel mode of a call: causal or not, with or without a padding mask
+#define KAT_MODE_SWITCH(a, ...)                                                  \
+  switch ((a.causal ? kModeCausal : 0) | (a.km != nullptr ? kModeKeyMask : 0)) { \
+    case kModeCausal: { constexpr int MODE = kModeCausal; __VA_ARGS__; }         \
+    case kModeCausal | kModeKeyMask: { constexpr int MODE = kModeCausal | kModeKeyMask; __VA_ARGS__; } \
+    case kModeKeyMask: { constexpr int MODE = kModeKeyMask; __VA_ARGS__; }       \
+    default: { constexpr int MODE = 0; __VA_ARGS__; }                            \
+  }
+
 template <typename T> int attn_fwd_mfma(const AttnArgs& a, hipStream_t st) {
   if ((int64_t)((a.T + kBM - 1) / kBM) * a.B * a.H > 0x7fffffffLL || !offsets_ok(a, false)) return KAT_EUNSUPPORTED;
-  if (a.D == 128) return launch_fwd<T, 128>(a, st);
-  if (a.D == 64) return launch_fwd<T, 64>(a, st);
+  if (a.D == 128) KAT_MODE_SWITCH(a, return (launch_fwd<T, 128, MODE>(a, st)));
+  if (a.D == 64) KAT_MODE_SWITCH(a, return (launch_fwd<T, 64, MODE>(a, st)));
   return KAT_EUNSUPPORTED;
 }
 
 template <typename T> int attn_bwd_mfma(const AttnArgs& a, void* ws, hipStream_t st) {
   if ((int64_t)((a.T + kBM - 1) / kBM) * a.B * a.H > 0x7fffffffLL || !offsets_ok(a, true)) return KAT_EUNSUPPORTED;
-  if (a.D == 128) return launch_bwd<T, 128>(a, ws, st);
-  if (a.D == 64) return launch_bwd<T, 64>(a, ws, st);
+  if (a.D == 128) KAT_MODE_SWITCH(a, return (launch_bwd<T, 128, MODE>(a, ws, st)));
+  if (a.D == 64) KAT_MODE_SWITCH(a, return (launch_bwd<T, 64, MODE>(a, ws, st)));
   return KAT_EUNSUPPORTED;
 }
 

@@ -40,9 +40,20 @@ def _unit_d(t):
     return t if t.stride(-1) == 1 or t.shape[-1] == 1 else t.contiguous()
 
 
-def _attn_fwd_into(q, k, v, out, L, alibi_slopes, scale, causal, eps):
-    """Launch kat_attn_fwd on [B,H,T,D] q, k, v and out (any (b, h, t) strides,
-    unit d-stride) and L [B,H,T] fp32."""
+def _key_mask_arg(key_mask, B, T, device):
+    """The padding mask as a uint8 [B, T] device tensor (nonzero = attend), or None."""
+    if key_mask is None:
+        return None
+    assert tuple(key_mask.shape) == (B, T), f"key_mask must be [B, T] = [{B}, {T}]"
+    return (key_mask.to(device) != 0).to(torch.uint8).contiguous()
+
+
+def _attn_fwd_into(q, k, v, out, L, alibi_slopes, scale, causal, eps, key_mask=None,
+                   extended=False):
+    """Launch the attention forward on [B,H,T,D] q, k, v and out (any (b, h, t)
+    strides, unit d-stride) and L [B,H,T] fp32. ``extended`` selects
+    kat_attn_fwd_masked, which applies ``key_mask`` (uint8 [B, T] or None) and
+    honours ``causal``; otherwise kat_attn_fwd, always causal as the reference."""
     lib = _lib.load()
     B, H, T, D = q.shape
     slopes = alibi_slopes.to(device=q.device, dtype=torch.float32).contiguous()
@@ -50,10 +61,17 @@ def _attn_fwd_into(q, k, v, out, L, alibi_slopes, scale, causal, eps):
     strides = _lib.i64_array(_bht_strides(q) + _bht_strides(k) + _bht_strides(v) +
                              _bht_strides(out))
     lstr = _lib.i64_array(_bht_strides(L))
-    _lib.check(lib.kat_attn_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
-                                L.data_ptr(), slopes.data_ptr(), B, H, T, D, strides, lstr,
-                                float(scale), float(eps), int(bool(causal)),
-                                _lib.dtype_code(q), _lib.stream(q)), "kat_attn_fwd")
+    if not extended:
+        _lib.check(lib.kat_attn_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                                    L.data_ptr(), slopes.data_ptr(), B, H, T, D, strides, lstr,
+                                    float(scale), float(eps), int(bool(causal)),
+                                    _lib.dtype_code(q), _lib.stream(q)), "kat_attn_fwd")
+        return
+    km_ptr = None if key_mask is None else key_mask.data_ptr()
+    _lib.check(lib.kat_attn_fwd_masked(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                                       L.data_ptr(), slopes.data_ptr(), km_ptr, T, B, H, T, D,
+                                       strides, lstr, float(scale), float(eps), int(bool(causal)),
+                                       _lib.dtype_code(q), _lib.stream(q)), "kat_attn_fwd_masked")
 
 
 def rational_attention_forward(q, k, v, alibi_slopes, scale, causal=True, eps=EPS):

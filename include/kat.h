@@ -172,6 +172,30 @@ int kat_attn_bwd(const void* q, const void* k, const void* v, const void* out,
                  const int64_t* l_strides, float scale, float eps, int causal, int dtype,
                  void* stream);
 
+/* Attention with a key padding mask and an optional non-causal mode; no
+ * counterpart launch in the reference, whose kernels ignore both (forward.py:273,
+ * backward.py:282) while its model's CPU path applies the padding mask
+ * (algebraic_model.py:112-136, mask == 0 drops a key, :129-131).
+ *   key_mask: uint8 [B, T], element (b, j) at key_mask[b * mask_stride_b + j];
+ *             key j of batch b is attended iff it is nonzero. NULL: every key.
+ *   causal:   nonzero -> keys j <= i (as kat_attn_fwd); 0 -> every key, with
+ *             ALiBi -slope * |i - j| (the CPU path's form, :118-121).
+ * A dropped key contributes nothing (the CPU path's -1e4 fill leaves
+ * sigma(-1e4)^4 ~ 6e-18 per key); a query with no visible key gets L = 0,
+ * o = 0, dq = 0, and dropped keys get dk = dv = 0. Other arguments, layouts
+ * and workspace as kat_attn_fwd / kat_attn_bwd. */
+int kat_attn_fwd_masked(const void* q, const void* k, const void* v, void* out, float* L,
+                        const float* slopes, const uint8_t* key_mask, int64_t mask_stride_b,
+                        int64_t B, int64_t H, int64_t T, int64_t D, const int64_t* strides,
+                        const int64_t* l_strides, float scale, float eps, int causal, int dtype,
+                        void* stream);
+int kat_attn_bwd_masked(const void* q, const void* k, const void* v, const void* out,
+                        const float* L, const void* dout, void* dq, void* dk, void* dv,
+                        const float* slopes, const uint8_t* key_mask, int64_t mask_stride_b,
+                        void* workspace, size_t workspace_bytes, int64_t B, int64_t H, int64_t T,
+                        int64_t D, const int64_t* strides, const int64_t* l_strides, float scale,
+                        float eps, int causal, int dtype, void* stream);
+
 /* ----------------------------------------------------------------------
  * Measurement helper (no counterpart in the reference; used by bench.py to
  * report a measured MFMA rate beside the spec peak). `blocks` x 256 threads

@@ -138,17 +138,27 @@ def alibi_slopes(n_heads):
 
 # ---------------------------------------------------------------------------
 # rational attention -- fwd forward.py:49-159 ; bwd backward.py:62-266
-# Layout [B, H, T, D]; always causal (forward.py:110, backward.py:125,222).
+# Layout [B, H, T, D]. The reference kernels are always causal
+# (forward.py:110, backward.py:125,222). Two extensions, following the
+# reference model's CPU attention (algebraic_model.py:112-136): a key padding
+# mask [B, T] (key j of batch b is dropped where mask[b, j] == 0,
+# algebraic_model.py:129-131) and a non-causal mode (every key visible, ALiBi
+# -slope * |i - j| as that CPU path writes it, algebraic_model.py:118-121).
+# Dropped keys contribute exactly nothing here (the reference CPU path's -1e4
+# fill leaves sigma(-1e4)^4 ~ 6e-18 per key).
 # ---------------------------------------------------------------------------
 
-def _scores(q, k, slopes, scale):
+def _scores(q, k, slopes, scale, causal=True, key_mask=None):
     # forward.py:129-133: s = (q.k) * scale - slope * |i - j|
     T = q.shape[-2]
     s = torch.matmul(q, k.transpose(-1, -2)) * scale
     pos = torch.arange(T)
     dist = (pos[:, None] - pos[None, :]).abs().to(q.dtype)
     s = s - slopes.to(q.dtype).view(1, -1, 1, 1) * dist
-    keep = pos[None, :] <= pos[:, None]
+    keep = (pos[None, :] <= pos[:, None]) if causal else torch.ones(T, T, dtype=torch.bool)
+    keep = keep[None, None]
+    if key_mask is not None:
+        keep = keep & (key_mask.to("cpu") != 0)[:, None, None, :]
     return s, keep
 
 
@@ -161,19 +171,25 @@ def _chunks(B, H, chunk):
             yield slice(b, b + 1), slice(h0, min(H, h0 + chunk))
 
 
-def attention_fwd(q, k, v, slopes, scale, eps=EPS, dtype=torch.float64, chunk=None):
+def _mask_rows(key_mask, bs):
+    return None if key_mask is None else key_mask[bs]
+
+
+def attention_fwd(q, k, v, slopes, scale, eps=EPS, dtype=torch.float64, chunk=None,
+                  causal=True, key_mask=None):
     """Returns (o, L). f = sigma(s)^4 for j <= i only (the kernel never visits
     j > i, forward.py:110,119); L = sum f stored WITHOUT eps (forward.py:159);
     o = sum f v / (L + eps) (forward.py:150-151). ``chunk`` bounds memory by
     processing ``chunk`` heads of one batch entry at a time (heads are
-    independent)."""
+    independent). ``causal=False`` / ``key_mask``: the extensions above."""
     q, k, v = _up(q, dtype), _up(k, dtype), _up(v, dtype)
     slopes = _up(slopes, dtype)
     B, H, T, D = q.shape
     o = torch.empty_like(q)
     L = torch.empty(B, H, T, dtype=dtype)
     for bs, hs in _chunks(B, H, chunk):
-        s, keep = _scores(q[bs, hs], k[bs, hs], slopes[hs], scale)
+        s, keep = _scores(q[bs, hs], k[bs, hs], slopes[hs], scale, causal,
+                          _mask_rows(key_mask, bs))
         f = torch.where(keep, _sig4(s), torch.zeros((), dtype=dtype))
         l = f.sum(dim=-1)
         L[bs, hs] = l
@@ -187,12 +203,13 @@ def attention_delta(o, do, dtype=torch.float64):
 
 
 def attention_bwd(q, k, v, o, L, do, slopes, scale, eps=EPS, dtype=torch.float64,
-                  chunk=None):
+                  chunk=None, causal=True, key_mask=None):
     """Returns (dq, dk, dv) following backward.py:116-154 (dQ) and
     backward.py:232-260 (dK, dV):
       p = f / (L + eps),  g = 2 / ((|s|+1)^2 (sigma + eps)),
       dS = p * g * (dO.v - Delta),  dQ = scale dS K,  dK = scale dS^T Q,
-      dV = P^T dO ;  only pairs j <= i contribute."""
+      dV = P^T dO ;  only pairs j <= i contribute (with ``causal=False`` every
+    pair; with ``key_mask`` only unmasked keys)."""
     q, k, v, o, do = (_up(t, dtype) for t in (q, k, v, o, do))
     L = _up(L, dtype)
     slopes = _up(slopes, dtype)
@@ -200,7 +217,7 @@ def attention_bwd(q, k, v, o, L, do, slopes, scale, eps=EPS, dtype=torch.float64
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     for bs, hs in _chunks(B, H, chunk):
         qq, kk, vv, oo, dd = q[bs, hs], k[bs, hs], v[bs, hs], o[bs, hs], do[bs, hs]
-        s, keep = _scores(qq, kk, slopes[hs], scale)
+        s, keep = _scores(qq, kk, slopes[hs], scale, causal, _mask_rows(key_mask, bs))
         den = s.abs() + 1.0
         sig = 0.5 * (s / den + 1.0)
         s2 = sig * sig
@@ -218,30 +235,38 @@ def attention_bwd(q, k, v, o, L, do, slopes, scale, eps=EPS, dtype=torch.float64
     return dq, dk, dv
 
 
-def harness_attention(q, k, v, slopes, scale, eps=EPS):
+def harness_attention(q, k, v, slopes, scale, eps=EPS, causal=True, key_mask=None):
     """The reference test harness formulation (tests.py:44-65 and the model's
     CPU path algebraic_model.py:112-136): full score matrix, ALiBi, the -1e4
-    causal fill, rational softmax over all T columns, then P @ V. Pure torch
-    ops on whatever dtype/grad state the inputs carry (used with autograd)."""
+    causal fill, the -1e4 padding fill where key_mask == 0
+    (algebraic_model.py:129-131), rational softmax over all T columns, then
+    P @ V. ``causal=False`` drops the causal fill. Pure torch ops on whatever
+    dtype/grad state the inputs carry (used with autograd)."""
     B, H, T, D = q.shape
     scores = torch.matmul(q, k.transpose(-2, -1)) * scale
     pos = torch.arange(T)
     rel = pos[:, None] - pos[None, :]
     scores = scores + (-rel.abs().to(q.dtype) * slopes.to(q.dtype).view(1, H, 1, 1))
-    upper = torch.triu(torch.ones(T, T, dtype=torch.bool), diagonal=1)
-    scores = scores.masked_fill(upper[None, None], NEG_FILL)
+    if causal:
+        upper = torch.triu(torch.ones(T, T, dtype=torch.bool), diagonal=1)
+        scores = scores.masked_fill(upper[None, None], NEG_FILL)
+    if key_mask is not None:
+        pad = key_mask.to("cpu")[:, None, None, :] == 0
+        scores = scores.masked_fill(pad, NEG_FILL)
     sig = 0.5 * (scores / (scores.abs() + 1.0) + 1.0)
     f = sig.pow(4)
     probs = f / (f.sum(dim=-1, keepdim=True) + eps)
     return torch.matmul(probs, v)
 
 
-def loop_attention_fwd(q, k, v, slopes, scale, eps=EPS):
+def loop_attention_fwd(q, k, v, slopes, scale, eps=EPS, causal=True, key_mask=None):
     """Scalar pure-Python loop over (b, h, i, j <= i), as the reference kernel
-    walks it (forward.py:80-159). Only for tiny inputs."""
+    walks it (forward.py:80-159); ``causal=False`` walks every j, ``key_mask``
+    skips masked keys. Only for tiny inputs."""
     q, k, v = (_up(t, torch.float64).tolist() for t in (q, k, v))
     sl = _up(slopes, torch.float64).tolist()
     B, H, T, D = len(q), len(q[0]), len(q[0][0]), len(q[0][0][0])
+    km = None if key_mask is None else key_mask.to("cpu").tolist()
     o = [[[[0.0] * D for _ in range(T)] for _ in range(H)] for _ in range(B)]
     L = [[[0.0] * T for _ in range(H)] for _ in range(B)]
     for b in range(B):
@@ -249,7 +274,9 @@ def loop_attention_fwd(q, k, v, slopes, scale, eps=EPS):
             for i in range(T):
                 acc = [0.0] * D
                 l = 0.0
-                for j in range(i + 1):
+                for j in range(i + 1 if causal else T):
+                    if km is not None and km[b][j] == 0:
+                        continue
                     s = sum(q[b][h][i][d] * k[b][h][j][d] for d in range(D)) * scale
                     s = s - sl[h] * abs(i - j)
                     sig = 0.5 * (s / (abs(s) + 1.0) + 1.0)

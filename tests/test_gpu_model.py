@@ -59,3 +59,32 @@ def test_model_gradient_checkpointing_matches(gpu):
     assert torch.equal(l1, l2)
     for a, p in zip(g1, m.parameters()):
         assert torch.equal(a, p.grad)
+
+
+def test_model_padding_mask_gpu_matches_cpu_path(gpu):
+    # the GPU path now applies attention_mask as the reference CPU path does
+    # (algebraic_model.py:129-131); dropped keys contribute exactly 0 here and
+    # sigma(-1e4)^4 ~ 6e-18 there
+    torch.manual_seed(2)
+    m = F.AlgebraicTransformerLM(vocab_size=300, d_model=128, n_head=2, n_layers=2, dropout=0.0)
+    ids = torch.randint(0, 300, (2, 70))
+    mask = torch.ones(2, 70, dtype=torch.long)
+    mask[0, :10] = 0
+    mask[1, 50:] = 0
+    logits_c, loss_c = m(ids, labels=ids, attention_mask=mask)
+    loss_c.backward()
+    grads_c = {n: p.grad.clone() for n, p in m.named_parameters()}
+    m.zero_grad(set_to_none=True)
+    mg = m.cuda()
+    logits_g, loss_g = mg(ids.cuda(), labels=ids.cuda(), attention_mask=mask.cuda())
+    loss_g.backward()
+    assert abs(loss_g.item() - loss_c.item()) <= 1e-5 * abs(loss_c.item())
+    assert torch.allclose(logits_g.cpu(), logits_c, rtol=1e-4, atol=1e-4)
+    for n, p in mg.named_parameters():
+        gc = grads_c[n]
+        err = float((p.grad.cpu() - gc).abs().max())
+        assert err <= 1e-4 * max(1.0, float(gc.abs().max())), (n, err)
+    # and the mask matters: without it the logits differ
+    with torch.no_grad():
+        unmasked, _ = mg(ids.cuda())
+    assert not torch.allclose(unmasked.cpu(), logits_c, rtol=1e-3, atol=1e-3)

@@ -146,3 +146,16 @@ def test_add_mean_error_norm_cpu_is_add_then_norm():
     h, y = F.add_mean_error_norm(x, r, w)
     assert torch.equal(h, x + r)
     assert torch.equal(y, F.mean_error_norm(x + r, w))
+
+
+def test_masked_attention_cpu_tensors_use_reference_cpu_formulation():
+    # CPU tensors take the reference model's CPU attention (-1e4 fill)
+    B, H, T, D = 2, 2, 9, 8
+    g = torch.Generator().manual_seed(4)
+    q, k, v = (torch.randn(B, H, T, D, generator=g) for _ in range(3))
+    km = torch.tensor([[1] * 9, [0, 1, 1, 0, 1, 1, 1, 1, 0]])
+    slopes = F.compute_alibi_slopes(H)
+    for causal in (True, False):
+        got = F.rational_attention_masked(q, k, v, slopes, 0.3, key_mask=km, causal=causal)
+        ref = O.harness_attention(q, k, v, slopes, 0.3, causal=causal, key_mask=km)
+        assert torch.allclose(got, ref.to(got.dtype), rtol=1e-5, atol=1e-6)

@@ -242,3 +242,107 @@ def test_attention_bwd_matches_finite_differences():
             fd = float(((op - om) * do).sum() / (2 * h))
             an = float(grads[which][idx])
             assert abs(fd - an) < 1e-6 + 1e-5 * abs(fd), (which, idx, fd, an)
+
+
+# ------------------------------------------ padding mask / non-causal ----
+# Extensions beyond the reference kernels (which are always causal and take no
+# mask). The padding mask is pinned to the reference's own CPU attention
+# (algebraic_model.py:112-136, restated by harness_attention: -1e4 fill where
+# mask == 0); the non-causal mode to closed forms, a symmetry the causal mode
+# lacks, the causal path at the last query, a pure-Python loop and autograd.
+
+def _padding_mask(B, T, seed):
+    g = _g(seed)
+    m = (torch.rand(B, T, generator=g) > 0.3).to(torch.int64)
+    m[0, : T // 3] = 0          # left padding, incl. queries that see no key
+    if B > 1:
+        m[1, -(T // 4):] = 0    # right padding
+    return m
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("B,H,T,D", [(2, 3, 21, 8), (3, 2, 64, 16)])
+def test_masked_attention_fwd_matches_reference_cpu_path(B, H, T, D, causal):
+    q, k, v, _ = _attn_inputs(B, H, T, D, 60 + T)
+    slopes = O.alibi_slopes(H)
+    scale = 1 / math.sqrt(D)
+    km = _padding_mask(B, T, T)
+    o, L = O.attention_fwd(q, k, v, slopes, scale, causal=causal, key_mask=km)
+    ref = O.harness_attention(q, k, v, slopes.double(), scale, causal=causal, key_mask=km)
+    # the fill leaves ~6e-18 per dropped key; rows with no visible key are
+    # 0 here and (count * 6e-18 * v) / 1e-6 ~ 1e-10 there
+    assert torch.allclose(o, ref, rtol=1e-10, atol=1e-9)
+    o2, L2 = O.attention_fwd(q, k, v, slopes, scale, chunk=1, causal=causal, key_mask=km)
+    assert torch.equal(o, o2) and torch.equal(L, L2)
+    # an all-ones mask is no mask
+    o3, L3 = O.attention_fwd(q, k, v, slopes, scale, causal=causal,
+                             key_mask=torch.ones(B, T, dtype=torch.int64))
+    o4, L4 = O.attention_fwd(q, k, v, slopes, scale, causal=causal)
+    assert torch.equal(o3, o4) and torch.equal(L3, L4)
+
+
+def test_masked_attention_fwd_matches_python_loop():
+    q, k, v, _ = _attn_inputs(2, 2, 7, 3, 61)
+    slopes = torch.tensor([0.5, 0.125])
+    km = torch.tensor([[1, 0, 1, 1, 0, 1, 0], [0, 0, 0, 1, 1, 1, 1]])
+    for causal in (True, False):
+        o, L = O.attention_fwd(q, k, v, slopes, 0.7, causal=causal, key_mask=km)
+        ol, Ll = O.loop_attention_fwd(q, k, v, slopes, 0.7, causal=causal, key_mask=km)
+        assert torch.allclose(o, ol, rtol=1e-13, atol=1e-14)
+        assert torch.allclose(L, Ll, rtol=1e-13, atol=1e-14)
+    # batch 1, causal: queries 0..2 see only masked keys -> L = 0, o = 0
+    o, L = O.attention_fwd(q, k, v, slopes, 0.7, key_mask=km)
+    assert torch.equal(L[1, :, :3], torch.zeros(2, 3, dtype=f64))
+    assert torch.equal(o[1, :, :3], torch.zeros(2, 3, 3, dtype=f64))
+
+
+def test_noncausal_known_answers_and_symmetry():
+    eps = 1e-6
+    T = 11
+    _, k, v, _ = _attn_inputs(1, 1, T, 5, 62)
+    # q = 0, slopes = 0: every f = 0.5^4 over all T keys -> o_i = mean(v) T / (T + 16 eps)
+    o, L = O.attention_fwd(torch.zeros(1, 1, T, 5, dtype=f64), k, v, torch.zeros(1), 1.0, eps,
+                           causal=False)
+    mean = v.mean(-2, keepdim=True).expand_as(v)
+    assert torch.allclose(o, mean * (T / (T + 16 * eps)), rtol=1e-13, atol=1e-15)
+    assert torch.allclose(L, torch.full_like(L, T / 16), rtol=1e-15, atol=0)
+    # ALiBi on |i - j| is symmetric: reversing the sequence reverses the output
+    # (the causal mode, and a signed i - j, break this)
+    q, k, v, _ = _attn_inputs(2, 3, 13, 4, 63)
+    slopes = O.alibi_slopes(3)
+    o, L = O.attention_fwd(q, k, v, slopes, 0.5, causal=False)
+    fl = lambda t: t.flip(-2)
+    orr, Lr = O.attention_fwd(fl(q), fl(k), fl(v), slopes, 0.5, causal=False)
+    assert torch.allclose(fl(orr), o, rtol=1e-13, atol=1e-14)
+    assert torch.allclose(Lr.flip(-1), L, rtol=1e-13, atol=0)
+    # the last query sees every key in both modes
+    oc, Lc = O.attention_fwd(q, k, v, slopes, 0.5)
+    assert torch.allclose(oc[..., -1, :], o[..., -1, :], rtol=1e-14, atol=1e-15)
+    assert not torch.allclose(oc[..., 0, :], o[..., 0, :])
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_masked_attention_bwd_matches_autograd_of_harness(causal):
+    B, H, T, D = 2, 3, 19, 8
+    q, k, v, do = _attn_inputs(B, H, T, D, 64)
+    slopes = O.alibi_slopes(H)
+    scale = 1 / math.sqrt(D)
+    # every query keeps at least one visible key here, so that the -1e4
+    # fill's remainders stay negligible in the gradients as well
+    km = torch.ones(B, T, dtype=torch.int64)
+    km[0, 3:7] = 0
+    km[1, -5:] = 0
+    km[1, 1] = 0
+    o, L = O.attention_fwd(q, k, v, slopes, scale, 0.0, causal=causal, key_mask=km)
+    dq, dk, dv = O.attention_bwd(q, k, v, o, L, do, slopes, scale, 0.0, causal=causal,
+                                 key_mask=km)
+    qr, kr, vr = (t.clone().requires_grad_(True) for t in (q, k, v))
+    ref = O.harness_attention(qr, kr, vr, slopes.double(), scale, 0.0, causal=causal, key_mask=km)
+    gq, gk, gv = torch.autograd.grad(ref, (qr, kr, vr), do)
+    for ours, theirs in ((dq, gq), (dk, gk), (dv, gv)):
+        err = float((ours - theirs).abs().max())
+        assert err < 1e-10 * max(1.0, float(theirs.abs().max())), err
+    # dropped keys get exactly zero dK, dV
+    drop = (km == 0)[:, None, :, None].expand_as(dk)
+    assert torch.equal(dk[drop], torch.zeros_like(dk[drop]))
+    assert torch.equal(dv[drop], torch.zeros_like(dv[drop]))
