@@ -101,7 +101,7 @@ def bench_attention(torch, F, steps, warmup, B=4, H=16, T=4096, D=128):
                 flops_step=7 * unit, flops_fwd=2 * unit, flops_bwd=5 * unit)
 
 
-def bench_attention_variants(torch, F, steps=5, warmup=2, B=4, H=16, T=4096, D=128):
+def bench_attention_variants(torch, F, steps=10, warmup=3, B=4, H=16, T=4096, D=128):
     """fwd+bwd of the masked / non-causal attention extension at the benchmark
     shape (bf16). TFLOP/s count the (query, key) pairs each variant attends:
     7 matmuls x 2 D flops per pair, the same accounting as the headline metric

@@ -139,7 +139,8 @@ int kat_add_men_bwd(const void* dy, const void* dh, const void* h, const void* w
 /* ------------------------------------------------------------------------
  * rational attention, layout [B, H, T, D] with arbitrary (b, h, t) strides and
  * unit d-stride. Always causal, as the reference (the `causal` flag is
- * accepted and ignored, forward.py:273 / backward.py:282).
+ * accepted and ignored, forward.py:273 / backward.py:282); the _masked entry
+ * points further down add a padding mask and a non-causal mode.
  *   s_ij = scale * <q_i, k_j> - slope_h * (i - j)   (j <= i)
  *   f_ij = sigma(s_ij)^4,  L_i = sum_j f_ij  (fp32, stored without eps)
  *   o_i  = sum_j f_ij v_j / (L_i + eps)
