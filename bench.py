@@ -18,6 +18,9 @@ throughput 7*B*H*S^2*D / step time in TFLOP/s. The same JSON line carries:
   * attention_variants -- fwd+bwd of the padding-mask / non-causal attention
                  extension at the same shape (right-padded batch, non-causal,
                  both), TFLOP/s over the (query, key) pairs each attends;
+  * decode     -- kat_attn_decode over bf16 KV caches (us per call, HBM GB/s
+                 of the K and V bytes) and generate() tokens/s with the KV
+                 cache against the reference's re-run-the-prefix loop;
   * device     -- CU count, a measured bf16 MFMA loop rate (beside the 2.5 PF
                  spec peak) and a measured 1 GiB device-copy bandwidth;
   * model_step -- one training step (bf16 autocast forward + loss + backward,
@@ -26,7 +29,7 @@ throughput 7*B*H*S^2*D / step time in TFLOP/s. The same JSON line carries:
                  also the 1.3 B-parameter model at batch 2 x 8192.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-fused]
-                       [--no-variants] [--no-model] [--model-large]
+                       [--no-variants] [--no-decode] [--no-model] [--model-large]
        python bench.py --copy-calibration   (one plain 1 GiB device copy, for
                                              scaling HBM byte counters)
 """
@@ -146,6 +149,58 @@ def bench_attention_variants(torch, F, steps=10, warmup=3, B=4, H=16, T=4096, D=
         out[name] = dict(ms=round(ms, 4), pairs=pairs, TFLOPs=round(flops / ms / 1e9, 2),
                          valid_keys=lens if km is not None else [T] * B)
     return out
+
+
+def bench_decode(torch, F, reps=50):
+    """kat_attn_decode (one query per (b, h) against a bf16 KV cache) at a
+    few cache shapes: time per call and HBM GB/s of the K and V bytes it must
+    read (2 B H n D x 2 bytes; q and out are negligible); plus the model's
+    generate() with its KV cache against the reference's loop, which re-runs
+    the whole prefix for every token (algebraic_model.py:239-265)."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(3)
+    res = {}
+    for B, H, n, D in ((1, 16, 4096, 128), (16, 16, 4096, 128), (4, 16, 32768, 128)):
+        q = torch.randn(B, H, D, generator=g).to(torch.bfloat16).to(dev)
+        kc = torch.randn(B, n, H, D, generator=g).to(torch.bfloat16).to(dev)
+        vc = torch.randn(B, n, H, D, generator=g).to(torch.bfloat16).to(dev)
+        k4, v4 = kc.permute(0, 2, 1, 3), vc.permute(0, 2, 1, 3)
+        slopes = torch.tensor([2.0 ** (-(i + 1) / 2) for i in range(H)], device=dev)
+        for _ in range(5):
+            F.rational_attention_decode(q, k4, v4, slopes, 1 / math.sqrt(D))
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            F.rational_attention_decode(q, k4, v4, slopes, 1 / math.sqrt(D))
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) / reps * 1e3
+        nbytes = 2 * B * H * n * D * 2
+        res[f"B{B}_H{H}_n{n}_D{D}"] = dict(us=round(us, 2), bytes=nbytes,
+                                            GBs=round(nbytes / us / 1e3, 1),
+                                            frac_hbm_peak=round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4))
+        del q, kc, vc, k4, v4
+    # model generate: config-4 model, batch 8, 512-token prompt, 64 new tokens
+    from fastalgebraictransformer_amd import AlgebraicTransformerLM
+    torch.manual_seed(0)
+    m = AlgebraicTransformerLM(32000, 768, 12, 12, dropout=0.0).to(dev).eval()
+    prompt = torch.randint(0, 32000, (8, 512), device=dev)
+    gen = {}
+    for name, use_cache in (("kv_cache", True), ("reference_loop", False)):
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            m.generate(prompt, 4, top_k=1, use_cache=use_cache)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            m.generate(prompt, 64, top_k=1, use_cache=use_cache)
+            torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+        gen[name] = dict(s=round(dt, 3), new_tokens_per_s=round(8 * 64 / dt, 1))
+    gen["speedup"] = round(gen["reference_loop"]["s"] / gen["kv_cache"]["s"], 2)
+    res["generate"] = dict(model="AlgebraicTransformerLM(32000, 768, 12, 12)", batch=8,
+                           prompt=512, new_tokens=64, dtype="bf16 autocast", **gen)
+    del m
+    return res
 
 
 def device_info(torch, lib):
@@ -381,6 +436,8 @@ def main():
     ap.add_argument("--no-fused", action="store_true")
     ap.add_argument("--no-variants", action="store_true",
                     help="skip the masked / non-causal attention variants")
+    ap.add_argument("--no-decode", action="store_true",
+                    help="skip the KV-cache decode attention and generate() timings")
     ap.add_argument("--no-model", action="store_true", help="skip the model training step")
     ap.add_argument("--model-large", action="store_true",
                     help="also time the ~1.3B model step (batch 2 x 8192, ~55 GB; reported only)")
@@ -446,6 +503,8 @@ def main():
     }
     if not args.no_variants:
         line["attention_variants"] = bench_attention_variants(torch, F)
+    if not args.no_decode:
+        line["decode"] = bench_decode(torch, F)
     if not args.no_fused:
         fused = bench_fused(torch, F)
         line["fused_ops"] = {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv)

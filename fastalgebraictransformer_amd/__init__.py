@@ -28,7 +28,7 @@ from .fused_ops import (
     rational_swiglu,
     rational_swiglu_packed,
 )
-from .forward import compute_alibi_slopes, rational_attention_forward
+from .forward import compute_alibi_slopes, rational_attention_decode, rational_attention_forward
 from .backward import (
     MaskedRationalAttentionFunction,
     PackedRationalAttention,
@@ -76,7 +76,9 @@ __all__ = [
 # [..., 2F] gate|value buffer -- the model's layouts, same kernels; and
 # add_mean_error_norm / ResidualMeanErrorNorm, the residual add fused with the
 # norm that reads it; rational_attention_masked / MaskedRationalAttentionFunction,
-# attention with a key padding mask and a real non-causal mode.
+# attention with a key padding mask and a real non-causal mode;
+# rational_attention_decode, one query against a KV cache (the model's
+# generate() uses it).
 
 
 def install_as(name="kernels"):

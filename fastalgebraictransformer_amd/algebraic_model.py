@@ -18,9 +18,21 @@ import torch.nn.functional as F
 from torch.utils.checkpoint import checkpoint
 
 from .backward import attention_torch, rational_attention_packed
-from .forward import compute_alibi_slopes
+from .forward import compute_alibi_slopes, rational_attention_decode
 from .fused_ops import (EPS, add_mean_error_norm, mean_error_norm, rational_softmax,
                         rational_swiglu_packed)
+
+
+class KVCache:
+    """Keys and values of one block for cached decoding: [batch, max_len,
+    n_head, d_head] each (token-major, as the qkv projection lays them out),
+    allocated on first use in the dtype the projection produces (bf16 under
+    autocast)."""
+
+    def __init__(self, max_len: int):
+        self.max_len = max_len
+        self.k: Optional[torch.Tensor] = None
+        self.v: Optional[torch.Tensor] = None
 
 
 class RationalMR(nn.Module):
@@ -84,6 +96,34 @@ class AlgebraicAttention(nn.Module):
             y = self._cpu_attention(q, k, v, mask).transpose(1, 2).contiguous().view(B, T, C)
         return self.dropout(self.out(y))
 
+    def forward_cached(self, x: torch.Tensor, cache, pos0: int) -> torch.Tensor:
+        """Causal attention of the tokens ``x`` at positions pos0.. over the
+        cached keys before them, appending their keys and values to ``cache``
+        = (k, v), each [B, max_len, H, D] (token-major, as the qkv projection
+        lays them out). A prompt (pos0 == 0) runs the causal kernel on x; one
+        new token runs the decode kernel over the cache (CUDA tensors). ``cache``
+        is a KVCache."""
+        B, T, C = x.shape
+        qkv = self.qkv(x).view(B, T, 3, self.n_head, self.d_head)
+        if cache.k is None:
+            shape = (B, cache.max_len, self.n_head, self.d_head)
+            cache.k = torch.empty(shape, dtype=qkv.dtype, device=qkv.device)
+            cache.v = torch.empty(shape, dtype=qkv.dtype, device=qkv.device)
+        assert pos0 + T <= cache.max_len, "KV cache is full"
+        kc, vc = cache.k, cache.v
+        kc[:, pos0:pos0 + T] = qkv[:, :, 1]
+        vc[:, pos0:pos0 + T] = qkv[:, :, 2]
+        if pos0 == 0:
+            y = rational_attention_packed(qkv, self.alibi_slopes, self.scale, eps=EPS).view(B, T, C)
+        else:
+            assert T == 1, "after the prompt, tokens are decoded one at a time"
+            n = pos0 + 1
+            y, _ = rational_attention_decode(qkv[:, 0, 0], kc[:, :n].permute(0, 2, 1, 3),
+                                             vc[:, :n].permute(0, 2, 1, 3), self.alibi_slopes,
+                                             self.scale, eps=EPS)
+            y = y.reshape(B, 1, C)
+        return self.dropout(self.out(y))
+
     def _cpu_attention(self, q, k, v, mask):
         """Reference CPU path (algebraic_model.py:112-136): full score matrix,
         ALiBi, -1e4 causal and padding fill, rational softmax, P @ V."""
@@ -115,6 +155,17 @@ class AlgebraicBlock(nn.Module):
         else:
             h0, n1 = add_mean_error_norm(x, r, self.norm1.weight, self.norm1.eps)
         h, n2 = add_mean_error_norm(h0, self.attn(n1, mask), self.norm2.weight, self.norm2.eps)
+        return h, self.ffn(n2)
+
+    def forward_pending_cached(self, x: torch.Tensor, r: Optional[torch.Tensor], cache, pos0: int):
+        """forward_pending for tokens at positions pos0.. with the attention's
+        keys and values kept in ``cache`` (AlgebraicAttention.forward_cached)."""
+        if r is None:
+            h0, n1 = x, self.norm1(x)
+        else:
+            h0, n1 = add_mean_error_norm(x, r, self.norm1.weight, self.norm1.eps)
+        h, n2 = add_mean_error_norm(h0, self.attn.forward_cached(n1, cache, pos0),
+                                    self.norm2.weight, self.norm2.eps)
         return h, self.ffn(n2)
 
 
@@ -188,21 +239,63 @@ class AlgebraicTransformerLM(nn.Module):
             loss = F.cross_entropy(pred.view(-1, pred.size(-1)), tgt.view(-1), ignore_index=-100)
         return logits, loss
 
+    def forward_cached(self, input_ids: torch.Tensor, caches, pos0: int) -> torch.Tensor:
+        """Logits of the tokens ``input_ids`` at positions pos0.., attending to
+        the keys and values of earlier positions held in ``caches`` (one
+        KVCache per block, see new_kv_caches) and appending theirs. Equal to
+        the corresponding rows of forward() on the whole sequence up to float
+        rounding."""
+        x = self.embed(input_ids)
+        r = None
+        for block, cache in zip(self.blocks, caches):
+            x, r = block.forward_pending_cached(x, r, cache, pos0)
+        normed = self.norm(x) if r is None else add_mean_error_norm(x, r, self.norm.weight,
+                                                                     self.norm.eps)[1]
+        return self.head(normed)
+
+    def new_kv_caches(self, max_len: int) -> list:
+        """One KVCache per block, for up to ``max_len`` positions."""
+        return [KVCache(max_len) for _ in self.blocks]
+
+    @staticmethod
+    def _sample(logits: torch.Tensor, temperature: float, top_k: Optional[int]) -> torch.Tensor:
+        # algebraic_model.py:255-263
+        if temperature != 1.0:
+            logits = logits / temperature
+        if top_k is not None:
+            kth = torch.topk(logits, min(top_k, logits.size(-1)))[0][:, [-1]]
+            logits[logits < kth] = float("-inf")
+        return torch.multinomial(F.softmax(logits, dim=-1), num_samples=1)
+
     @torch.no_grad()
     def generate(self, idx: torch.Tensor, max_new_tokens: int, temperature: float = 1.0,
-                 top_k: Optional[int] = None) -> torch.Tensor:
-        """Sample ``max_new_tokens`` tokens, re-running the (cropped) prefix per
-        step (reference algebraic_model.py:239-265)."""
-        for _ in range(max_new_tokens):
-            ctx = idx if idx.size(1) <= self.block_size else idx[:, -self.block_size:]
-            logits, _ = self.forward(ctx)
-            logits = logits[:, -1, :]
-            if temperature != 1.0:
-                logits = logits / temperature
-            if top_k is not None:
-                kth = torch.topk(logits, min(top_k, logits.size(-1)))[0][:, [-1]]
-                logits[logits < kth] = float("-inf")
-            nxt = torch.multinomial(F.softmax(logits, dim=-1), num_samples=1)
+                 top_k: Optional[int] = None, use_cache: bool = True) -> torch.Tensor:
+        """Sample ``max_new_tokens`` tokens (reference algebraic_model.py:239-265).
+
+        The reference re-runs the (cropped) prefix for every token. On CUDA
+        tensors (``use_cache``) the prompt is run once into per-block key /
+        value caches and each new token then costs one decode step; the logits
+        are those of the full forward up to float rounding, and the sampling
+        (temperature, top_k, multinomial) is the reference's. Once the context
+        exceeds block_size the reference crops it, which changes every cached
+        state, so from there on each token re-runs the cropped window as the
+        reference does. ``use_cache=False`` (or CPU tensors) always does."""
+        T0 = idx.size(1)
+        cached = use_cache and idx.is_cuda and max_new_tokens > 0 and T0 <= self.block_size
+        caches = None
+        for s in range(max_new_tokens):
+            n = idx.size(1)
+            if cached and n <= self.block_size:
+                if caches is None:
+                    caches = self.new_kv_caches(min(T0 + max_new_tokens, self.block_size))
+                    logits = self.forward_cached(idx, caches, 0)[:, -1, :]
+                else:
+                    logits = self.forward_cached(idx[:, -1:], caches, n - 1)[:, -1, :]
+            else:
+                ctx = idx if n <= self.block_size else idx[:, -self.block_size:]
+                logits, _ = self.forward(ctx)
+                logits = logits[:, -1, :]
+            nxt = self._sample(logits, temperature, top_k)
             idx = torch.cat((idx, nxt), dim=1)
         return idx
 

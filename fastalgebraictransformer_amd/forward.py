@@ -90,3 +90,42 @@ def rational_attention_forward(q, k, v, alibi_slopes, scale, causal=True, eps=EP
     L = torch.empty((B, H, T), dtype=torch.float32, device=q.device)
     _attn_fwd_into(q, k, v, out, L, alibi_slopes, scale, causal, eps)
     return out, L
+
+
+def rational_attention_decode(q, k_cache, v_cache, alibi_slopes, scale, lengths=None, eps=EPS):
+    """One query per (batch, head) against a KV cache: the last row of the
+    causal attention over the cached keys, which the reference's generate()
+    recomputes over the whole prefix for every new token
+    (algebraic_model.py:239-265). An extension beyond the reference API.
+
+    q: [B, H, D]; k_cache, v_cache: [B, H, T, D] (any (b, h, t) strides with a
+    unit last-dim stride, e.g. permuted views of token-major [B, T, H, D]
+    caches). ``lengths`` (int32 [B] on the device, optional): keys cached per
+    batch row, default T; the query sits at position lengths[b] - 1.
+    Returns (out [B, H, D] in q's dtype, L [B, H] fp32 without eps). Runs
+    ``kat_attn_decode`` (split-KV, deterministic); CUDA tensors only."""
+    assert q.is_cuda and k_cache.is_cuda and v_cache.is_cuda
+    B, H, D = q.shape
+    T = k_cache.shape[2]
+    assert tuple(k_cache.shape) == (B, H, T, D) and tuple(v_cache.shape) == (B, H, T, D)
+    lib = _lib.load()
+    k_cache, v_cache = k_cache.to(q.dtype), v_cache.to(q.dtype)
+    q, k_cache, v_cache = _unit_d(q), _unit_d(k_cache), _unit_d(v_cache)
+    slopes = alibi_slopes.to(device=q.device, dtype=torch.float32).contiguous()
+    assert slopes.numel() == H, "alibi_slopes must have n_heads entries"
+    if lengths is not None:
+        lengths = lengths.to(device=q.device, dtype=torch.int32).contiguous()
+        assert lengths.numel() == B, "lengths must have B entries"
+    out = torch.empty((B, H, D), dtype=q.dtype, device=q.device)
+    L = torch.empty((B, H), dtype=torch.float32, device=q.device)
+    code = _lib.dtype_code(q)
+    ws_bytes = lib.kat_attn_decode_workspace_size(B, H, T, D, code)
+    ws = torch.empty(max(ws_bytes, 4), dtype=torch.uint8, device=q.device)
+    strides = _lib.i64_array((q.stride(0), q.stride(1)) + _bht_strides(k_cache) +
+                             _bht_strides(v_cache) + (out.stride(0), out.stride(1)))
+    _lib.check(lib.kat_attn_decode(q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+                                   out.data_ptr(), L.data_ptr(), slopes.data_ptr(),
+                                   None if lengths is None else lengths.data_ptr(), ws.data_ptr(),
+                                   ws_bytes, B, H, T, D, strides, float(scale), float(eps), code,
+                                   _lib.stream(q)), "kat_attn_decode")
+    return out, L

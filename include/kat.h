@@ -198,6 +198,27 @@ int kat_attn_bwd_masked(const void* q, const void* k, const void* v, const void*
                         float eps, int causal, int dtype, void* stream);
 
 /* ----------------------------------------------------------------------
+ * Decode: one query per (batch, head) against a KV cache -- the last row of
+ * the causal attention that the reference's generate() recomputes over the
+ * whole prefix for every new token (algebraic_model.py:239-265 ->
+ * forward.py:267-319). With n = lengths[b] (or T when lengths is NULL; values
+ * are clamped to [0, T]) cached keys and the query at position i = n - 1:
+ *   s_j = scale <q, k_j> - slope_h (i - j),  f_j = sigma(s_j)^4   (j < n)
+ *   L = sum_j f_j (fp32, without eps),  out = sum_j f_j v_j / (L + eps)
+ * q, out: [B, H, D] with (b, h) strides; k, v: [B, H, T, D] caches with
+ * (b, h, t) strides (any layout, e.g. token-major [B, T, H, D]); unit
+ * d-stride and 16-byte aligned rows. strides: 10 int64 = q (b, h), k (b, h, t),
+ * v (b, h, t), out (b, h). L: [B*H] fp32 or NULL. dtype KAT_F32 (D in
+ * {32, 64, 128}), KAT_BF16 / KAT_F16 (D in {64, 128, 256}). Keys are split
+ * into chunks across work-groups and the partial sums added in a fixed order
+ * (deterministic); the workspace holds the partials. */
+size_t kat_attn_decode_workspace_size(int64_t B, int64_t H, int64_t T, int64_t D, int dtype);
+int kat_attn_decode(const void* q, const void* k, const void* v, void* out, float* L,
+                    const float* slopes, const int32_t* lengths, void* workspace,
+                    size_t workspace_bytes, int64_t B, int64_t H, int64_t T, int64_t D,
+                    const int64_t* strides, float scale, float eps, int dtype, void* stream);
+
+/* ----------------------------------------------------------------------
  * Measurement helper (no counterpart in the reference; used by bench.py to
  * report a measured MFMA rate beside the spec peak). `blocks` x 256 threads
  * each run `iters` rounds of 16 independent v_mfma_f32_16x16x32_bf16 chains

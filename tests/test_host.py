@@ -159,3 +159,23 @@ def test_masked_attention_cpu_tensors_use_reference_cpu_formulation():
         got = F.rational_attention_masked(q, k, v, slopes, 0.3, key_mask=km, causal=causal)
         ref = O.harness_attention(q, k, v, slopes, 0.3, causal=causal, key_mask=km)
         assert torch.allclose(got, ref.to(got.dtype), rtol=1e-5, atol=1e-6)
+
+
+def test_generate_cpu_follows_reference_loop():
+    # CPU tensors take the reference loop (algebraic_model.py:239-265)
+    torch.manual_seed(0)
+    m = F.AlgebraicTransformerLM(vocab_size=30, d_model=16, n_head=2, n_layers=1, dropout=0.0,
+                                 block_size=8).eval()
+    prompt = torch.randint(0, 30, (2, 5))
+    torch.manual_seed(1)
+    out = m.generate(prompt, 6, temperature=0.7, top_k=5)
+    torch.manual_seed(1)
+    idx = prompt
+    with torch.no_grad():
+        for _ in range(6):
+            ctx = idx if idx.size(1) <= 8 else idx[:, -8:]
+            logits = m(ctx)[0][:, -1, :] / 0.7
+            v, _ = torch.topk(logits, 5)
+            logits[logits < v[:, [-1]]] = float("-inf")
+            idx = torch.cat((idx, torch.multinomial(torch.softmax(logits, -1), 1)), dim=1)
+    assert torch.equal(out, idx)
