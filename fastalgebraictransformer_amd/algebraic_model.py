@@ -124,6 +124,23 @@ class AlgebraicAttention(nn.Module):
             y = y.reshape(B, 1, C)
         return self.dropout(self.out(y))
 
+    def decode_step(self, x: torch.Tensor, cache: KVCache, pos: torch.Tensor,
+                    lengths: torch.Tensor) -> torch.Tensor:
+        """One new token per batch row (x: [B, 1, C]) at the position held on the
+        device in ``pos`` (int64 [1]), with ``lengths`` = pos + 1 (int32 [B]):
+        its key and value go into the cache at ``pos`` and the decode kernel
+        attends over the first ``lengths`` cached positions. No host-side
+        position enters the computation, so the step can be captured in a
+        HIP graph and replayed for every token."""
+        B, T, C = x.shape
+        qkv = self.qkv(x).view(B, 1, 3, self.n_head, self.d_head)
+        cache.k.index_copy_(1, pos, qkv[:, :, 1])
+        cache.v.index_copy_(1, pos, qkv[:, :, 2])
+        y, _ = rational_attention_decode(qkv[:, 0, 0], cache.k.permute(0, 2, 1, 3),
+                                         cache.v.permute(0, 2, 1, 3), self.alibi_slopes,
+                                         self.scale, lengths=lengths, eps=EPS)
+        return self.dropout(self.out(y.reshape(B, 1, C)))
+
     def _cpu_attention(self, q, k, v, mask):
         """Reference CPU path (algebraic_model.py:112-136): full score matrix,
         ALiBi, -1e4 causal and padding fill, rational softmax, P @ V."""
@@ -155,6 +172,17 @@ class AlgebraicBlock(nn.Module):
         else:
             h0, n1 = add_mean_error_norm(x, r, self.norm1.weight, self.norm1.eps)
         h, n2 = add_mean_error_norm(h0, self.attn(n1, mask), self.norm2.weight, self.norm2.eps)
+        return h, self.ffn(n2)
+
+    def decode_pending(self, x: torch.Tensor, r: Optional[torch.Tensor], cache, pos: torch.Tensor,
+                       lengths: torch.Tensor):
+        """forward_pending for one new token (AlgebraicAttention.decode_step)."""
+        if r is None:
+            h0, n1 = x, self.norm1(x)
+        else:
+            h0, n1 = add_mean_error_norm(x, r, self.norm1.weight, self.norm1.eps)
+        h, n2 = add_mean_error_norm(h0, self.attn.decode_step(n1, cache, pos, lengths),
+                                    self.norm2.weight, self.norm2.eps)
         return h, self.ffn(n2)
 
     def forward_pending_cached(self, x: torch.Tensor, r: Optional[torch.Tensor], cache, pos0: int):
@@ -253,6 +281,18 @@ class AlgebraicTransformerLM(nn.Module):
                                                                      self.norm.eps)[1]
         return self.head(normed)
 
+    def decode_step(self, tokens: torch.Tensor, caches, pos: torch.Tensor,
+                    lengths: torch.Tensor) -> torch.Tensor:
+        """Logits [B, vocab] of one new token per row (tokens: [B, 1]) at the
+        device-side position ``pos`` (int64 [1]; ``lengths`` = pos + 1, int32
+        [B]) over filled ``caches``. Capturable in a HIP graph."""
+        x = self.embed(tokens)
+        r = None
+        for block, cache in zip(self.blocks, caches):
+            x, r = block.decode_pending(x, r, cache, pos, lengths)
+        _, normed = add_mean_error_norm(x, r, self.norm.weight, self.norm.eps)
+        return self.head(normed)[:, -1, :]
+
     def new_kv_caches(self, max_len: int) -> list:
         """One KVCache per block, for up to ``max_len`` positions."""
         return [KVCache(max_len) for _ in self.blocks]
@@ -269,7 +309,8 @@ class AlgebraicTransformerLM(nn.Module):
 
     @torch.no_grad()
     def generate(self, idx: torch.Tensor, max_new_tokens: int, temperature: float = 1.0,
-                 top_k: Optional[int] = None, use_cache: bool = True) -> torch.Tensor:
+                 top_k: Optional[int] = None, use_cache: bool = True,
+                 use_graph: bool = True) -> torch.Tensor:
         """Sample ``max_new_tokens`` tokens (reference algebraic_model.py:239-265).
 
         The reference re-runs the (cropped) prefix for every token. On CUDA
@@ -279,10 +320,14 @@ class AlgebraicTransformerLM(nn.Module):
         (temperature, top_k, multinomial) is the reference's. Once the context
         exceeds block_size the reference crops it, which changes every cached
         state, so from there on each token re-runs the cropped window as the
-        reference does. ``use_cache=False`` (or CPU tensors) always does."""
+        reference does. ``use_cache=False`` (or CPU tensors) always does.
+        With ``use_graph`` the one-token decode step is captured once in a HIP
+        graph and replayed per token (under autocast it is captured with the
+        autocast weight cache off, as graph capture requires)."""
         T0 = idx.size(1)
         cached = use_cache and idx.is_cuda and max_new_tokens > 0 and T0 <= self.block_size
         caches = None
+        step = None
         for s in range(max_new_tokens):
             n = idx.size(1)
             if cached and n <= self.block_size:
@@ -290,7 +335,9 @@ class AlgebraicTransformerLM(nn.Module):
                     caches = self.new_kv_caches(min(T0 + max_new_tokens, self.block_size))
                     logits = self.forward_cached(idx, caches, 0)[:, -1, :]
                 else:
-                    logits = self.forward_cached(idx[:, -1:], caches, n - 1)[:, -1, :]
+                    if step is None:
+                        step = _DecodeStep(self, caches, idx.size(0), idx.device, use_graph)
+                    logits = step(idx[:, -1:], n - 1)
             else:
                 ctx = idx if n <= self.block_size else idx[:, -self.block_size:]
                 logits, _ = self.forward(ctx)
@@ -298,6 +345,51 @@ class AlgebraicTransformerLM(nn.Module):
             nxt = self._sample(logits, temperature, top_k)
             idx = torch.cat((idx, nxt), dim=1)
         return idx
+
+
+class _DecodeStep:
+    """The model's one-token decode step over fixed caches, run eagerly or as a
+    captured HIP graph: the token ids, position and lengths live in static
+    device buffers that are refilled before each replay."""
+
+    def __init__(self, model, caches, batch: int, device, use_graph: bool):
+        self.model, self.caches = model, caches
+        self.tok = torch.zeros(batch, 1, dtype=torch.long, device=device)
+        self.pos = torch.zeros(1, dtype=torch.long, device=device)
+        self.lengths = torch.ones(batch, dtype=torch.int32, device=device)
+        self.use_graph = use_graph
+        self.graph = None
+
+    def _run(self):
+        return self.model.decode_step(self.tok, self.caches, self.pos, self.lengths)
+
+    def _capture(self):
+        ac = torch.is_autocast_enabled()
+        ac_dtype = torch.get_autocast_dtype("cuda") if ac else torch.float32
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            # the warm-up runs the step on the buffers already filled for the
+            # first real step: it writes the cache row that step rewrites
+            with torch.autocast("cuda", dtype=ac_dtype, enabled=ac, cache_enabled=False):
+                self._run()
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            with torch.autocast("cuda", dtype=ac_dtype, enabled=ac, cache_enabled=False):
+                self.logits = self._run()
+        self.graph = graph
+
+    def __call__(self, tokens: torch.Tensor, pos: int) -> torch.Tensor:
+        self.tok.copy_(tokens)
+        self.pos.fill_(pos)
+        self.lengths.fill_(pos + 1)
+        if not self.use_graph:
+            return self._run()
+        if self.graph is None:
+            self._capture()
+        self.graph.replay()
+        return self.logits
 
 
 def create_small_model(vocab_size: int = 32000, **kwargs) -> AlgebraicTransformerLM:

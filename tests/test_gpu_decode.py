@@ -158,3 +158,43 @@ def test_cached_generate_bf16_autocast_runs(gpu):
         out = m.generate(prompt, 8, temperature=0.8, top_k=50)
     assert out.shape == (3, 17) and torch.equal(out[:, :9], prompt)
     assert int(out.min()) >= 0 and int(out.max()) < 500
+
+
+def test_decode_graph_replays_match_eager_steps(gpu):
+    # the captured one-token step against the same step run eagerly, position
+    # by position, with unrelated eager work and synchronisations between the
+    # replays (every replay checked)
+    from fastalgebraictransformer_amd.algebraic_model import _DecodeStep
+    m = _small_model(4)
+    ids = torch.randint(0, 500, (3, 30), device=dev)
+    with torch.no_grad():
+        caches = m.new_kv_caches(30)
+        m.forward_cached(ids[:, :20], caches, 0)
+        eager = _DecodeStep(m, caches, 3, ids.device, use_graph=False)
+        graph = _DecodeStep(m, caches, 3, ids.device, use_graph=True)
+        for pos in range(20, 30):
+            a = eager(ids[:, pos:pos + 1], pos).clone()
+            torch.cuda.synchronize()
+            junk = torch.randn(256, 256, device=dev) @ torch.randn(256, 256, device=dev)
+            b = graph(ids[:, pos:pos + 1], pos).clone()
+            torch.cuda.synchronize()
+            assert torch.equal(a, b), pos
+            del junk
+        full, _ = m(ids)
+    assert float((b - full[:, -1]).abs().max()) <= 1e-4 * max(1.0, float(full.abs().max()))
+
+
+@pytest.mark.parametrize("autocast", [False, True])
+def test_generate_graph_matches_eager_cache(gpu, autocast):
+    m = _small_model(5, block_size=48)
+    prompt = torch.randint(0, 500, (2, 13), device=dev)
+    outs = []
+    for use_graph in (True, False):
+        torch.manual_seed(9)
+        with torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast):
+            outs.append(m.generate(prompt, 24, top_k=1, use_graph=use_graph))
+    assert torch.equal(outs[0], outs[1])
+    if not autocast:
+        torch.manual_seed(9)
+        ref = m.generate(prompt, 24, top_k=1, use_cache=False)
+        assert torch.equal(outs[0], ref)
