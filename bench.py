@@ -310,16 +310,20 @@ def bench_fused(torch, F, reps=10):
     res = {}
 
     def timed(fn):
-        ts = []
+        # every rep: flush, then the step between two events; all reps are
+        # enqueued before one synchronisation, so the host runs ahead of the
+        # GPU and the events bracket the step's GPU work rather than Python's
+        # dispatch latency in front of its first kernel
+        evs = []
         for _ in range(reps + 2):
             flush.sum()
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record()
             fn()
             e1.record()
-            torch.cuda.synchronize()
-            ts.append(e0.elapsed_time(e1))
-        ts = sorted(ts[2:])
+            evs.append((e0, e1))
+        torch.cuda.synchronize()
+        ts = sorted(e0.elapsed_time(e1) for e0, e1 in evs[2:])
         return ts[len(ts) // 2]
 
     # mean_error_norm: x [16384, 4096] bf16, gamma fp32

@@ -718,34 +718,34 @@ __global__ __launch_bounds__(256) void men_bwd_mp_k(
   }
 }
 
-// dw[c] = sum_g partial[g][c] in a fixed order. A block owns 64 columns; its
-// 16 waves stride over g with 4 independent accumulators each (loads stay in
-// flight), then the 16 wave sums are added in wave order.
+// dw[c] = sum_g partial[g][c] in a fixed order. A block owns 16 columns and
+// 64 row groups (4 per wave, 16 waves): row group rg adds rows rg, rg + 64, ...
+// in two interleaved accumulators, then the 64 group sums are added in group
+// order. 16 columns per block give cols / 16 blocks (256 at 4096 columns), so
+// the reduction spreads over the whole chip.
 template <typename A>
 __global__ __launch_bounds__(1024) void colsum_k(const A* __restrict__ partial, int G, int n_cols,
                                                  A* __restrict__ out) {
-  __shared__ A red[16][64];
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int col = blockIdx.x * 64 + lane;
-  A s0 = A(0), s1 = A(0), s2 = A(0), s3 = A(0);
+  __shared__ A red[64][17];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c = lane & 15, rg = wave * 4 + (lane >> 4);
+  const int col = blockIdx.x * 16 + c;
+  A s0 = A(0), s1 = A(0);
   if (col < n_cols) {
-    int g = wave;
-    for (; g + 48 < G; g += 64) {
+    int g = rg;
+    for (; g + 64 < G; g += 128) {
       s0 += partial[(int64_t)g * n_cols + col];
-      s1 += partial[(int64_t)(g + 16) * n_cols + col];
-      s2 += partial[(int64_t)(g + 32) * n_cols + col];
-      s3 += partial[(int64_t)(g + 48) * n_cols + col];
+      s1 += partial[(int64_t)(g + 64) * n_cols + col];
     }
-    for (; g < G; g += 16) s0 += partial[(int64_t)g * n_cols + col];
+    for (; g < G; g += 64) s0 += partial[(int64_t)g * n_cols + col];
   }
-  red[wave][lane] = (s0 + s1) + (s2 + s3);
+  red[rg][c] = s0 + s1;
   __syncthreads();
-  if (wave == 0 && col < n_cols) {
+  if (threadIdx.x < 16 && blockIdx.x * 16 + (int)threadIdx.x < n_cols) {
     A t = A(0);
-#pragma unroll
-    for (int ww = 0; ww < 16; ++ww) t += red[ww][lane];
-    out[col] = t;
+#pragma unroll 8
+    for (int i = 0; i < 64; ++i) t += red[i][threadIdx.x];
+    out[blockIdx.x * 16 + threadIdx.x] = t;
   }
 }
 
@@ -953,7 +953,7 @@ static int men_bwd_t(const T* dy, const T* x, const W* w, const float* mu, T* dx
   }
   int rc = check_launch(nm);
   if (rc) return rc;
-  hipLaunchKernelGGL((colsum_k<A>), dim3((unsigned)((cols + 63) / 64)), dim3(1024), 0, st,
+  hipLaunchKernelGGL((colsum_k<A>), dim3((unsigned)((cols + 15) / 16)), dim3(1024), 0, st,
                      partial, G, (int)cols, dw);
   return check_launch(kAdd ? "kat_add_men_bwd (dw reduction)" : "kat_men_bwd (dw reduction)");
 }
