@@ -328,7 +328,7 @@ class AlgebraicTransformerLM(nn.Module):
         cached = use_cache and idx.is_cuda and max_new_tokens > 0 and T0 <= self.block_size
         caches = None
         step = None
-        for s in range(max_new_tokens):
+        for _ in range(max_new_tokens):
             n = idx.size(1)
             if cached and n <= self.block_size:
                 if caches is None:
