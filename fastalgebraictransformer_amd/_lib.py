@@ -39,9 +39,9 @@ _SIGNATURES = {
     "kat_men_bwd": ([_P, _P, _P, _P, _P, _P, _P, _SZ, _I64, _I64, _I64, _I64, _I64, _F, _INT,
                      _INT, _P], _INT),
     "kat_add_men_fwd": ([_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F, _INT,
-                         _INT, _INT, _P], _INT),
+                         _INT, _INT, _INT, _P], _INT),
     "kat_add_men_bwd": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _I64, _I64, _I64, _I64, _I64,
-                         _I64, _I64, _F, _INT, _INT, _INT, _P], _INT),
+                         _I64, _I64, _F, _INT, _INT, _INT, _INT, _P], _INT),
     "kat_attn_fwd": ([_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64P, _I64P, _F, _F, _INT,
                       _INT, _P], _INT),
     "kat_attn_bwd_workspace_size": ([_I64, _I64, _I64, _I64, _INT], _SZ),

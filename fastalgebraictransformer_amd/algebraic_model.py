@@ -23,6 +23,17 @@ from .fused_ops import (EPS, add_mean_error_norm, mean_error_norm, rational_soft
                         rational_swiglu_packed)
 
 
+def _narrow(x: torch.Tensor) -> Optional[torch.dtype]:
+    """The dtype a norm output feeding an autocast matmul is cast to before
+    the matmul reads it: the autocast dtype for an fp32 CUDA stream under
+    autocast, else None (keep x's dtype). The fused norm writes that dtype
+    directly, with the cast's own rounding, so the matmul's input is the
+    same bits and the separate cast pass (and its backward) disappears."""
+    if x.is_cuda and x.dtype == torch.float32 and torch.is_autocast_enabled("cuda"):
+        return torch.get_autocast_dtype("cuda")
+    return None
+
+
 class KVCache:
     """Keys and values of one block for cached decoding: [batch, max_len,
     n_head, d_head] each (token-major, as the qkv projection lays them out),
@@ -170,8 +181,9 @@ class AlgebraicBlock(nn.Module):
         if r is None:
             h0, n1 = x, self.norm1(x)
         else:
-            h0, n1 = add_mean_error_norm(x, r, self.norm1.weight, self.norm1.eps)
-        h, n2 = add_mean_error_norm(h0, self.attn(n1, mask), self.norm2.weight, self.norm2.eps)
+            h0, n1 = add_mean_error_norm(x, r, self.norm1.weight, self.norm1.eps, _narrow(x))
+        h, n2 = add_mean_error_norm(h0, self.attn(n1, mask), self.norm2.weight, self.norm2.eps,
+                                    _narrow(h0))
         return h, self.ffn(n2)
 
     def decode_pending(self, x: torch.Tensor, r: Optional[torch.Tensor], cache, pos: torch.Tensor,
@@ -180,9 +192,9 @@ class AlgebraicBlock(nn.Module):
         if r is None:
             h0, n1 = x, self.norm1(x)
         else:
-            h0, n1 = add_mean_error_norm(x, r, self.norm1.weight, self.norm1.eps)
+            h0, n1 = add_mean_error_norm(x, r, self.norm1.weight, self.norm1.eps, _narrow(x))
         h, n2 = add_mean_error_norm(h0, self.attn.decode_step(n1, cache, pos, lengths),
-                                    self.norm2.weight, self.norm2.eps)
+                                    self.norm2.weight, self.norm2.eps, _narrow(h0))
         return h, self.ffn(n2)
 
     def forward_pending_cached(self, x: torch.Tensor, r: Optional[torch.Tensor], cache, pos0: int):
@@ -191,9 +203,9 @@ class AlgebraicBlock(nn.Module):
         if r is None:
             h0, n1 = x, self.norm1(x)
         else:
-            h0, n1 = add_mean_error_norm(x, r, self.norm1.weight, self.norm1.eps)
+            h0, n1 = add_mean_error_norm(x, r, self.norm1.weight, self.norm1.eps, _narrow(x))
         h, n2 = add_mean_error_norm(h0, self.attn.forward_cached(n1, cache, pos0),
-                                    self.norm2.weight, self.norm2.eps)
+                                    self.norm2.weight, self.norm2.eps, _narrow(h0))
         return h, self.ffn(n2)
 
 
@@ -257,14 +269,20 @@ class AlgebraicTransformerLM(nn.Module):
         if r is None:
             normed = self.norm(x)
         else:
-            _, normed = add_mean_error_norm(x, r, self.norm.weight, self.norm.eps)
+            _, normed = add_mean_error_norm(x, r, self.norm.weight, self.norm.eps, _narrow(x))
         logits = self.head(normed)
         loss = None
         if labels is not None:
-            # next-token loss: position t predicts token t+1
-            pred = logits[..., :-1, :].contiguous()
-            tgt = labels[..., 1:].contiguous()
-            loss = F.cross_entropy(pred.view(-1, pred.size(-1)), tgt.view(-1), ignore_index=-100)
+            # next-token loss: position t predicts token t+1 (algebraic_model.py
+            # :229-236). The reference copies logits[..., :-1, :] into a new
+            # tensor (and autograd scatters its gradient back); here the full
+            # logits are used in place with the last position's target set to
+            # the ignored index: the same terms and the same mean (up to the
+            # summation order of the scalar loss), the same gradients.
+            tgt = labels.new_full(labels.shape, -100)
+            tgt[..., :-1] = labels[..., 1:]
+            loss = F.cross_entropy(logits.reshape(-1, logits.size(-1)), tgt.reshape(-1),
+                                   ignore_index=-100)
         return logits, loss
 
     def forward_cached(self, input_ids: torch.Tensor, caches, pos0: int) -> torch.Tensor:
@@ -277,8 +295,8 @@ class AlgebraicTransformerLM(nn.Module):
         r = None
         for block, cache in zip(self.blocks, caches):
             x, r = block.forward_pending_cached(x, r, cache, pos0)
-        normed = self.norm(x) if r is None else add_mean_error_norm(x, r, self.norm.weight,
-                                                                     self.norm.eps)[1]
+        normed = self.norm(x) if r is None else add_mean_error_norm(
+            x, r, self.norm.weight, self.norm.eps, _narrow(x))[1]
         return self.head(normed)
 
     def decode_step(self, tokens: torch.Tensor, caches, pos: torch.Tensor,
@@ -290,7 +308,7 @@ class AlgebraicTransformerLM(nn.Module):
         r = None
         for block, cache in zip(self.blocks, caches):
             x, r = block.decode_pending(x, r, cache, pos, lengths)
-        _, normed = add_mean_error_norm(x, r, self.norm.weight, self.norm.eps)
+        _, normed = add_mean_error_norm(x, r, self.norm.weight, self.norm.eps, _narrow(x))
         return self.head(normed)[:, -1, :]
 
     def new_kv_caches(self, max_len: int) -> list:

@@ -62,6 +62,37 @@ template <typename A> __device__ __forceinline__ A sign_of(A x) {
   return x > A(0) ? A(1) : (x < A(0) ? A(-1) : A(0));
 }
 
+// The norm backward's per-element terms with every fused multiply-add written
+// out, so the rounding does not depend on which products the compiler
+// contracts in a given template instance: the plain, residual-fused and
+// narrow-dy kernels, single- and multi-pass, all round identically.
+//   dx = dy * (w * inv) - sign(x) * corr * inv     (fused_ops.py:418-421)
+template <typename A>
+__device__ __forceinline__ A men_dx(A yy, A xx, A wv, A inv, A corr) {
+  return __builtin_fma(yy, wv * inv, -(sign_of(xx) * corr * inv));
+}
+template <>
+__device__ __forceinline__ float men_dx<float>(float yy, float xx, float wv, float inv, float corr) {
+  return __builtin_fmaf(yy, wv * inv, -(sign_of(xx) * corr * inv));
+}
+// v narrowed to Y (bf16 / fp16 from fp32) by a plain conversion of the
+// rounded fp32 register value. Without the empty asm the compiler may fold the
+// narrowing into the multiply that produced v (a mixed-precision FMA rounding
+// the exact product once to fp16), which differs from the fp32 result followed
+// by torch's cast in the last bit now and then; the narrow-output kernels must
+// equal that cast.
+template <typename Y, typename A> __device__ __forceinline__ Y narrow_to(A v) {
+  if constexpr (sizeof(Y) < sizeof(A)) asm("" : "+v"(v));
+  return from_acc<Y>(v);
+}
+//   acc + dy * p     (row sum of dy * y_hat; column sum of dy * x_hat)
+template <typename A> __device__ __forceinline__ A men_fma(A yy, A p, A acc) {
+  return __builtin_fma(yy, p, acc);
+}
+template <> __device__ __forceinline__ float men_fma<float>(float yy, float p, float acc) {
+  return __builtin_fmaf(yy, p, acc);
+}
+
 // Block-wide sum for the multi-pass kernels (256 threads).
 template <typename A> __device__ A block_sum(A v, A* sh) {
   v = wave_sum(v);
@@ -466,9 +497,9 @@ __device__ __forceinline__ void load_row_any(const R* __restrict__ base, int n_c
 // norm1, algebraic_model.py:150-151): h = x + r is rounded to T exactly as
 // torch's promoted add rounds it, written once, and normalised from registers,
 // so (h, y, mu) are bit-identical to the add followed by the plain norm.
-template <typename T, typename W, int NCH, typename R = void>
+template <typename T, typename W, int NCH, typename R = void, typename Y = T>
 __global__ __launch_bounds__(256) void men_fwd_k(const T* __restrict__ x, const W* __restrict__ w,
-                                                 T* __restrict__ y, float* __restrict__ mu,
+                                                 Y* __restrict__ y, float* __restrict__ mu,
                                                  int64_t n_rows, int n_cols, int64_t ldx,
                                                  int64_t ldy, float eps, const void* __restrict__ rp,
                                                  T* __restrict__ h, int64_t ldr, int64_t ldh) {
@@ -519,10 +550,10 @@ __global__ __launch_bounds__(256) void men_fwd_k(const T* __restrict__ x, const 
     for (int k = 0; k < NCH; ++k) {
       const int col = ((int)threadIdx.x + 256 * k) * V;
       if (col < n_cols) {
-        VecT<T, V> o;
+        VecT<Y, V> o;
 #pragma unroll
-        for (int i = 0; i < V; ++i) o.v[i] = from_acc<T>(to_acc(cur[k].v[i]) * inv * wv[k][i]);  // :340
-        st_vec<T, V>(y + row * ldy + col, o);
+        for (int i = 0; i < V; ++i) o.v[i] = narrow_to<Y>(to_acc(cur[k].v[i]) * inv * wv[k][i]);  // :340
+        st_vec_any<Y, V>(y + row * ldy + col, o);
       }
     }
 #pragma unroll
@@ -547,9 +578,9 @@ constexpr int kNormPf = 2;
 // through the residual stream, and dx = round_T(norm_bwd) + dh (the sum
 // autograd forms for h, in T), written for x and, cast to R, for r (dr may
 // be null).
-template <typename T, typename W, int NCH, typename R = void>
+template <typename T, typename W, int NCH, typename R = void, typename Y = T>
 __global__ __launch_bounds__(256) void men_bwd_k(
-    const T* __restrict__ dy, const T* __restrict__ x, const W* __restrict__ w,
+    const Y* __restrict__ dy, const T* __restrict__ x, const W* __restrict__ w,
     const float* __restrict__ mu, T* __restrict__ dx, typename AccT<T>::type* __restrict__ partial,
     int64_t n_rows, int n_cols, int64_t lddy, int64_t ldx, int64_t lddx, float eps,
     const T* __restrict__ dh, int64_t lddh, void* __restrict__ drp, int64_t lddr) {
@@ -570,7 +601,8 @@ __global__ __launch_bounds__(256) void men_bwd_k(
   const int64_t G = gridDim.x;
   int64_t row = blockIdx.x;
   // ring of rows row, row + G, ..., row + PF*G: slot 0 is reduced next
-  VecT<T, V> by[PF + 1][NCH], bx[PF + 1][NCH], bh[PF + 1][NCH];
+  VecT<Y, V> by[PF + 1][NCH];
+  VecT<T, V> bx[PF + 1][NCH], bh[PF + 1][NCH];
   float bm[PF + 1];
   // Rows past the end are clamped to the last row (loaded, never used):
   // a conditional load would make the compiler wait for it on the spot.
@@ -578,7 +610,7 @@ __global__ __launch_bounds__(256) void men_bwd_k(
 #pragma unroll
   for (int j = 0; j < PF; ++j) {
     const int64_t r = std::min(row + j * G, last);
-    load_row<T, NCH>(dy + r * lddy, n_cols, by[j]);
+    load_row_any<Y, V, NCH>(dy + r * lddy, n_cols, by[j]);
     load_row<T, NCH>(x + r * ldx, n_cols, bx[j]);
     if constexpr (kAdd) load_row<T, NCH>(dh + r * lddh, n_cols, bh[j]);
     bm[j] = mu[r];  // the row statistic travels with its row
@@ -586,7 +618,7 @@ __global__ __launch_bounds__(256) void men_bwd_k(
   for (int par = 0; row < n_rows; row += G, par ^= 1) {
     {
       const int64_t r = std::min(row + PF * G, last);
-      load_row<T, NCH>(dy + r * lddy, n_cols, by[PF]);
+      load_row_any<Y, V, NCH>(dy + r * lddy, n_cols, by[PF]);
       load_row<T, NCH>(x + r * ldx, n_cols, bx[PF]);
       if constexpr (kAdd) load_row<T, NCH>(dh + r * lddh, n_cols, bh[PF]);
       bm[PF] = mu[r];
@@ -597,8 +629,10 @@ __global__ __launch_bounds__(256) void men_bwd_k(
     for (int k = 0; k < NCH; ++k) {
       const bool in = chunk_in(k, V, n_cols);
 #pragma unroll
-      for (int i = 0; i < V; ++i)
-        cs += in ? to_acc(by[0][k].v[i]) * (to_acc(bx[0][k].v[i]) * inv * wv[k][i]) : A(0);  // :404-405
+      for (int i = 0; i < V; ++i) {
+        const A p = to_acc(bx[0][k].v[i]) * inv * wv[k][i];
+        cs = in ? men_fma(to_acc(by[0][k].v[i]), p, cs) : cs;  // fused_ops.py:404-405
+      }
     }
     cs = block_sum_par(cs, red, par);
     const A corr = cs / A(n_cols);  // fused_ops.py:408
@@ -611,16 +645,16 @@ __global__ __launch_bounds__(256) void men_bwd_k(
       for (int i = 0; i < V; ++i) {
         const A yy = to_acc(by[0][k].v[i]);
         const A xx = to_acc(bx[0][k].v[i]);
-        o.v[i] = from_acc<T>(yy * wv[k][i] * inv - sign_of(xx) * corr * inv);  // :418-421
+        o.v[i] = narrow_to<T>(men_dx(yy, xx, wv[k][i], inv, corr));  // fused_ops.py:418-421
         if constexpr (kAdd) o.v[i] = from_acc<T>(to_acc(o.v[i]) + to_acc(bh[0][k].v[i]));
-        dg[k][i] += in ? yy * (xx * inv) : A(0);  // fused_ops.py:595-597
+        dg[k][i] = in ? men_fma(yy, xx * inv, dg[k][i]) : dg[k][i];  // fused_ops.py:595-597
       }
       if (in) st_vec<T, V>(dx + row * lddx + col, o);
       if constexpr (kAdd) {
         if (in && dr != nullptr) {
           VecT<RT, V> od;
 #pragma unroll
-          for (int i = 0; i < V; ++i) od.v[i] = from_acc<RT>(to_acc(o.v[i]));
+          for (int i = 0; i < V; ++i) od.v[i] = narrow_to<RT>(to_acc(o.v[i]));
           st_vec_any<RT, V>(dr + row * lddr + col, od);
         }
       }
@@ -647,9 +681,9 @@ __global__ __launch_bounds__(256) void men_bwd_k(
 
 // h = x + r (R non-void) is formed in the first pass, written, and formed
 // again from x and r in the second (the same rounding, so the same value).
-template <typename T, typename R = void>
+template <typename T, typename R = void, typename Y = T>
 __global__ __launch_bounds__(256) void men_fwd_mp_k(const T* __restrict__ x, const void* __restrict__ wp,
-                                                    int w_is_f32, T* __restrict__ y,
+                                                    int w_is_f32, Y* __restrict__ y,
                                                     float* __restrict__ mu, int64_t n_rows,
                                                     int n_cols, int64_t ldx, int64_t ldy,
                                                     float eps, const void* __restrict__ rp,
@@ -676,13 +710,13 @@ __global__ __launch_bounds__(256) void men_fwd_mp_k(const T* __restrict__ x, con
   if (threadIdx.x == 0) mu[row] = (float)mean;
   for (int c = threadIdx.x; c < n_cols; c += blockDim.x) {
     const A wv = w_is_f32 ? (A)((const float*)wp)[c] : to_acc(((const T*)wp)[c]);
-    y[row * ldy + c] = from_acc<T>(to_acc(xin(c)) * inv * wv);
+    y[row * ldy + c] = narrow_to<Y>(to_acc(xin(c)) * inv * wv);
   }
 }
 
-template <typename T, typename R = void>
+template <typename T, typename R = void, typename Y = T>
 __global__ __launch_bounds__(256) void men_bwd_mp_k(
-    const T* __restrict__ dy, const T* __restrict__ x, const void* __restrict__ wp, int w_is_f32,
+    const Y* __restrict__ dy, const T* __restrict__ x, const void* __restrict__ wp, int w_is_f32,
     const float* __restrict__ mu, T* __restrict__ dx, typename AccT<T>::type* __restrict__ partial,
     int64_t n_rows, int n_cols, int64_t lddy, int64_t ldx, int64_t lddx, float eps,
     const T* __restrict__ dh, int64_t lddh, void* __restrict__ drp, int64_t lddr) {
@@ -699,7 +733,7 @@ __global__ __launch_bounds__(256) void men_bwd_mp_k(
     A cs = A(0);
     for (int c = threadIdx.x; c < n_cols; c += blockDim.x) {
       const A wv = w_is_f32 ? (A)((const float*)wp)[c] : to_acc(((const T*)wp)[c]);
-      cs += to_acc(dy[row * lddy + c]) * (to_acc(x[row * ldx + c]) * inv * wv);
+      cs = men_fma(to_acc(dy[row * lddy + c]), to_acc(x[row * ldx + c]) * inv * wv, cs);
     }
     cs = block_sum(cs, sh);
     const A corr = cs / A(n_cols);
@@ -707,13 +741,13 @@ __global__ __launch_bounds__(256) void men_bwd_mp_k(
       const A wv = w_is_f32 ? (A)((const float*)wp)[c] : to_acc(((const T*)wp)[c]);
       const A yy = to_acc(dy[row * lddy + c]);
       const A xx = to_acc(x[row * ldx + c]);
-      T g = from_acc<T>(yy * wv * inv - sign_of(xx) * corr * inv);
+      T g = narrow_to<T>(men_dx(yy, xx, wv, inv, corr));
       if constexpr (kAdd) {
         g = from_acc<T>(to_acc(g) + to_acc(dh[row * lddh + c]));
-        if (dr != nullptr) dr[row * lddr + c] = from_acc<RT>(to_acc(g));
+        if (dr != nullptr) dr[row * lddr + c] = narrow_to<RT>(to_acc(g));
       }
       dx[row * lddx + c] = g;
-      part[c] += yy * (xx * inv);  // same thread owns column c throughout
+      part[c] = men_fma(yy, xx * inv, part[c]);  // same thread owns column c throughout
     }
   }
 }
@@ -889,25 +923,25 @@ static int rsoftmax_bwd_t(const T* dy, const T* x, const T* p, T* dx, int64_t ro
   return check_launch("kat_rsoftmax_bwd");
 }
 
-template <typename T, typename W, typename R = void>
-static int men_fwd_t(const T* x, const W* w, T* y, float* mu, int64_t rows, int64_t cols,
+template <typename T, typename W, typename R = void, typename Y = T>
+static int men_fwd_t(const T* x, const W* w, Y* y, float* mu, int64_t rows, int64_t cols,
                      int64_t ldx, int64_t ldy, float eps, hipStream_t st, const R* r = nullptr,
                      T* h = nullptr, int64_t ldr = 0, int64_t ldh = 0) {
   constexpr int V = Raw<T>::V;
   constexpr bool kAdd = !std::is_void<R>::value;
-  bool vec = cols % V == 0 && ldx % V == 0 && ldy % V == 0 && aligned16(x) && aligned16(y) &&
-             aligned16(w);
+  bool vec = cols % V == 0 && ldx % V == 0 && ldy % V == 0 && aligned16(x) &&
+             reinterpret_cast<uintptr_t>(y) % (V * sizeof(Y)) == 0 && aligned16(w);
   if constexpr (kAdd)
     vec = vec && ldr % V == 0 && ldh % V == 0 && aligned16(h) &&
           reinterpret_cast<uintptr_t>(r) % (V * sizeof(R)) == 0;
   const int nch = vec ? pick_nch(cols, 256 * V) : 0;
   if (nch) {
     const int64_t blocks = row_grid(rows, kRowBlocksPerCU);
-    KAT_NCH_SWITCH(nch, hipLaunchKernelGGL((men_fwd_k<T, W, N, R>), dim3((unsigned)blocks),
+    KAT_NCH_SWITCH(nch, hipLaunchKernelGGL((men_fwd_k<T, W, N, R, Y>), dim3((unsigned)blocks),
                                            dim3(256), 0, st, x, w, y, mu, rows, (int)cols, ldx,
                                            ldy, eps, (const void*)r, h, ldr, ldh));
   } else {
-    hipLaunchKernelGGL((men_fwd_mp_k<T, R>), dim3((unsigned)rows), dim3(256), 0, st, x,
+    hipLaunchKernelGGL((men_fwd_mp_k<T, R, Y>), dim3((unsigned)rows), dim3(256), 0, st, x,
                        (const void*)w, (int)std::is_same<W, float>::value, y, mu, rows, (int)cols,
                        ldx, ldy, eps, (const void*)r, h, ldr, ldh);
   }
@@ -921,8 +955,8 @@ static int men_bwd_grid(int64_t rows, bool resident) {
   return (int)row_grid(rows, 2);
 }
 
-template <typename T, typename W, typename R = void>
-static int men_bwd_t(const T* dy, const T* x, const W* w, const float* mu, T* dx,
+template <typename T, typename W, typename R = void, typename Y = T>
+static int men_bwd_t(const Y* dy, const T* x, const W* w, const float* mu, T* dx,
                      typename AccT<T>::type* dw, void* ws, size_t ws_bytes, int64_t rows,
                      int64_t cols, int64_t lddy, int64_t ldx, int64_t lddx, float eps,
                      hipStream_t st, const T* dh = nullptr, int64_t lddh = 0, R* dr = nullptr,
@@ -932,7 +966,8 @@ static int men_bwd_t(const T* dy, const T* x, const W* w, const float* mu, T* dx
   constexpr bool kAdd = !std::is_void<R>::value;
   const char* nm = kAdd ? "kat_add_men_bwd" : "kat_men_bwd";
   bool vec = cols % V == 0 && lddy % V == 0 && ldx % V == 0 && lddx % V == 0 &&
-             aligned16(dy) && aligned16(x) && aligned16(dx) && aligned16(w);
+             reinterpret_cast<uintptr_t>(dy) % (V * sizeof(Y)) == 0 && aligned16(x) &&
+             aligned16(dx) && aligned16(w);
   if constexpr (kAdd)
     vec = vec && lddh % V == 0 && aligned16(dh) &&
           (dr == nullptr || (lddr % V == 0 && reinterpret_cast<uintptr_t>(dr) % (V * sizeof(R)) == 0));
@@ -943,11 +978,11 @@ static int men_bwd_t(const T* dy, const T* x, const W* w, const float* mu, T* dx
     return fail(KAT_EINVAL, "%s: workspace %zu bytes < required %zu", nm, ws_bytes, need);
   A* partial = reinterpret_cast<A*>(ws);
   if (nch) {
-    KAT_NCH_SWITCH(nch, hipLaunchKernelGGL((men_bwd_k<T, W, N, R>), dim3(G), dim3(256), 0, st, dy,
+    KAT_NCH_SWITCH(nch, hipLaunchKernelGGL((men_bwd_k<T, W, N, R, Y>), dim3(G), dim3(256), 0, st, dy,
                                            x, w, mu, dx, partial, rows, (int)cols, lddy, ldx, lddx,
                                            eps, dh, lddh, (void*)dr, lddr));
   } else {
-    hipLaunchKernelGGL((men_bwd_mp_k<T, R>), dim3(G), dim3(256), 0, st, dy, x, (const void*)w,
+    hipLaunchKernelGGL((men_bwd_mp_k<T, R, Y>), dim3(G), dim3(256), 0, st, dy, x, (const void*)w,
                        (int)std::is_same<W, float>::value, mu, dx, partial, rows, (int)cols, lddy,
                        ldx, lddx, eps, dh, lddh, (void*)dr, lddr);
   }
@@ -1111,54 +1146,49 @@ extern "C" int kat_men_bwd(const void* dy, const void* x, const void* w, const f
 
 // Residual add fused with the norm. The residual branch r (and its gradient
 // dr) has the stream's dtype, or bf16 / fp16 beside an fp32 stream (the
-// branch output of an autocast matmul added to the fp32 residual).
-template <typename T, typename W>
-static int add_men_fwd_d(const char* nm, int dtype, int dtype_r, const void* x, const void* r,
-                         const void* w, void* h, void* y, float* mu, int64_t rows, int64_t cols,
-                         int64_t ldx, int64_t ldr, int64_t ldh, int64_t ldy, float eps,
-                         hipStream_t st) {
-  if (dtype_r == dtype)
-    return men_fwd_t<T, W, T>((const T*)x, (const W*)w, (T*)y, mu, rows, cols, ldx, ldy, eps, st,
-                              (const T*)r, (T*)h, ldr, ldh);
-  if constexpr (std::is_same<T, float>::value) {
-    if (dtype_r == KAT_BF16)
-      return men_fwd_t<T, W, bf16>((const T*)x, (const W*)w, (T*)y, mu, rows, cols, ldx, ldy, eps,
-                                   st, (const bf16*)r, (T*)h, ldr, ldh);
-    if (dtype_r == KAT_F16)
-      return men_fwd_t<T, W, f16>((const T*)x, (const W*)w, (T*)y, mu, rows, cols, ldx, ldy, eps,
-                                  st, (const f16*)r, (T*)h, ldr, ldh);
+// branch output of an autocast matmul added to the fp32 residual); so has the
+// normalised output y (and its gradient dy): an autocast matmul reads it in
+// its own dtype, so y is rounded once, as the cast would.
+#define KAT_NARROW_SWITCH(code, U, dtype, ...)                                          \
+  if ((code) == (dtype)) { typedef T U; __VA_ARGS__; }                                 \
+  if constexpr (std::is_same<T, float>::value) {                                        \
+    if ((code) == KAT_BF16) { typedef bf16 U; __VA_ARGS__; }                            \
+    if ((code) == KAT_F16) { typedef f16 U; __VA_ARGS__; }                              \
   }
-  return fail(KAT_EUNSUPPORTED, "%s: residual dtype %d with stream dtype %d", nm, dtype_r, dtype);
+
+template <typename T, typename W>
+static int add_men_fwd_d(const char* nm, int dtype, int dtype_r, int dtype_y, const void* x,
+                         const void* r, const void* w, void* h, void* y, float* mu, int64_t rows,
+                         int64_t cols, int64_t ldx, int64_t ldr, int64_t ldh, int64_t ldy,
+                         float eps, hipStream_t st) {
+  KAT_NARROW_SWITCH(dtype_r, R, dtype,
+    KAT_NARROW_SWITCH(dtype_y, Y, dtype,
+      return (men_fwd_t<T, W, R, Y>((const T*)x, (const W*)w, (Y*)y, mu, rows, cols, ldx, ldy, eps,
+                                    st, (const R*)r, (T*)h, ldr, ldh))))
+  return fail(KAT_EUNSUPPORTED, "%s: residual dtype %d / output dtype %d with stream dtype %d", nm,
+              dtype_r, dtype_y, dtype);
 }
 
 template <typename T, typename W>
-static int add_men_bwd_d(const char* nm, int dtype, int dtype_r, const void* dy, const void* dh,
-                         const void* h, const void* w, const float* mu, void* dx, void* dr,
-                         void* dw, void* ws, size_t ws_bytes, int64_t rows, int64_t cols,
+static int add_men_bwd_d(const char* nm, int dtype, int dtype_r, int dtype_y, const void* dy,
+                         const void* dh, const void* h, const void* w, const float* mu, void* dx,
+                         void* dr, void* dw, void* ws, size_t ws_bytes, int64_t rows, int64_t cols,
                          int64_t lddy, int64_t lddh, int64_t ldh, int64_t lddx, int64_t lddr,
                          float eps, hipStream_t st) {
   typedef typename AccT<T>::type A;
-  if (dtype_r == dtype)
-    return men_bwd_t<T, W, T>((const T*)dy, (const T*)h, (const W*)w, mu, (T*)dx, (A*)dw, ws,
-                              ws_bytes, rows, cols, lddy, ldh, lddx, eps, st, (const T*)dh, lddh,
-                              (T*)dr, lddr);
-  if constexpr (std::is_same<T, float>::value) {
-    if (dtype_r == KAT_BF16)
-      return men_bwd_t<T, W, bf16>((const T*)dy, (const T*)h, (const W*)w, mu, (T*)dx, (A*)dw, ws,
-                                   ws_bytes, rows, cols, lddy, ldh, lddx, eps, st, (const T*)dh,
-                                   lddh, (bf16*)dr, lddr);
-    if (dtype_r == KAT_F16)
-      return men_bwd_t<T, W, f16>((const T*)dy, (const T*)h, (const W*)w, mu, (T*)dx, (A*)dw, ws,
-                                  ws_bytes, rows, cols, lddy, ldh, lddx, eps, st, (const T*)dh,
-                                  lddh, (f16*)dr, lddr);
-  }
-  return fail(KAT_EUNSUPPORTED, "%s: residual dtype %d with stream dtype %d", nm, dtype_r, dtype);
+  KAT_NARROW_SWITCH(dtype_r, R, dtype,
+    KAT_NARROW_SWITCH(dtype_y, Y, dtype,
+      return (men_bwd_t<T, W, R, Y>((const Y*)dy, (const T*)h, (const W*)w, mu, (T*)dx, (A*)dw, ws,
+                                    ws_bytes, rows, cols, lddy, ldh, lddx, eps, st, (const T*)dh,
+                                    lddh, (R*)dr, lddr))))
+  return fail(KAT_EUNSUPPORTED, "%s: residual dtype %d / output dtype %d with stream dtype %d", nm,
+              dtype_r, dtype_y, dtype);
 }
 
 extern "C" int kat_add_men_fwd(const void* x, const void* r, const void* w, void* h, void* y,
                                float* mu, int64_t n_rows, int64_t n_cols, int64_t ld_x,
                                int64_t ld_r, int64_t ld_h, int64_t ld_y, float eps, int dtype,
-                               int dtype_r, int dtype_w, void* stream) {
+                               int dtype_r, int dtype_y, int dtype_w, void* stream) {
   const char* nm = "kat_add_men_fwd";
   if (int rc = check_rows(nm, n_rows, n_cols)) return rc;
   if (n_rows == 0 || n_cols == 0) return KAT_OK;
@@ -1167,13 +1197,13 @@ extern "C" int kat_add_men_fwd(const void* x, const void* r, const void* w, void
   const hipStream_t st = as_stream(stream);
   if (dtype_w == dtype) {
     KAT_DISPATCH_T(dtype, nm,
-                   (add_men_fwd_d<T, T>(nm, dtype, dtype_r, x, r, w, h, y, mu, n_rows, n_cols,
-                                        ld_x, ld_r, ld_h, ld_y, eps, st)));
+                   (add_men_fwd_d<T, T>(nm, dtype, dtype_r, dtype_y, x, r, w, h, y, mu, n_rows,
+                                        n_cols, ld_x, ld_r, ld_h, ld_y, eps, st)));
   }
   if (dtype_w == KAT_F32 && dtype != KAT_F64) {
     KAT_DISPATCH_T(dtype, nm,
-                   (add_men_fwd_d<T, float>(nm, dtype, dtype_r, x, r, w, h, y, mu, n_rows, n_cols,
-                                            ld_x, ld_r, ld_h, ld_y, eps, st)));
+                   (add_men_fwd_d<T, float>(nm, dtype, dtype_r, dtype_y, x, r, w, h, y, mu, n_rows,
+                                            n_cols, ld_x, ld_r, ld_h, ld_y, eps, st)));
   }
   return fail(KAT_EUNSUPPORTED, "%s: weight dtype %d with input dtype %d", nm, dtype_w, dtype);
 }
@@ -1182,8 +1212,8 @@ extern "C" int kat_add_men_bwd(const void* dy, const void* dh, const void* h, co
                                const float* mu, void* dx, void* dr, void* dw, void* workspace,
                                size_t workspace_bytes, int64_t n_rows, int64_t n_cols,
                                int64_t ld_dy, int64_t ld_dh, int64_t ld_h, int64_t ld_dx,
-                               int64_t ld_dr, float eps, int dtype, int dtype_r, int dtype_w,
-                               void* stream) {
+                               int64_t ld_dr, float eps, int dtype, int dtype_r, int dtype_y,
+                               int dtype_w, void* stream) {
   const char* nm = "kat_add_men_bwd";
   if (int rc = check_rows(nm, n_rows, n_cols)) return rc;
   if (n_cols == 0) return KAT_OK;
@@ -1197,13 +1227,13 @@ extern "C" int kat_add_men_bwd(const void* dy, const void* dh, const void* h, co
   const hipStream_t st = as_stream(stream);
   if (dtype_w == dtype) {
     KAT_DISPATCH_T(dtype, nm,
-                   (add_men_bwd_d<T, T>(nm, dtype, dtype_r, dy, dh, h, w, mu, dx, dr, dw,
+                   (add_men_bwd_d<T, T>(nm, dtype, dtype_r, dtype_y, dy, dh, h, w, mu, dx, dr, dw,
                                         workspace, workspace_bytes, n_rows, n_cols, ld_dy, ld_dh,
                                         ld_h, ld_dx, ld_dr, eps, st)));
   }
   if (dtype_w == KAT_F32 && dtype != KAT_F64) {
     KAT_DISPATCH_T(dtype, nm,
-                   (add_men_bwd_d<T, float>(nm, dtype, dtype_r, dy, dh, h, w, mu, dx, dr, dw,
+                   (add_men_bwd_d<T, float>(nm, dtype, dtype_r, dtype_y, dy, dh, h, w, mu, dx, dr, dw,
                                             workspace, workspace_bytes, n_rows, n_cols, ld_dy,
                                             ld_dh, ld_h, ld_dx, ld_dr, eps, st)));
   }

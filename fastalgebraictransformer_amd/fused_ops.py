@@ -192,11 +192,14 @@ class ResidualMeanErrorNorm(torch.autograd.Function):
 
     ``r`` may be narrower than ``x`` (bf16/fp16 branch output beside an fp32
     residual stream, as under autocast); ``h`` has ``x``'s dtype exactly as
-    torch's promoted add gives it. Outputs and gradients equal those of
-    ``h = x + r; y = MeanErrorNorm.apply(h, weight, eps)`` bit for bit."""
+    torch's promoted add gives it. ``out_dtype`` (bf16/fp16 beside an fp32
+    stream) stores ``y`` narrowed, as the cast in front of an autocast matmul
+    would, and takes its gradient in that dtype. Outputs and gradients equal
+    those of ``h = x + r; y = MeanErrorNorm.apply(h, weight, eps)`` (followed
+    by ``y.to(out_dtype)``) bit for bit."""
 
     @staticmethod
-    def forward(ctx, x, r, weight, eps=EPS):
+    def forward(ctx, x, r, weight, eps=EPS, out_dtype=None):
         assert x.is_cuda and r.is_cuda, "Input must be on CUDA"
         assert r.shape == x.shape, "residual branch must have the stream's shape"
         lib = _lib.load()
@@ -206,15 +209,16 @@ class ResidualMeanErrorNorm(torch.autograd.Function):
         r2, ldr = _lib.rows2d(r)
         rows, cols = x2.shape
         h = torch.empty((rows, cols), dtype=x.dtype, device=x.device)
-        y = torch.empty((rows, cols), dtype=x.dtype, device=x.device)
+        y = torch.empty((rows, cols), dtype=out_dtype or x.dtype, device=x.device)
         mean = torch.empty(rows, dtype=torch.float32, device=x.device)
         _lib.check(lib.kat_add_men_fwd(_ptr(x2), _ptr(r2), _ptr(w), _ptr(h), _ptr(y), _ptr(mean),
                                        rows, cols, ldx, ldr, cols, cols, float(eps),
-                                       _lib.dtype_code(x), _lib.dtype_code(r),
+                                       _lib.dtype_code(x), _lib.dtype_code(r), _lib.dtype_code(y),
                                        _lib.dtype_code(w), _lib.stream(x)), "kat_add_men_fwd")
         ctx.save_for_backward(h, w, mean)
         ctx.eps = eps
         ctx.r_dtype = r.dtype
+        ctx.y_dtype = y.dtype
         return h.view(x.shape), y.view(x.shape)
 
     @staticmethod
@@ -222,7 +226,7 @@ class ResidualMeanErrorNorm(torch.autograd.Function):
         h, w, mean = ctx.saved_tensors
         lib = _lib.load()
         rows, cols = h.shape
-        g2, ldg = _lib.rows2d(grad_y.to(h.dtype))
+        g2, ldg = _lib.rows2d(grad_y.to(ctx.y_dtype))
         d2, ldd = _lib.rows2d(grad_h.to(h.dtype))
         code = _lib.dtype_code(h)
         dx = torch.empty((rows, cols), dtype=h.dtype, device=h.device)
@@ -240,14 +244,15 @@ class ResidualMeanErrorNorm(torch.autograd.Function):
                                        ws_bytes, rows, cols, ldg, ldd, cols, cols, cols,
                                        float(ctx.eps), code,
                                        _lib.dtype_code(dr if dr is not None else h),
-                                       _lib.dtype_code(w), _lib.stream(h)), "kat_add_men_bwd")
+                                       _lib.dtype_code(g2), _lib.dtype_code(w), _lib.stream(h)),
+                   "kat_add_men_bwd")
         shape = grad_y.shape
         dx = dx.view(shape)
         if not ctx.needs_input_grad[1]:
             d_r = None
         else:
             d_r = dx if dr is None else dr.view(shape)
-        return dx, d_r, dw, None
+        return dx, d_r, dw, None, None
 
 
 def rational_softmax(x, eps=EPS):
@@ -275,14 +280,18 @@ def mean_error_norm(x, weight, eps=EPS):
     return (x / (m + eps)) * weight
 
 
-def add_mean_error_norm(x, r, weight, eps=EPS):
+def add_mean_error_norm(x, r, weight, eps=EPS, out_dtype=None):
     """(x + r, mean_error_norm(x + r, weight, eps)) with the add fused into the
     norm on CUDA tensors (see ResidualMeanErrorNorm); CPU tensors use the
-    reference formulas."""
+    reference formulas. ``out_dtype``: the normalised output's dtype when it
+    feeds a narrower (autocast) matmul; default x's dtype."""
+    if out_dtype == x.dtype:
+        out_dtype = None
     if x.is_cuda:
-        return ResidualMeanErrorNorm.apply(x, r, weight, eps)
+        return ResidualMeanErrorNorm.apply(x, r, weight, eps, out_dtype)
     h = x + r
-    return h, mean_error_norm(h, weight, eps)
+    y = mean_error_norm(h, weight, eps)
+    return h, (y if out_dtype is None else y.to(out_dtype))
 
 
 def rational_swiglu_packed(gv):

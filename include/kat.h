@@ -111,18 +111,20 @@ int kat_men_bwd(const void* dy, const void* x, const void* w, const float* mu, v
 /* Residual add fused with the norm:
  *   h = x + r   (rounded to `dtype` as torch's promoted add rounds it)
  *   y = h / (mean|h| + eps) * w,  mu = mean|h|
- * x, h, y have `dtype`; r has `dtype_r`: `dtype`, or KAT_BF16 / KAT_F16 when
- * dtype is KAT_F32 (an autocast branch added to an fp32 residual stream).
- * h, y and mu equal the add followed by kat_men_fwd bit for bit. Replaces the
- * pre-norm block's `x = x + branch(...)` and the norm that reads it
- * (algebraic_model.py:150-151 -> fused_ops.py:558-564). h must not overlap
- * x or r. */
+ * x, h have `dtype`; r has `dtype_r` and y `dtype_y`, each `dtype`, or
+ * KAT_BF16 / KAT_F16 when dtype is KAT_F32 (an autocast branch added to an
+ * fp32 residual stream; a y read by an autocast matmul, rounded once as its
+ * cast would). h, y and mu equal the add followed by kat_men_fwd (and the
+ * cast) bit for bit. Replaces the pre-norm block's `x = x + branch(...)` and
+ * the norm that reads it (algebraic_model.py:150-151 -> fused_ops.py:558-564).
+ * h must not overlap x or r. */
 int kat_add_men_fwd(const void* x, const void* r, const void* w, void* h, void* y, float* mu,
                     int64_t n_rows, int64_t n_cols, int64_t ld_x, int64_t ld_r, int64_t ld_h,
-                    int64_t ld_y, float eps, int dtype, int dtype_r, int dtype_w, void* stream);
+                    int64_t ld_y, float eps, int dtype, int dtype_r, int dtype_y, int dtype_w,
+                    void* stream);
 
 /* Backward of kat_add_men_fwd. dh is the gradient reaching h through the
- * residual stream (dtype), dy the gradient of y:
+ * residual stream (dtype), dy the gradient of y (dtype_y):
  *   dx = round(norm_bwd(dy, h)) + dh   (as autograd sums h's two gradients)
  *   dr = dx cast to dtype_r (skipped when dr is NULL)
  *   dw = sum_rows dy * h / (mu + eps)
@@ -133,8 +135,8 @@ int kat_add_men_fwd(const void* x, const void* r, const void* w, void* h, void* 
 int kat_add_men_bwd(const void* dy, const void* dh, const void* h, const void* w, const float* mu,
                     void* dx, void* dr, void* dw, void* workspace, size_t workspace_bytes,
                     int64_t n_rows, int64_t n_cols, int64_t ld_dy, int64_t ld_dh, int64_t ld_h,
-                    int64_t ld_dx, int64_t ld_dr, float eps, int dtype, int dtype_r, int dtype_w,
-                    void* stream);
+                    int64_t ld_dx, int64_t ld_dr, float eps, int dtype, int dtype_r, int dtype_y,
+                    int dtype_w, void* stream);
 
 /* ------------------------------------------------------------------------
  * rational attention, layout [B, H, T, D] with arbitrary (b, h, t) strides and

@@ -44,6 +44,32 @@ def test_model_small_bf16_autocast_step(gpu):
     assert math.isfinite(gn) and gn > 0
 
 
+@pytest.mark.parametrize("ckpt", [False, True])
+def test_model_autocast_narrow_norm_outputs_change_no_bits(gpu, monkeypatch, ckpt):
+    # under autocast the fused norms write their outputs in bf16 directly;
+    # with that switched off (fp32 outputs, cast by the matmuls) the step
+    # must give the same logits, loss and gradients bit for bit
+    from fastalgebraictransformer_amd import algebraic_model as AM
+    torch.manual_seed(2)
+    m = F.AlgebraicTransformerLM(vocab_size=700, d_model=256, n_head=4, n_layers=3,
+                                 dropout=0.0, gradient_checkpointing=ckpt).cuda()
+    ids = torch.randint(0, 700, (2, 96), device="cuda")
+    runs = []
+    for narrow in (True, False):
+        if not narrow:
+            monkeypatch.setattr(AM, "_narrow", lambda x: None)
+        m.zero_grad(set_to_none=True)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            logits, loss = m(ids, labels=ids)
+        loss.backward()
+        runs.append((logits.detach().clone(), loss.detach().clone(),
+                     [p.grad.clone() for p in m.parameters()]))
+    (la, sa, ga), (lb, sb, gb) = runs
+    assert torch.equal(la, lb) and torch.equal(sa, sb)
+    for a, b in zip(ga, gb):
+        assert torch.equal(a, b)
+
+
 def test_model_gradient_checkpointing_matches(gpu):
     torch.manual_seed(1)
     m = F.AlgebraicTransformerLM(vocab_size=500, d_model=128, n_head=2, n_layers=2,

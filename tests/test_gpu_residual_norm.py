@@ -83,3 +83,34 @@ def test_fused_empty_rows(gpu):
     h, y = F.add_mean_error_norm(x, r, w)
     (h.sum() + y.sum()).backward()
     assert h.shape == (0, 64) and torch.equal(w.grad, torch.zeros(64, device="cuda"))
+
+
+@pytest.mark.parametrize("rd,yd,rows,cols", [(torch.bfloat16, torch.bfloat16, 300, 768),
+                                             (torch.float16, torch.float16, 64, 5000),
+                                             (torch.bfloat16, torch.float16, 50, 517),
+                                             (torch.float32, torch.bfloat16, 6, 33000)])
+def test_fused_narrow_output_matches_norm_then_cast(gpu, rd, yd, rows, cols):
+    # an fp32 stream whose norm output feeds an autocast matmul: y written in
+    # the narrow dtype equals the fp32 y cast to it, and its narrow gradient
+    # flows back as through the cast
+    seed = 3 * rows + cols
+    x0 = _rand((rows, cols), torch.float32, seed)
+    r0 = _rand((rows, cols), rd, seed + 1, 0.5)
+    w0 = (torch.rand(cols, generator=torch.Generator().manual_seed(seed + 2)) + 0.5).cuda()
+    dh = _rand((rows, cols), torch.float32, seed + 3)
+    dy = _rand((rows, cols), yd, seed + 4)
+
+    xf, rf, wf = (t.clone().requires_grad_(True) for t in (x0, r0, w0))
+    hf, yf = F.add_mean_error_norm(xf, rf, wf, out_dtype=yd)
+    torch.autograd.backward([hf, yf], [dh, dy])
+
+    xu, ru, wu = (t.clone().requires_grad_(True) for t in (x0, r0, w0))
+    hu = xu + ru
+    yu = F.mean_error_norm(hu, wu).to(yd)
+    torch.autograd.backward([hu, yu], [dh, dy])
+
+    assert yf.dtype == yd and hf.dtype == torch.float32
+    assert torch.equal(hf, hu) and torch.equal(yf, yu)
+    assert torch.equal(xf.grad, xu.grad)
+    assert rf.grad.dtype == rd and torch.equal(rf.grad, ru.grad)
+    assert torch.equal(wf.grad, wu.grad)

@@ -148,6 +148,37 @@ def test_add_mean_error_norm_cpu_is_add_then_norm():
     assert torch.equal(y, F.mean_error_norm(x + r, w))
 
 
+def test_add_mean_error_norm_cpu_out_dtype_is_the_cast():
+    x, r = torch.randn(4, 40), torch.randn(4, 40).to(torch.bfloat16)
+    w = torch.rand(40) + 0.5
+    h, y = F.add_mean_error_norm(x, r, w, out_dtype=torch.bfloat16)
+    assert h.dtype == torch.float32 and y.dtype == torch.bfloat16
+    assert torch.equal(y, F.mean_error_norm(x + r, w).to(torch.bfloat16))
+    _, y32 = F.add_mean_error_norm(x, r, w, out_dtype=torch.float32)
+    assert y32.dtype == torch.float32
+
+
+def test_model_loss_matches_reference_shifted_cross_entropy():
+    """The loss uses the full logits with the last position's target ignored;
+    the reference slices logits[..., :-1, :] and labels[..., 1:]
+    (algebraic_model.py:229-236). Same value (up to the order of the final
+    mean) and the same gradient, including labels that are already -100."""
+    torch.manual_seed(7)
+    m = F.AlgebraicTransformerLM(vocab_size=37, d_model=16, n_head=2, n_layers=1, dropout=0.0)
+    ids = torch.randint(0, 37, (3, 11))
+    labels = ids.clone()
+    labels[1, 4] = -100
+    logits, loss = m(ids, labels=labels)
+    lg = logits.detach().requires_grad_(True)
+    ref = torch.nn.functional.cross_entropy(lg[..., :-1, :].contiguous().view(-1, 37),
+                                            labels[..., 1:].contiguous().view(-1))
+    assert math.isclose(loss.item(), ref.item(), rel_tol=1e-6)
+    (g_ref,) = torch.autograd.grad(ref, lg)
+    (g_got,) = torch.autograd.grad(loss, logits)
+    assert torch.allclose(g_got, g_ref, rtol=1e-6, atol=1e-9)
+    assert torch.equal(g_got[:, -1], torch.zeros_like(g_got[:, -1]))
+
+
 def test_masked_attention_cpu_tensors_use_reference_cpu_formulation():
     # CPU tensors take the reference model's CPU attention (-1e4 fill)
     B, H, T, D = 2, 2, 9, 8
