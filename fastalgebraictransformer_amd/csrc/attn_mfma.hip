@@ -31,6 +31,13 @@
 // Backward math. With cinv_i = 1 / (16 (L_i + eps)):
 //   p  = t^4 cinv_i,   dS = p g (dP - Delta_i) = 4 cinv_i t^3 r^2 (dP - Delta_i)
 //   dQ = scale dS K,   dK = scale dS^T Q,   dV = P^T dO.
+// dS enters the dQ and dK products in fp16, which keeps 11 significant bits
+// only down to 2^-14: dS scales with the upstream gradient dO, and a training
+// step's dO (~1e-5 .. 1e-7 per element) would put it into fp16's subnormal
+// range or below. Every head therefore scales its dS by a power of two,
+// 2^k_bh, chosen from max |dO| of the head (max |dO| 2^k in [4, 8), the range
+// of an N(0,1) dO), and unscales dQ and dK by 2^-k_bh: exact in binary
+// floating point, so the results do not depend on the scale of dO.
 // The reference writes g = 2 / ((|s|+1)^2 (sigma + eps)) (backward.py:145);
 // these kernels use sigma in place of sigma + eps, a relative change of
 // eps / (sigma + eps) in dS: <= 2e-6 wherever s >= 0, and otherwise on scores
@@ -291,10 +298,13 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_k(AttnArgs a) {
 
 // ============================================================================
 // Backward prep (row-parallel, 8 elements per thread): k16 = K rounded to fp16
-// (clamped to +-65504), [B*H][T][D].
+// (clamped to +-65504), [B*H][T][D], and dmax = max_d |dO| per row, [B*H*T].
+// The LPR lanes of a row are consecutive lanes of one wave (LPR divides 64),
+// and a row's lanes all pass or all fail the range check together.
 // ============================================================================
 template <typename T, int D>
-__global__ __launch_bounds__(256) void attn_bwd_prep_k(AttnArgs a, f16* __restrict__ k16) {
+__global__ __launch_bounds__(256) void attn_bwd_prep_k(AttnArgs a, f16* __restrict__ k16,
+                                                       float* __restrict__ dmax) {
   constexpr int LPR = D / 8;
   const int sub = threadIdx.x % LPR;
   const int64_t row = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / LPR;
@@ -305,7 +315,40 @@ __global__ __launch_bounds__(256) void attn_bwd_prep_k(AttnArgs a, f16* __restri
   const int b = (int)(bh / a.H), h = (int)(bh % a.H);
   const int d = 8 * sub;
   const i16x8 kv = *reinterpret_cast<const i16x8*>((const T*)a.k + b * a.sk[0] + h * a.sk[1] + (int64_t)i * a.sk[2] + d);
+  const i16x8 gv = *reinterpret_cast<const i16x8*>((const T*)a.dout + b * a.sdo[0] + h * a.sdo[1] + (int64_t)i * a.sdo[2] + d);
   *reinterpret_cast<i16x8*>(k16 + row * D + d) = to_f16x8<T>(kv);
+  const VecT<T, 8> g8 = __builtin_bit_cast(VecT<T, 8>, gv);
+  float m = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf((float)g8.v[e]));
+#pragma unroll
+  for (int o = LPR / 2; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+  if (sub == 0) dmax[row] = m;
+}
+
+// The per-head dS scale: dscale[bh] = (2^k, 2^-k) with max |dO| 2^k in [4, 8)
+// over the head's rows; k = 0 when dO is all zero or not finite. One block per
+// (b, h); a fixed-order reduction.
+__global__ __launch_bounds__(256) void attn_bwd_dscale_k(const float* __restrict__ dmax, int T,
+                                                         float2* __restrict__ dscale) {
+  __shared__ float red[4];
+  const float* p = dmax + (int64_t)blockIdx.x * T;
+  float m = 0.f;
+  for (int t = threadIdx.x; t < T; t += 256) m = fmaxf(m, p[t]);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    int k = 0;
+    if (m > 0.f && m <= 3.0e38f) {
+      int e;
+      (void)frexpf(m, &e);  // m = f 2^e, f in [0.5, 1)
+      k = std::min(64, std::max(-64, 3 - e));
+    }
+    dscale[blockIdx.x] = make_float2(ldexpf(1.f, k), ldexpf(1.f, -k));
+  }
 }
 
 // ============================================================================
@@ -319,7 +362,8 @@ __global__ __launch_bounds__(256) void attn_bwd_prep_k(AttnArgs a, f16* __restri
 // ============================================================================
 template <typename T, int D, int MODE>
 __global__ __launch_bounds__(256, 2) void attn_bwd_dq_k(AttnArgs a, float2* __restrict__ stats,
-                                                        f16* __restrict__ q16, const f16* __restrict__ k16) {
+                                                        f16* __restrict__ q16, const f16* __restrict__ k16,
+                                                        const float2* __restrict__ dscale) {
   typedef Mfma<T> M;
   constexpr int KK = D / 32;
   constexpr int DS = D / 16;
@@ -350,7 +394,8 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_k(AttnArgs a, float2* __re
   const float scale = a.scale;
 
   i16x8 qf[2][KK], dof[2][KK];
-  float c4[2], nc4d[2];  // 4 cinv_q and -4 cinv_q Delta_q for q = qw + 16 qs + li
+  const float2 dsc = dscale[bh];  // (2^k, 2^-k) of this head's dS
+  float c4[2], nc4d[2];  // 2^k 4 cinv_q and -2^k 4 cinv_q Delta_q for q = qw + 16 qs + li
   {
     const __amdgpu_buffer_rsrc_t rq = rsrc(qp, row_bytes(T_, sq2, D));
     const __amdgpu_buffer_rsrc_t rd = rsrc(dop, row_bytes(T_, sdo2, D));
@@ -374,7 +419,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_k(AttnArgs a, float2* __re
       dsum += __shfl_xor(dsum, 32, 64);
       const bool ok = qrow < T_;
       const float l = ok ? Lp[(int64_t)qrow * a.sl[2]] : 0.f;
-      c4[qs] = ok ? 4.f / (16.f * (l + a.eps)) : 0.f;
+      c4[qs] = ok ? 4.f / (16.f * (l + a.eps)) * dsc.x : 0.f;  // dS scaled by 2^k
       nc4d[qs] = -c4[qs] * dsum;
       if (ok) {
         const int64_t r = (int64_t)bh * T_ + qrow;
@@ -553,8 +598,9 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_k(AttnArgs a, float2* __re
 #pragma unroll
       for (int ds = 0; ds < DS; ++ds) {
         const f32x4 o = dqacc[ds][qs];
+        const float osc = scale * dsc.y;  // and dS's 2^k undone (exact)
         *reinterpret_cast<u32x2*>(row + 16 * ds + 4 * g) =
-            u32x2{M::pack2(o[0] * scale, o[1] * scale), M::pack2(o[2] * scale, o[3] * scale)};
+            u32x2{M::pack2(o[0] * osc, o[1] * osc), M::pack2(o[2] * osc, o[3] * osc)};
       }
     }
   }
@@ -588,7 +634,8 @@ struct DkvSmem {
 
 template <typename T, int D, int MODE>
 __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float2* __restrict__ stats,
-                                                         const f16* __restrict__ q16) {
+                                                         const f16* __restrict__ q16,
+                                                         const float2* __restrict__ dscale) {
   typedef Mfma<T> M;
   constexpr int KK = D / 32;
   constexpr int DS = D / 16;
@@ -618,6 +665,9 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
   const uint32_t stbytes = (uint32_t)T_ * 8u;
   const float slope = a.slopes[h];
   const float scale = a.scale;
+  // the stats carry dS's 2^k (stats.x = 2^k 4 cinv); P takes 4 cinv / 16 = cinv / 4
+  const float2 dsc = dscale[bh];
+  const float p4 = 0.25f * dsc.y;
 
   // B operands: K16^T (P role) or V^T (D role) fragments; lane (g, li) holds row
   // kw + 16 ks + li, columns 32 kk + 8 g .. +7
@@ -719,7 +769,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
         const float t = fmaf(s, r, 1.f);
         const float t2 = t * t;
         const float u = t * r;
-        pv[j] = (t2 * t2) * (0.25f * c4v[j]);
+        pv[j] = (t2 * t2) * (p4 * c4v[j]);
         wv[j] = u * u * t;
         if (DIAG && kCausal && kw + 16 * ks + li > qh + 4 * g + j) {
           pv[j] = 0.f;
@@ -845,7 +895,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
 
   T* __restrict__ outp = prole ? (T*)a.dv + b * a.sdv[0] + h * a.sdv[1] : (T*)a.dk + b * a.sdk[0] + h * a.sdk[1];
   const int64_t ostr = prole ? a.sdv[2] : a.sdk[2];
-  const float osc = prole ? 1.f : scale;
+  const float osc = prole ? 1.f : scale * dsc.y;  // dK: dS's 2^k undone (exact)
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
     const int key = kw + 16 * ks + li;
@@ -870,7 +920,8 @@ bool attn_mfma_supported(int D) { return D == 64 || D == 128; }
 size_t attn_mfma_workspace(int64_t B, int64_t H, int64_t T, int64_t D) {
   const size_t rows = (size_t)(B * H * T);
   auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
-  return al(rows * sizeof(float2)) + 2 * al(rows * (size_t)D * sizeof(f16));
+  return al(rows * sizeof(float2)) + 2 * al(rows * (size_t)D * sizeof(f16)) + al(rows * sizeof(float)) +
+         al((size_t)(B * H) * sizeof(float2));
 }
 
 namespace {
@@ -899,15 +950,20 @@ int launch_bwd(const AttnArgs& a, void* ws, hipStream_t st) {
   float2* stats = reinterpret_cast<float2*>(ws);
   f16* q16 = reinterpret_cast<f16*>(reinterpret_cast<char*>(ws) + al(rows * sizeof(float2)));
   f16* k16 = reinterpret_cast<f16*>(reinterpret_cast<char*>(q16) + al(rows * D * sizeof(f16)));
+  float* dmax = reinterpret_cast<float*>(reinterpret_cast<char*>(k16) + al(rows * D * sizeof(f16)));
+  float2* dscale = reinterpret_cast<float2*>(reinterpret_cast<char*>(dmax) + al(rows * sizeof(float)));
   constexpr int rpb = 256 / (D / 8);
   hipLaunchKernelGGL((attn_bwd_prep_k<T, D>), dim3((unsigned)((rows + rpb - 1) / rpb)), dim3(256), 0, st, a,
-                     k16);
+                     k16, dmax);
   if (int rc = check_launch("kat_attn_bwd (prep)")) return rc;
+  hipLaunchKernelGGL(attn_bwd_dscale_k, dim3((unsigned)(a.B * a.H)), dim3(256), 0, st, dmax, a.T, dscale);
+  if (int rc = check_launch("kat_attn_bwd (dscale)")) return rc;
   // dq also writes stats and q16, which the dK / dV kernel reads
   const int64_t nt = (int64_t)((a.T + kBM - 1) / kBM) * a.B * a.H;
-  hipLaunchKernelGGL((attn_bwd_dq_k<T, D, MODE>), dim3((unsigned)nt), dim3(256), 0, st, a, stats, q16, k16);
+  hipLaunchKernelGGL((attn_bwd_dq_k<T, D, MODE>), dim3((unsigned)nt), dim3(256), 0, st, a, stats, q16, k16,
+                     dscale);
   if (int rc = check_launch("kat_attn_bwd (dq, mfma)")) return rc;
-  hipLaunchKernelGGL((attn_bwd_dkv_k<T, D, MODE>), dim3((unsigned)nt), dim3(512), 0, st, a, stats, q16);
+  hipLaunchKernelGGL((attn_bwd_dkv_k<T, D, MODE>), dim3((unsigned)nt), dim3(512), 0, st, a, stats, q16, dscale);
   return check_launch("kat_attn_bwd (dkv, mfma)");
 }
 

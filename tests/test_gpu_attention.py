@@ -216,3 +216,43 @@ def test_backward_is_deterministic(gpu, monkeypatch):
     b = _run(q, k, v, do, slopes, 0.088)
     for x, y in zip(a, b):
         assert torch.equal(x, y)
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("masked", [False, True])
+def test_mfma_backward_is_invariant_to_the_upstream_gradient_scale(gpu, D, masked, monkeypatch):
+    # dQ, dK, dV are linear in dO. A training step's dO is ~1e-5 .. 1e-7 per
+    # element, where an unscaled fp16 dS would lose its significant bits; the
+    # kernels scale dS per head by a power of two, so dO * 2^-e must give
+    # exactly 2^-e times the gradients of dO (bit for bit: every scaling is a
+    # power of two and the outputs stay within bf16's exponent range)
+    monkeypatch.setenv("KAT_ATTN_IMPL", "mfma")
+    B, H, T = 2, 3, 300
+    q, k, v, do = _inputs(31 + D, B, H, T, D, torch.bfloat16)
+    slopes = F.compute_alibi_slopes(H).to(dev)
+    scale = 1.0 / math.sqrt(D)
+    km = None
+    if masked:
+        km = torch.ones(B, T, dtype=torch.int32, device=dev)
+        km[1, T // 2:] = 0
+
+    def grads(dout):
+        qq, kk, vv = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+        if masked:
+            o = F.rational_attention_masked(qq, kk, vv, slopes, scale, key_mask=km)
+        else:
+            o = F.rational_attention(qq, kk, vv, slopes, scale)
+        o.backward(dout)
+        torch.cuda.synchronize()
+        return qq.grad, kk.grad, vv.grad
+
+    base = grads(do)
+    for e in (12, 20, 28):
+        got = grads(do * 2.0 ** -e)
+        for name, gt, b in zip(("dq", "dk", "dv"), got, base):
+            assert torch.equal(gt.float() * 2.0 ** e, b.float()), (name, e)
+    if not masked:  # and the unscaled gradients still meet the oracle bar
+        o, L = F.rational_attention_forward(q, k, v, slopes, scale)
+        rq, rk, rv = O.attention_bwd(q, k, v, o, L, do, slopes, scale, dtype=torch.float32)
+        for name, gt, r in zip(("dq", "dk", "dv"), base, (rq, rk, rv)):
+            assert_lowp(gt, r, torch.bfloat16, name)
