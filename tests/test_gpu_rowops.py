@@ -197,12 +197,22 @@ def test_softmax_config2_bf16(gpu):
 
 # ------------------------------------------------------- layouts, edges ----
 
-def test_swiglu_on_packed_chunks_matches_contiguous(gpu):
-    gv = _seeded(40, 3, 50, 2 * 264, dtype=torch.bfloat16).to(dev)
-    gate, value = gv.chunk(2, dim=-1)
-    a = F.rational_swiglu(gate, value)
-    b = F.rational_swiglu(gate.contiguous(), value.contiguous())
+@pytest.mark.parametrize("dtype,f", [(torch.bfloat16, 264), (torch.bfloat16, 2048),
+                                     (torch.float32, 1024), (torch.float32, 36)])
+def test_swiglu_on_packed_chunks_matches_contiguous(gpu, dtype, f):
+    # strided halves (row-indexed kernels: a general row length, and power-of-two
+    # lengths, which index by shifts) against the flat launch over contiguous
+    # copies, forward and backward
+    gv = _seeded(40 + f, 3, 50, 2 * f, dtype=dtype).to(dev)
+    dy = _seeded(41 + f, 3, 50, f, dtype=dtype).to(dev)
+    ga, va = (t.detach().requires_grad_(True) for t in gv.chunk(2, dim=-1))
+    gb, vb = (t.detach().contiguous().requires_grad_(True) for t in gv.chunk(2, dim=-1))
+    a = F.rational_swiglu(ga, va)
+    b = F.rational_swiglu(gb, vb)
     assert torch.equal(a, b)
+    a.backward(dy)
+    b.backward(dy)
+    assert torch.equal(ga.grad, gb.grad) and torch.equal(va.grad, vb.grad)
 
 
 @pytest.mark.parametrize("cols", [1, 7, 13, 100, 1000, 9000, 20000])
