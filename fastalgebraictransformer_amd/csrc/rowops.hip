@@ -207,36 +207,73 @@ __global__ __launch_bounds__(kEwThreads) void swiglu_bwd_k(
   }
 }
 
-// Scalar fallback for misaligned / odd-width inputs.
+// Scalar fallback for misaligned / odd-width inputs (e.g. the packed gate /
+// value halves of an odd d_ffn, whose value half is only 2-byte aligned). A 2D
+// grid: blockIdx.y walks rows, x and the unrolled lanes walk columns, so no
+// element index is divided by the row length (a 64-bit division per element
+// cost more than the memory traffic); each thread keeps kEwUnroll elements in
+// flight, 256 columns apart, for coalesced 2-byte accesses.
 template <typename T>
 __global__ __launch_bounds__(kEwThreads) void swiglu_fwd_scalar_k(
-    const T* __restrict__ g, const T* __restrict__ v, T* __restrict__ o, uint64_t n,
-    uint64_t cols, int64_t ldg, int64_t ldv, int64_t ldo) {
+    const T* __restrict__ g, const T* __restrict__ v, T* __restrict__ o, int64_t rows,
+    int64_t cols, int64_t ldg, int64_t ldv, int64_t ldo) {
   typedef typename AccT<T>::type A;
-  for (uint64_t e = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n;
-       e += (uint64_t)gridDim.x * blockDim.x) {
-    const int64_t r = (int64_t)(e / cols), c = (int64_t)(e - (uint64_t)r * cols);
-    const A gg = to_acc(g[r * ldg + c]), vv = to_acc(v[r * ldv + c]);
-    o[r * ldo + c] = from_acc<T>(gg * rsig(gg) * vv);
+  const int64_t c0 = (int64_t)blockIdx.x * (kEwThreads * kEwUnroll) + threadIdx.x;
+  for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
+    T gr[kEwUnroll], vr[kEwUnroll];
+#pragma unroll
+    for (int u = 0; u < kEwUnroll; ++u) {
+      const int64_t c = c0 + u * kEwThreads;
+      const int64_t cc = c < cols ? c : 0;
+      gr[u] = g[r * ldg + cc];
+      vr[u] = v[r * ldv + cc];
+    }
+#pragma unroll
+    for (int u = 0; u < kEwUnroll; ++u) {
+      const int64_t c = c0 + u * kEwThreads;
+      const A gg = to_acc(gr[u]), vv = to_acc(vr[u]);
+      if (c < cols) o[r * ldo + c] = from_acc<T>(gg * rsig(gg) * vv);  // fused_ops.py:224-227
+    }
   }
 }
 
 template <typename T>
 __global__ __launch_bounds__(kEwThreads) void swiglu_bwd_scalar_k(
     const T* __restrict__ dy, const T* __restrict__ g, const T* __restrict__ v,
-    T* __restrict__ dg, T* __restrict__ dv, uint64_t n, uint64_t cols, int64_t lddy, int64_t ldg,
+    T* __restrict__ dg, T* __restrict__ dv, int64_t rows, int64_t cols, int64_t lddy, int64_t ldg,
     int64_t ldv, int64_t lddg, int64_t lddv) {
   typedef typename AccT<T>::type A;
-  for (uint64_t e = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n;
-       e += (uint64_t)gridDim.x * blockDim.x) {
-    const int64_t r = (int64_t)(e / cols), c = (int64_t)(e - (uint64_t)r * cols);
-    const A y = to_acc(dy[r * lddy + c]), gg = to_acc(g[r * ldg + c]), vv = to_acc(v[r * ldv + c]);
-    const A den = fabs(gg) + A(1);
-    const A sig = A(0.5) * (gg / den + A(1));
-    const A sd = A(0.5) / (den * den);
-    dv[r * lddv + c] = from_acc<T>(y * gg * sig);
-    dg[r * lddg + c] = from_acc<T>(y * vv * (sig + gg * sd));
+  const int64_t c0 = (int64_t)blockIdx.x * (kEwThreads * kEwUnroll) + threadIdx.x;
+  for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
+    T yr[kEwUnroll], gr[kEwUnroll], vr[kEwUnroll];
+#pragma unroll
+    for (int u = 0; u < kEwUnroll; ++u) {
+      const int64_t c = c0 + u * kEwThreads;
+      const int64_t cc = c < cols ? c : 0;
+      yr[u] = dy[r * lddy + cc];
+      gr[u] = g[r * ldg + cc];
+      vr[u] = v[r * ldv + cc];
+    }
+#pragma unroll
+    for (int u = 0; u < kEwUnroll; ++u) {
+      const int64_t c = c0 + u * kEwThreads;
+      const A y = to_acc(yr[u]), gg = to_acc(gr[u]), vv = to_acc(vr[u]);
+      const A den = fabs(gg) + A(1);  // fused_ops.py:276-285
+      const A sig = A(0.5) * (gg / den + A(1));
+      const A sd = A(0.5) / (den * den);
+      if (c < cols) {
+        dv[r * lddv + c] = from_acc<T>(y * gg * sig);
+        dg[r * lddg + c] = from_acc<T>(y * vv * (sig + gg * sd));
+      }
+    }
   }
+}
+
+// 2D grid of the scalar SwiGLU kernels: column blocks by row blocks (rows are
+// walked in a loop past 65535)
+static dim3 scalar_grid(int64_t rows, int64_t cols) {
+  const int64_t per = (int64_t)kEwThreads * kEwUnroll;
+  return dim3((unsigned)((cols + per - 1) / per), (unsigned)std::min<int64_t>(rows, 65535));
 }
 
 // ============================================================================
@@ -975,10 +1012,8 @@ static int swiglu_fwd_t(const T* g, const T* v, T* o, int64_t rows, int64_t cols
                          ldv, ldo);
     }
   } else {
-    const uint64_t n = (uint64_t)rows * (uint64_t)cols;
-    const uint64_t blocks = std::min<uint64_t>((n + kEwThreads - 1) / kEwThreads, 65536);
-    hipLaunchKernelGGL((swiglu_fwd_scalar_k<T>), dim3((unsigned)blocks), dim3(kEwThreads), 0, st,
-                       g, v, o, n, (uint64_t)cols, ldg, ldv, ldo);
+    hipLaunchKernelGGL((swiglu_fwd_scalar_k<T>), scalar_grid(rows, cols), dim3(kEwThreads), 0, st, g,
+                       v, o, rows, cols, ldg, ldv, ldo);
   }
   return check_launch("kat_rswiglu_fwd");
 }
@@ -1009,10 +1044,8 @@ static int swiglu_bwd_t(const T* dy, const T* g, const T* v, T* dg, T* dv, int64
                          dv + r0 * lddv, n_chunks, (uint32_t)cpr, lddy, ldg, ldv, lddg, lddv);
     }
   } else {
-    const uint64_t n = (uint64_t)rows * (uint64_t)cols;
-    const uint64_t blocks = std::min<uint64_t>((n + kEwThreads - 1) / kEwThreads, 65536);
-    hipLaunchKernelGGL((swiglu_bwd_scalar_k<T>), dim3((unsigned)blocks), dim3(kEwThreads), 0, st,
-                       dy, g, v, dg, dv, n, (uint64_t)cols, lddy, ldg, ldv, lddg, lddv);
+    hipLaunchKernelGGL((swiglu_bwd_scalar_k<T>), scalar_grid(rows, cols), dim3(kEwThreads), 0, st, dy,
+                       g, v, dg, dv, rows, cols, lddy, ldg, ldv, lddg, lddv);
   }
   return check_launch("kat_rswiglu_bwd");
 }

@@ -215,6 +215,26 @@ def test_swiglu_on_packed_chunks_matches_contiguous(gpu, dtype, f):
     assert torch.equal(ga.grad, gb.grad) and torch.equal(va.grad, vb.grad)
 
 
+@pytest.mark.parametrize("dtype,f", [(torch.bfloat16, 263), (torch.float16, 5461),
+                                     (torch.float32, 37)])
+def test_swiglu_odd_packed_halves_match_oracle(gpu, dtype, f):
+    # an odd d_ffn: the value half of the packed [rows, 2F] buffer is only
+    # element-aligned, so the scalar kernels run (2D grid, rows past 65535
+    # walked in a loop -- 70000 rows here), forward and backward
+    rows = 70000 if f < 300 else 40
+    gv = _seeded(70 + f, rows, 2 * f, dtype=dtype).to(dev)
+    dy = _seeded(71 + f, rows, f, dtype=dtype).to(dev)
+    gvr = gv.clone().requires_grad_(True)
+    out = F.rational_swiglu_packed(gvr)
+    out.backward(dy)
+    g, v = gv.chunk(2, dim=-1)
+    tol = 1e-5 if dtype == torch.float32 else 1e-2
+    assert_rel(out, O.swiglu_fwd(g.cpu(), v.cpu()), tol, "swiglu odd fwd", floor_frac=tol)
+    dg, dv = O.swiglu_bwd(dy.cpu(), g.cpu(), v.cpu())
+    assert_rel(gvr.grad[..., :f], dg, tol, "swiglu odd dgate", floor_frac=tol)
+    assert_rel(gvr.grad[..., f:], dv, tol, "swiglu odd dvalue", floor_frac=tol)
+
+
 @pytest.mark.parametrize("cols", [1, 7, 13, 100, 1000, 9000, 20000])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 def test_odd_and_wide_rows(gpu, cols, dtype):
