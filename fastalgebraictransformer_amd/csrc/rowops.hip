@@ -300,17 +300,19 @@ template <typename A> __device__ __forceinline__ A block_sum_par(A v, A (*red)[k
 // row's first chunk (always in bounds) and are masked where they are used:
 // a conditional load here would compile to a branch that waits for the data
 // on the spot, serialising the prefetch.
-template <typename T, int NCH>
+// FULL: the row is exactly NCH chunk rounds long, so every chunk is in range
+// and the column tests fold away (the norm kernels take this when it holds).
+template <typename T, int NCH, bool FULL = false>
 __device__ __forceinline__ void load_row(const T* __restrict__ base, int n_cols, VecT<T, Raw<T>::V> (&r)[NCH]) {
   constexpr int V = Raw<T>::V;
 #pragma unroll
   for (int k = 0; k < NCH; ++k) {
     const int col = ((int)threadIdx.x + 256 * k) * V;
-    r[k] = ld_vec<T, V>(base + (col < n_cols ? col : 0));
+    r[k] = ld_vec<T, V>(base + ((FULL || col < n_cols) ? col : 0));
   }
 }
-__device__ __forceinline__ bool chunk_in(int k, int V, int n_cols) {
-  return ((int)threadIdx.x + 256 * k) * V < n_cols;
+template <bool FULL = false> __device__ __forceinline__ bool chunk_in(int k, int V, int n_cols) {
+  return FULL || ((int)threadIdx.x + 256 * k) * V < n_cols;
 }
 
 // The weight values of this thread's chunks, with 16-byte loads (the caller
@@ -637,13 +639,13 @@ __device__ __forceinline__ void st_vec_any(R* __restrict__ p, const VecT<R, V>& 
     __builtin_nontemporal_store(__builtin_bit_cast(u32x2_t, v), reinterpret_cast<u32x2_t*>(p));
   }
 }
-template <typename R, int V, int NCH>
+template <typename R, int V, int NCH, bool FULL = false>
 __device__ __forceinline__ void load_row_any(const R* __restrict__ base, int n_cols,
                                              VecT<R, V> (&r)[NCH]) {
 #pragma unroll
   for (int k = 0; k < NCH; ++k) {
     const int col = ((int)threadIdx.x + 256 * k) * V;
-    r[k] = ld_vec_any<R, V>(base + (col < n_cols ? col : 0));
+    r[k] = ld_vec_any<R, V>(base + ((FULL || col < n_cols) ? col : 0));
   }
 }
 
@@ -652,7 +654,7 @@ __device__ __forceinline__ void load_row_any(const R* __restrict__ base, int n_c
 // norm1, algebraic_model.py:150-151): h = x + r is rounded to T exactly as
 // torch's promoted add rounds it, written once, and normalised from registers,
 // so (h, y, mu) are bit-identical to the add followed by the plain norm.
-template <typename T, typename W, int NCH, typename R = void, typename Y = T>
+template <typename T, typename W, int NCH, typename R = void, typename Y = T, bool FULL = false>
 __global__ __launch_bounds__(256) void men_fwd_k(const T* __restrict__ x, const W* __restrict__ w,
                                                  Y* __restrict__ y, float* __restrict__ mu,
                                                  int64_t n_rows, int n_cols, int64_t ldx,
@@ -671,29 +673,29 @@ __global__ __launch_bounds__(256) void men_fwd_k(const T* __restrict__ x, const 
   const int64_t last = n_rows - 1;
   VecT<T, V> cur[NCH], nx1[NCH];
   VecT<RT, V> rc[NCH], r1[NCH];
-  load_row<T, NCH>(x + std::min(row, last) * ldx, n_cols, cur);
-  if constexpr (kAdd) load_row_any<RT, V, NCH>(r + std::min(row, last) * ldr, n_cols, rc);
-  load_row<T, NCH>(x + std::min(row + G, last) * ldx, n_cols, nx1);
-  if constexpr (kAdd) load_row_any<RT, V, NCH>(r + std::min(row + G, last) * ldr, n_cols, r1);
+  load_row<T, NCH, FULL>(x + std::min(row, last) * ldx, n_cols, cur);
+  if constexpr (kAdd) load_row_any<RT, V, NCH, FULL>(r + std::min(row, last) * ldr, n_cols, rc);
+  load_row<T, NCH, FULL>(x + std::min(row + G, last) * ldx, n_cols, nx1);
+  if constexpr (kAdd) load_row_any<RT, V, NCH, FULL>(r + std::min(row + G, last) * ldr, n_cols, r1);
   for (int par = 0; row < n_rows; row += G, par ^= 1) {
     VecT<T, V> nx2[NCH];
     VecT<RT, V> r2[NCH];
-    load_row<T, NCH>(x + std::min(row + 2 * G, last) * ldx, n_cols, nx2);
+    load_row<T, NCH, FULL>(x + std::min(row + 2 * G, last) * ldx, n_cols, nx2);
     if constexpr (kAdd) {
-      load_row_any<RT, V, NCH>(r + std::min(row + 2 * G, last) * ldr, n_cols, r2);
+      load_row_any<RT, V, NCH, FULL>(r + std::min(row + 2 * G, last) * ldr, n_cols, r2);
 #pragma unroll
       for (int k = 0; k < NCH; ++k) {
         const int col = ((int)threadIdx.x + 256 * k) * V;
 #pragma unroll
         for (int i = 0; i < V; ++i)
           cur[k].v[i] = from_acc<T>(to_acc(cur[k].v[i]) + to_acc(rc[k].v[i]));
-        if (col < n_cols) st_vec<T, V>(h + row * ldh + col, cur[k]);
+        if (FULL || col < n_cols) st_vec<T, V>(h + row * ldh + col, cur[k]);
       }
     }
     A s = A(0);
 #pragma unroll
     for (int k = 0; k < NCH; ++k) {
-      const bool in = chunk_in(k, V, n_cols);
+      const bool in = chunk_in<FULL>(k, V, n_cols);
 #pragma unroll
       for (int i = 0; i < V; ++i) s += in ? fabs(to_acc(cur[k].v[i])) : A(0);  // fused_ops.py:324
     }
@@ -704,7 +706,7 @@ __global__ __launch_bounds__(256) void men_fwd_k(const T* __restrict__ x, const 
 #pragma unroll
     for (int k = 0; k < NCH; ++k) {
       const int col = ((int)threadIdx.x + 256 * k) * V;
-      if (col < n_cols) {
+      if (FULL || col < n_cols) {
         VecT<Y, V> o;
 #pragma unroll
         for (int i = 0; i < V; ++i) o.v[i] = narrow_to<Y>(to_acc(cur[k].v[i]) * inv * wv[k][i]);  // :340
@@ -733,7 +735,7 @@ constexpr int kNormPf = 2;
 // through the residual stream, and dx = round_T(norm_bwd) + dh (the sum
 // autograd forms for h, in T), written for x and, cast to R, for r (dr may
 // be null).
-template <typename T, typename W, int NCH, typename R = void, typename Y = T>
+template <typename T, typename W, int NCH, typename R = void, typename Y = T, bool FULL = false>
 __global__ __launch_bounds__(256) void men_bwd_k(
     const Y* __restrict__ dy, const T* __restrict__ x, const W* __restrict__ w,
     const float* __restrict__ mu, T* __restrict__ dx, typename AccT<T>::type* __restrict__ partial,
@@ -765,24 +767,24 @@ __global__ __launch_bounds__(256) void men_bwd_k(
 #pragma unroll
   for (int j = 0; j < PF; ++j) {
     const int64_t r = std::min(row + j * G, last);
-    load_row_any<Y, V, NCH>(dy + r * lddy, n_cols, by[j]);
-    load_row<T, NCH>(x + r * ldx, n_cols, bx[j]);
-    if constexpr (kAdd) load_row<T, NCH>(dh + r * lddh, n_cols, bh[j]);
+    load_row_any<Y, V, NCH, FULL>(dy + r * lddy, n_cols, by[j]);
+    load_row<T, NCH, FULL>(x + r * ldx, n_cols, bx[j]);
+    if constexpr (kAdd) load_row<T, NCH, FULL>(dh + r * lddh, n_cols, bh[j]);
     bm[j] = mu[r];  // the row statistic travels with its row
   }
   for (int par = 0; row < n_rows; row += G, par ^= 1) {
     {
       const int64_t r = std::min(row + PF * G, last);
-      load_row_any<Y, V, NCH>(dy + r * lddy, n_cols, by[PF]);
-      load_row<T, NCH>(x + r * ldx, n_cols, bx[PF]);
-      if constexpr (kAdd) load_row<T, NCH>(dh + r * lddh, n_cols, bh[PF]);
+      load_row_any<Y, V, NCH, FULL>(dy + r * lddy, n_cols, by[PF]);
+      load_row<T, NCH, FULL>(x + r * ldx, n_cols, bx[PF]);
+      if constexpr (kAdd) load_row<T, NCH, FULL>(dh + r * lddh, n_cols, bh[PF]);
       bm[PF] = mu[r];
     }
     const A inv = A(1) / ((A)bm[0] + e);  // fused_ops.py:389-390
     A cs = A(0);
 #pragma unroll
     for (int k = 0; k < NCH; ++k) {
-      const bool in = chunk_in(k, V, n_cols);
+      const bool in = chunk_in<FULL>(k, V, n_cols);
 #pragma unroll
       for (int i = 0; i < V; ++i) {
         const A p = to_acc(bx[0][k].v[i]) * inv * wv[k][i];
@@ -794,7 +796,7 @@ __global__ __launch_bounds__(256) void men_bwd_k(
 #pragma unroll
     for (int k = 0; k < NCH; ++k) {
       const int col = ((int)threadIdx.x + 256 * k) * V;
-      const bool in = col < n_cols;
+      const bool in = FULL || col < n_cols;
       VecT<T, V> o;
 #pragma unroll
       for (int i = 0; i < V; ++i) {
@@ -830,7 +832,7 @@ __global__ __launch_bounds__(256) void men_bwd_k(
     const int col = ((int)threadIdx.x + 256 * k) * V;
 #pragma unroll
     for (int i = 0; i < V; ++i)
-      if (col + i < n_cols) partial[(int64_t)blockIdx.x * n_cols + col + i] = dg[k][i];
+      if (FULL || col + i < n_cols) partial[(int64_t)blockIdx.x * n_cols + col + i] = dg[k][i];
   }
 }
 
@@ -979,6 +981,13 @@ static inline bool wave_rows(int64_t rows) { return rows <= (int64_t)16 * num_cu
     default: { constexpr int N = 8; __VA_ARGS__; } break; \
   }
 
+// The predicate-free (FULL) norm kernels exist for 2 and 4 chunk rounds: rows
+// of 4096 / 8192 bf16 or 2048 / 4096 fp32 values, the benchmark's and model
+// widths (measured 4% faster backward at 16384 x 4096); at 8 rounds the 16-bit
+// residual-add backward would spill.
+constexpr bool kat_full_nch(int n) { return n == 2 || n == 4; }
+static inline bool kat_full_variant(int n, bool full) { return full && kat_full_nch(n); }
+
 #define KAT_NCH_SWITCH(nch, ...)          \
   switch (nch) {                          \
     case 1: { constexpr int N = 1; __VA_ARGS__; } break;  \
@@ -1112,9 +1121,16 @@ static int men_fwd_t(const T* x, const W* w, Y* y, float* mu, int64_t rows, int6
   const int nch = vec ? pick_nch(cols, 256 * V) : 0;
   if (nch) {
     const int64_t blocks = row_grid(rows, kRowBlocksPerCU);
-    KAT_NCH_SWITCH(nch, hipLaunchKernelGGL((men_fwd_k<T, W, N, R, Y>), dim3((unsigned)blocks),
-                                           dim3(256), 0, st, x, w, y, mu, rows, (int)cols, ldx,
-                                           ldy, eps, (const void*)r, h, ldr, ldh));
+    const bool full = cols == (int64_t)nch * 256 * V;
+    KAT_NCH_SWITCH(nch, {
+      if (kat_full_variant(N, full))
+        hipLaunchKernelGGL((men_fwd_k<T, W, N, R, Y, kat_full_nch(N)>), dim3((unsigned)blocks),
+                           dim3(256), 0, st, x, w, y, mu, rows, (int)cols, ldx, ldy, eps,
+                           (const void*)r, h, ldr, ldh);
+      else
+        hipLaunchKernelGGL((men_fwd_k<T, W, N, R, Y>), dim3((unsigned)blocks), dim3(256), 0, st, x,
+                           w, y, mu, rows, (int)cols, ldx, ldy, eps, (const void*)r, h, ldr, ldh);
+    });
   } else {
     hipLaunchKernelGGL((men_fwd_mp_k<T, R, Y>), dim3((unsigned)rows), dim3(256), 0, st, x,
                        (const void*)w, (int)std::is_same<W, float>::value, y, mu, rows, (int)cols,
@@ -1153,9 +1169,17 @@ static int men_bwd_t(const Y* dy, const T* x, const W* w, const float* mu, T* dx
     return fail(KAT_EINVAL, "%s: workspace %zu bytes < required %zu", nm, ws_bytes, need);
   A* partial = reinterpret_cast<A*>(ws);
   if (nch) {
-    KAT_NCH_SWITCH(nch, hipLaunchKernelGGL((men_bwd_k<T, W, N, R, Y>), dim3(G), dim3(256), 0, st, dy,
-                                           x, w, mu, dx, partial, rows, (int)cols, lddy, ldx, lddx,
-                                           eps, dh, lddh, (void*)dr, lddr));
+    const bool full = cols == (int64_t)nch * 256 * V;
+    KAT_NCH_SWITCH(nch, {
+      if (kat_full_variant(N, full))
+        hipLaunchKernelGGL((men_bwd_k<T, W, N, R, Y, kat_full_nch(N)>), dim3(G), dim3(256), 0, st,
+                           dy, x, w, mu, dx, partial, rows, (int)cols, lddy, ldx, lddx, eps, dh,
+                           lddh, (void*)dr, lddr);
+      else
+        hipLaunchKernelGGL((men_bwd_k<T, W, N, R, Y>), dim3(G), dim3(256), 0, st, dy, x, w, mu, dx,
+                           partial, rows, (int)cols, lddy, ldx, lddx, eps, dh, lddh, (void*)dr,
+                           lddr);
+    });
   } else {
     hipLaunchKernelGGL((men_bwd_mp_k<T, R, Y>), dim3(G), dim3(256), 0, st, dy, x, (const void*)w,
                        (int)std::is_same<W, float>::value, mu, dx, partial, rows, (int)cols, lddy,

@@ -30,6 +30,8 @@ CASES = [
     (torch.float64, torch.float64, torch.float64, 33, 256),
     (torch.float32, torch.bfloat16, torch.float32, 50, 517),    # odd width: multi-pass kernels
     (torch.bfloat16, torch.bfloat16, torch.bfloat16, 6, 33000),  # wider than the resident path
+    (torch.float32, torch.bfloat16, torch.float32, 256, 2048),  # whole chunk rounds: the
+    (torch.bfloat16, torch.bfloat16, torch.float32, 128, 4096),  # predicate-free kernels
 ]
 
 
@@ -86,6 +88,7 @@ def test_fused_empty_rows(gpu):
 
 
 @pytest.mark.parametrize("rd,yd,rows,cols", [(torch.bfloat16, torch.bfloat16, 300, 768),
+                                             (torch.bfloat16, torch.bfloat16, 200, 4096),
                                              (torch.float16, torch.float16, 64, 5000),
                                              (torch.bfloat16, torch.float16, 50, 517),
                                              (torch.float32, torch.bfloat16, 6, 33000)])
