@@ -53,7 +53,7 @@ PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
 # counter reads for a plain 1 GiB copy (python bench.py --copy-calibration:
 # FETCH_SIZE x 2.0, WRITE_SIZE x 1.0). Summary and commands:
 # profiles/attention_bench_hbm_traffic.md
-MEASURED_TRAFFIC_BYTES = {"kat_attn_fwd": 749.1 * 2 ** 20, "kat_attn_bwd": 1976.3 * 2 ** 20}
+MEASURED_TRAFFIC_BYTES = {"kat_attn_fwd": 745.8 * 2 ** 20, "kat_attn_bwd": 1985.5 * 2 ** 20}
 
 
 def attention_inputs(torch, B, H, T, D, dev, seed=0):
