@@ -1,14 +1,15 @@
 // bf16 / fp16 MFMA rational attention for gfx950 (CDNA4).
 //
-// Three kernels carry the attention math, plus a streaming prep pass:
-//   attn_fwd_k      O, L      query-tile blocks; K, V tiles stream through LDS
-//   attn_bwd_prep_k fp16 copy of K (row-parallel)
-//   attn_bwd_dq_k   dQ        query-tile blocks; fp16 K and V tiles stream; also
-//                             Delta, the row stats and the fp16 copy of Q
-//   attn_bwd_dkv_k  dK, dV    key-tile blocks; fp16 Q and dO tiles stream; the
-//                             waves split into a dV role and a dK role
-// No atomics: every output element is written by one wave, so results are
-// deterministic.
+// Three kernels carry the attention math, plus two streaming passes:
+//   attn_fwd_k         O, L      query-tile blocks; K, V tiles stream through LDS
+//   attn_bwd_prep_k    fp16 copy of K, per-tile exponents and V row norms
+//   attn_bwd_dq_k      dQ        query-tile blocks; fp16 K and V tiles stream; also
+//                                Delta, the row stats and the fp16 copy of Q
+//   attn_bwd_stscale_k scales the row stats by the head's dS exponent
+//   attn_bwd_dkv_k     dK, dV    key-tile blocks; fp16 Q and dO tiles stream; the
+//                                waves split into a dV role and a dK role
+// Every output element is written by one wave, so results are deterministic
+// (the only atomic is a max over non-negative floats, which is order-free).
 //
 // Common structure. Each wave owns 32 rows (queries, or keys for dK/dV) whose
 // operand fragments stay in VGPRs as the B operand of v_mfma_f32_16x16x32; the
@@ -31,13 +32,25 @@
 // Backward math. With cinv_i = 1 / (16 (L_i + eps)):
 //   p  = t^4 cinv_i,   dS = p g (dP - Delta_i) = 4 cinv_i t^3 r^2 (dP - Delta_i)
 //   dQ = scale dS K,   dK = scale dS^T Q,   dV = P^T dO.
-// dS enters the dQ and dK products in fp16, which keeps 11 significant bits
-// only down to 2^-14: dS scales with the upstream gradient dO, and a training
-// step's dO (~1e-5 .. 1e-7 per element) would put it into fp16's subnormal
-// range or below. Every head therefore scales its dS by a power of two,
-// 2^k_bh, chosen from max |dO| of the head (max |dO| 2^k in [4, 8), the range
-// of an N(0,1) dO), and unscales dQ and dK by 2^-k_bh: exact in binary
-// floating point, so the results do not depend on the scale of dO.
+// Range. dS enters the dQ and dK products in fp16 (normal range 2^-14 ..
+// 65504), and so do the copies of Q and K those products (and the recomputed
+// S) take. Every fp16 operand carries a power-of-two scale chosen from the
+// data, and every scale is undone exactly (binary floating point):
+//   * Q16 and K16: one exponent per 64-row tile (tile_exp of the tile's
+//     max |x|): 0 while max |x| lies in [2^-6, 2^15), else max |x| 2^e lands
+//     in [2^14, 2^15); covered for tile maxima in [2^-46, 2^55]. S comes out
+//     of the MFMA scaled by both tiles' factors, which the bias and the scale
+//     applied to it absorb; an accumulator is rescaled when a new tile brings
+//     another exponent.
+//   * dS in the dQ kernel: per query row, from the bound
+//     w |dP - Delta_i| <= 1.11 (||dO_i||_2 max_j ||v_j||_2 + |Delta_i|)
+//     (w = t^3 r^2 <= 1.11), so that the scaled dS stays below 2^14.
+//   * dS in the dK / dV kernel: per head (dK sums over rows), from the largest
+//     row bound 4 cinv_i w |dP - Delta_i| = p g |dP - Delta_i| with p g <= 4
+//     (p <= 1 when L is the forward's row sum).
+// So the gradients are exactly equivariant under power-of-two scalings of q,
+// k, v and dO, and dO's scale (a training step's is ~1e-5 .. 1e-7 per element)
+// does not move dS into fp16's subnormal range.
 // The reference writes g = 2 / ((|s|+1)^2 (sigma + eps)) (backward.py:145);
 // these kernels use sigma in place of sigma + eps, a relative change of
 // eps / (sigma + eps) in dS: <= 2e-6 wherever s >= 0, and otherwise on scores
@@ -297,58 +310,92 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_k(AttnArgs a) {
 }
 
 // ============================================================================
-// Backward prep (row-parallel, 8 elements per thread): k16 = K rounded to fp16
-// (clamped to +-65504), [B*H][T][D], and dmax = max_d |dO| per row, [B*H*T].
-// The LPR lanes of a row are consecutive lanes of one wave (LPR divides 64),
-// and a row's lanes all pass or all fail the range check together.
+// Backward prep, one block per 64-row tile of one (b, h):
+//   k16   the fp16 copy of K scaled by 2^kexp, kexp = tile_exp(max |k| of the
+//         tile) (exact: a power of two), [B*H][T][D];
+//   kexp  that exponent per tile, [B*H][nt] (nt = ceil(T / 64));
+//   vnrm  the largest row norm ||v_j||_2 of the tile's V rows, [B*H][nt];
+//   bmax  cleared for the head by its tile-0 block (the dQ kernel raises it
+//         with atomicMax to the head's bound on |dS|).
+// A row's LPR = D / 8 lanes are consecutive lanes of one wave; the block
+// covers its 64 rows in NP passes of 256 / LPR rows.
 // ============================================================================
 template <typename T, int D>
 __global__ __launch_bounds__(256) void attn_bwd_prep_k(AttnArgs a, f16* __restrict__ k16,
-                                                       float* __restrict__ dmax) {
+                                                       int* __restrict__ kexp, float* __restrict__ vnrm,
+                                                       unsigned* __restrict__ bmax) {
   constexpr int LPR = D / 8;
-  const int sub = threadIdx.x % LPR;
-  const int64_t row = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / LPR;
-  const int64_t nrows = (int64_t)a.B * a.H * a.T;
-  if (row >= nrows) return;
-  const int i = (int)(row % a.T);
-  const int64_t bh = row / a.T;
-  const int b = (int)(bh / a.H), h = (int)(bh % a.H);
-  const int d = 8 * sub;
-  const i16x8 kv = *reinterpret_cast<const i16x8*>((const T*)a.k + b * a.sk[0] + h * a.sk[1] + (int64_t)i * a.sk[2] + d);
-  const i16x8 gv = *reinterpret_cast<const i16x8*>((const T*)a.dout + b * a.sdo[0] + h * a.sdo[1] + (int64_t)i * a.sdo[2] + d);
-  *reinterpret_cast<i16x8*>(k16 + row * D + d) = to_f16x8<T>(kv);
-  const VecT<T, 8> g8 = __builtin_bit_cast(VecT<T, 8>, gv);
-  float m = 0.f;
+  constexpr int RPP = 256 / LPR;
+  constexpr int NP = 64 / RPP;
+  __shared__ float red[2][4];
+  const int nt = (a.T + 63) / 64;
+  const int bh = (int)(blockIdx.x / (unsigned)nt), t = (int)blockIdx.x - bh * nt;
+  const int b = bh / a.H, h = bh - b * a.H;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int sub = tid % LPR, d = 8 * sub;
+  const T* kp = (const T*)a.k + b * a.sk[0] + h * a.sk[1];
+  const T* vp = (const T*)a.v + b * a.sv[0] + h * a.sv[1];
+  i16x8 kv[NP];
+  float km = 0.f, vm = 0.f;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf((float)g8.v[e]));
+  for (int u = 0; u < NP; ++u) {
+    const int row = 64 * t + RPP * u + tid / LPR;
+    kv[u] = i16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    float vs = 0.f;
+    if (row < a.T) {
+      kv[u] = *reinterpret_cast<const i16x8*>(kp + (int64_t)row * a.sk[2] + d);
+      const VecT<T, 8> v8 = *reinterpret_cast<const VecT<T, 8>*>(vp + (int64_t)row * a.sv[2] + d);
+      km = fmaxf(km, absmax8<T>(kv[u]));
 #pragma unroll
-  for (int o = LPR / 2; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-  if (sub == 0) dmax[row] = m;
+      for (int e = 0; e < 8; ++e) vs = fmaf((float)v8.v[e], (float)v8.v[e], vs);
+    }
+#pragma unroll
+    for (int o = LPR / 2; o > 0; o >>= 1) vs += __shfl_xor(vs, o, 64);
+    vm = fmaxf(vm, sqrtf(vs));
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    km = fmaxf(km, __shfl_xor(km, o, 64));
+    vm = fmaxf(vm, __shfl_xor(vm, o, 64));
+  }
+  if (lane == 0) {
+    red[0][w] = km;
+    red[1][w] = vm;
+  }
+  __syncthreads();
+  km = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+  vm = fmaxf(fmaxf(red[1][0], red[1][1]), fmaxf(red[1][2], red[1][3]));
+  const int e = tile_exp(km);
+  const float f = ldexpf(1.f, e);
+  f16* kq = k16 + (int64_t)bh * a.T * D;
+#pragma unroll
+  for (int u = 0; u < NP; ++u) {
+    const int row = 64 * t + RPP * u + tid / LPR;
+    if (row < a.T) *reinterpret_cast<i16x8*>(kq + (int64_t)row * D + d) = to_f16x8s<T>(kv[u], f);
+  }
+  if (tid == 0) {
+    kexp[blockIdx.x] = e;
+    vnrm[blockIdx.x] = vm;
+    if (t == 0) bmax[bh] = 0u;
+  }
 }
 
-// The per-head dS scale: dscale[bh] = (2^k, 2^-k) with max |dO| 2^k in [4, 8)
-// over the head's rows; k = 0 when dO is all zero or not finite. One block per
-// (b, h); a fixed-order reduction.
-__global__ __launch_bounds__(256) void attn_bwd_dscale_k(const float* __restrict__ dmax, int T,
-                                                         float2* __restrict__ dscale) {
-  __shared__ float red[4];
-  const float* p = dmax + (int64_t)blockIdx.x * T;
-  float m = 0.f;
-  for (int t = threadIdx.x; t < T; t += 256) m = fmaxf(m, p[t]);
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    int k = 0;
-    if (m > 0.f && m <= 3.0e38f) {
-      int e;
-      (void)frexpf(m, &e);  // m = f 2^e, f in [0.5, 1)
-      k = std::min(64, std::max(-64, 3 - e));
-    }
-    dscale[blockIdx.x] = make_float2(ldexpf(1.f, k), ldexpf(1.f, -k));
-  }
+// Scale of the dK / dV kernel's dS: 2^kh with kh = ds_exp(the head's bound on
+// |dS|, raised by the dQ kernel). The per-row stats (4 cinv, -4 cinv Delta)
+// are multiplied by 2^kh in place (exact), so dS = w (stats.x dP + stats.y)
+// comes out scaled; one thread per row.
+__device__ __forceinline__ int head_dsexp(const unsigned* bmax, int bh) {
+  return ds_exp(__uint_as_float(bmax[bh]));
+}
+
+__global__ __launch_bounds__(256) void attn_bwd_stscale_k(float2* __restrict__ stats,
+                                                          const unsigned* __restrict__ bmax,
+                                                          int T, int64_t rows) {
+  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows) return;
+  const float f = ldexpf(1.f, head_dsexp(bmax, (int)(r / T)));
+  const float2 s = stats[r];
+  stats[r] = make_float2(s.x * f, s.y * f);
 }
 
 // ============================================================================
@@ -357,13 +404,16 @@ __global__ __launch_bounds__(256) void attn_bwd_dscale_k(const float* __restrict
 //   dP^T = V dO^T             A = V   (LDS rows)         B = dO^T  (VGPRs)
 //   dQ^T += K16^T dS^T        A = K16^T (LDS transposed) B = dS^T  (from S^T, dP^T)
 // Each block also forms, for its own query rows, Delta_i = <dO_i, O_i> and
-// stats_i = (4 cinv_i, -4 cinv_i Delta_i), and writes stats and the fp16 copy
-// of Q (clamped to +-65504) for the dK / dV kernel, which runs after it.
+// stats_i = (4 cinv_i, -4 cinv_i Delta_i), and writes stats, the fp16 copy of
+// Q (per-tile exponents in qexp) and the rows' dS bound (atomicMax into bmax)
+// for the dK / dV kernel, which runs after it.
 // ============================================================================
 template <typename T, int D, int MODE>
 __global__ __launch_bounds__(256, 2) void attn_bwd_dq_k(AttnArgs a, float2* __restrict__ stats,
                                                         f16* __restrict__ q16, const f16* __restrict__ k16,
-                                                        const float2* __restrict__ dscale) {
+                                                        const int* __restrict__ kexp, int* __restrict__ qexp,
+                                                        const float* __restrict__ vnrm,
+                                                        unsigned* __restrict__ bmax) {
   typedef Mfma<T> M;
   constexpr int KK = D / 32;
   constexpr int DS = D / 16;
@@ -392,41 +442,71 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_k(AttnArgs a, float2* __re
   const uint32_t kbytes = row_bytes(T_, D, D), vbytes = row_bytes(T_, sv2, D);
   const float slope = a.slopes[h];
   const float scale = a.scale;
+  const int nt = (T_ + 63) / 64;  // 64-row tiles of the head
+  const int* kexp_h = kexp + (int64_t)bh * nt;
+  const float* Lp = a.L + b * a.sl[0] + h * a.sl[1];
+  __shared__ float xq[kNW];  // max |q| per wave, for the Q16 tile exponents
 
+  // Range of the fp16 dS (dQ part): row q's dS enters dQ^T += K16^T dS^T as
+  // 2^k_q w (dP - Delta_q), w = t^3 r^2 <= 1.11, with k_q = ds_exp of a bound
+  // on it: |dP - Delta_q| <= ||dO_q||_2 max_j ||v_j||_2 + |Delta_q|. The row
+  // scale is undone per lane in the epilogue (dQ's columns are its queries),
+  // with the factor 4 cinv_q = 1 / (4 (L_q + eps)) the dS of the reference
+  // carries: dS = 4 cinv_q w (dP - Delta_q).
   i16x8 qf[2][KK], dof[2][KK];
-  const float2 dsc = dscale[bh];  // (2^k, 2^-k) of this head's dS
-  float c4[2], nc4d[2];  // 2^k 4 cinv_q and -2^k 4 cinv_q Delta_q for q = qw + 16 qs + li
+  float c4[2], nc4d[2];  // 2^k_q and -2^k_q Delta_q for q = qw + 16 qs + li
+  float qmax = 0.f;
   {
     const __amdgpu_buffer_rsrc_t rq = rsrc(qp, row_bytes(T_, sq2, D));
     const __amdgpu_buffer_rsrc_t rd = rsrc(dop, row_bytes(T_, sdo2, D));
     const __amdgpu_buffer_rsrc_t ro = rsrc(op, row_bytes(T_, so2, D));
-    const float* Lp = a.L + b * a.sl[0] + h * a.sl[1];
+    float mv = 0.f;  // max_j ||v_j||_2 of the head
+    for (int i = lane; i < nt; i += 64) mv = fmaxf(mv, vnrm[(int64_t)bh * nt + i]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mv = fmaxf(mv, __shfl_xor(mv, o, 64));
+    float bk = 0.f;  // the dK / dV kernel's bound on |dS| over this wave's rows
 #pragma unroll
     for (int qs = 0; qs < 2; ++qs) {
       const int qrow = qw + 16 * qs + li;
-      // Delta: lane (g, li) sums 32 of the row's D products, then across g
-      float dsum = 0.f;
+      // Delta and ||dO||^2: lane (g, li) sums 32 of the row's D products, then across g
+      float dsum = 0.f, dsq = 0.f;
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk) {
-        qf[qs][kk] = to_f16x8<T>(load16(rq, ((uint32_t)qrow * sq2 + 32 * kk + 8 * g) * 2));
+        qf[qs][kk] = load16(rq, ((uint32_t)qrow * sq2 + 32 * kk + 8 * g) * 2);
+        qmax = fmaxf(qmax, absmax8<T>(qf[qs][kk]));
         dof[qs][kk] = load16(rd, ((uint32_t)qrow * sdo2 + 32 * kk + 8 * g) * 2);
         const i16x8 ov = load16(ro, ((uint32_t)qrow * so2 + 32 * kk + 8 * g) * 2);
         const VecT<T, 8> o8 = __builtin_bit_cast(VecT<T, 8>, ov), g8 = __builtin_bit_cast(VecT<T, 8>, dof[qs][kk]);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) dsum = fmaf((float)g8.v[e], (float)o8.v[e], dsum);
+        for (int e = 0; e < 8; ++e) {
+          dsum = fmaf((float)g8.v[e], (float)o8.v[e], dsum);
+          dsq = fmaf((float)g8.v[e], (float)g8.v[e], dsq);
+        }
       }
       dsum += __shfl_xor(dsum, 16, 64);
       dsum += __shfl_xor(dsum, 32, 64);
+      dsq += __shfl_xor(dsq, 16, 64);
+      dsq += __shfl_xor(dsq, 32, 64);
       const bool ok = qrow < T_;
-      const float l = ok ? Lp[(int64_t)qrow * a.sl[2]] : 0.f;
-      c4[qs] = ok ? 4.f / (16.f * (l + a.eps)) * dsc.x : 0.f;  // dS scaled by 2^k
+      const float dpb = fmaf(sqrtf(dsq), mv, fabsf(dsum));  // bound on |dP - Delta| of the row
+      c4[qs] = ok ? ldexpf(1.f, ds_exp(1.125f * dpb)) : 0.f;
       nc4d[qs] = -c4[qs] * dsum;
       if (ok) {
-        const int64_t r = (int64_t)bh * T_ + qrow;
-        if (g == 0) stats[r] = make_float2(c4[qs], nc4d[qs]);
-#pragma unroll
-        for (int kk = 0; kk < KK; ++kk) *reinterpret_cast<i16x8*>(q16 + r * D + 32 * kk + 8 * g) = qf[qs][kk];
+        const float c4u = 1.f / (4.f * (Lp[(int64_t)qrow * a.sl[2]] + a.eps));
+        if (g == 0) stats[(int64_t)bh * T_ + qrow] = make_float2(c4u, -c4u * dsum);
+        // dK / dV kernel: |dS| = 4 cinv w |dP - Delta| = p g |dP - Delta| with
+        // p g <= 4 (p <= 1 when L is the forward's row sum)
+        bk = fmaxf(bk, fminf(4.1f, 1.125f * c4u) * dpb);
       }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      bk = fmaxf(bk, __shfl_xor(bk, o, 64));
+      qmax = fmaxf(qmax, __shfl_xor(qmax, o, 64));
+    }
+    if (lane == 0) {
+      atomicMax(bmax + bh, __float_as_uint(bk));  // non-negative floats order as their bits
+      xq[w] = qmax;
     }
   }
   f32x4 cb;
@@ -435,6 +515,11 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_k(AttnArgs a, float2* __re
   // bias in use and key validity of the current tile, as in the forward
   f32x4 cbx = cb;
   float sgn = 1.f;
+  // S^T comes out of the MFMA scaled by 2^(ek + eq) (the fp16 copies' tile
+  // exponents): the bias in cbx carries that factor and sc = scale 2^-(ek + eq)
+  // removes it; dqacc holds 2^ek times the sum (ek: the K16 tile in use)
+  int ek = 0;
+  float sc = scale;
   uint64_t vm = ~0ull;
   int kcur = 0;
   const uint8_t* kmb = kKM ? a.km + (int64_t)b * a.skm : nullptr;
@@ -479,7 +564,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_k(AttnArgs a, float2* __re
       float d[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        float s = fmaf(s_[qs][j], scale, tterm);
+        float s = fmaf(s_[qs][j], sc, tterm);
         if constexpr (MASKED && !kCausal) {
           const float sd = sgn * (float)((kh + 4 * g + j) - (qw + 16 * qs + li));
           if (sd > 0.f) s = fmaf(-2.f * slope, sd, s);
@@ -565,6 +650,24 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_k(AttnArgs a, float2* __re
   dv.issue(sv[0], vp, vbytes, 0, sv2, w);
   dma_wait();
   __syncthreads();
+  {
+    // Q16 = Q 2^eq with the exponent of this wave's 64-row tile (waves w and
+    // w ^ 1 hold its rows); the dK / dV kernel reads Q16 and qexp per tile
+    const int eq = tile_exp(fmaxf(xq[w], xq[w ^ 1]));
+    const float fq = ldexpf(1.f, eq);
+#pragma unroll
+    for (int qs = 0; qs < 2; ++qs) {
+      const int qrow = qw + 16 * qs + li;
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) {
+        qf[qs][kk] = to_f16x8s<T>(qf[qs][kk], fq);
+        if (qrow < T_) *reinterpret_cast<i16x8*>(q16 + ((int64_t)bh * T_ + qrow) * D + 32 * kk + 8 * g) = qf[qs][kk];
+      }
+    }
+    if ((w & 1) == 0 && lane == 0 && qw < T_) qexp[(int64_t)bh * nt + (qw >> 6)] = eq;
+    cbx *= fq;
+    sc = ldexpf(scale, -eq);
+  }
   // unrolled by two: static buffers (see the forward)
   auto step = [&](int kt, auto buf_tag) __attribute__((always_inline)) {
     constexpr int buf = decltype(buf_tag)::value;
@@ -574,6 +677,19 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_k(AttnArgs a, float2* __re
     }
     const int k0 = kt * kBN;
     kcur = k0;
+    const int ekt = kexp_h[kt];
+    if (ekt != ek) {
+      // a K16 tile with another exponent: rescale the bias, sc and the
+      // accumulated dQ to it (powers of two: exact)
+      const float f = ldexpf(1.f, ekt - ek);
+      cbx *= f;
+      sc = ldexpf(sc, ek - ekt);
+#pragma unroll
+      for (int ds = 0; ds < DS; ++ds)
+#pragma unroll
+        for (int qs = 0; qs < 2; ++qs) dqacc[ds][qs] *= f;
+      ek = ekt;
+    }
     if constexpr (kKM) {
       vm = __builtin_amdgcn_ballot_w64(kmn != 0u);
       if (kt + 1 < n_kt) kmn = kmbyte(kt + 1);
@@ -595,10 +711,12 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_k(AttnArgs a, float2* __re
     const int qrow = qw + 16 * qs + li;
     if (qrow < T_) {
       T* row = dqp + (int64_t)qrow * a.sdq[2];
+      // scale 4 cinv_q, with the row's dS exponent and the K16 tile exponent undone
+      const float c4u = 1.f / (4.f * (Lp[(int64_t)qrow * a.sl[2]] + a.eps));
+      const float osc = ldexpf(scale * c4u, -ek) / c4[qs];
 #pragma unroll
       for (int ds = 0; ds < DS; ++ds) {
         const f32x4 o = dqacc[ds][qs];
-        const float osc = scale * dsc.y;  // and dS's 2^k undone (exact)
         *reinterpret_cast<u32x2*>(row + 16 * ds + 4 * g) =
             u32x2{M::pack2(o[0] * osc, o[1] * osc), M::pack2(o[2] * osc, o[3] * osc)};
       }
@@ -635,7 +753,8 @@ struct DkvSmem {
 template <typename T, int D, int MODE>
 __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float2* __restrict__ stats,
                                                          const f16* __restrict__ q16,
-                                                         const float2* __restrict__ dscale) {
+                                                         const int* __restrict__ qexp,
+                                                         const unsigned* __restrict__ bmax) {
   typedef Mfma<T> M;
   constexpr int KK = D / 32;
   constexpr int DS = D / 16;
@@ -665,24 +784,43 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
   const uint32_t stbytes = (uint32_t)T_ * 8u;
   const float slope = a.slopes[h];
   const float scale = a.scale;
-  // the stats carry dS's 2^k (stats.x = 2^k 4 cinv); P takes 4 cinv / 16 = cinv / 4
-  const float2 dsc = dscale[bh];
-  const float p4 = 0.25f * dsc.y;
+  // the stats carry dS's 2^kh (stats.x = 2^kh 4 cinv); P takes 4 cinv / 16 = cinv / 4
+  const int kh = head_dsexp(bmax, bh);
+  const float p4 = ldexpf(0.25f, -kh);
+  const int nt = (T_ + 63) / 64;
+  const int* qexp_h = qexp + (int64_t)bh * nt;
 
   // B operands: K16^T (P role) or V^T (D role) fragments; lane (g, li) holds row
   // kw + 16 ks + li, columns 32 kk + 8 g .. +7
+  // (P role: scaled by 2^ekw, the exponent tile_exp gives the wave's 32 keys)
   i16x8 bfr[2][KK];
+  int ekw = 0;
   {
     const __amdgpu_buffer_rsrc_t rk = rsrc(kp, row_bytes(T_, sk2, D));
     const __amdgpu_buffer_rsrc_t rv = rsrc(vp, row_bytes(T_, sv2, D));
+    float km = 0.f;
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       const uint32_t key = (uint32_t)(kw + 16 * ks + li);
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk) {
-        if (prole) bfr[ks][kk] = to_f16x8<T>(load16(rk, (key * sk2 + 32 * kk + 8 * g) * 2));
-        else bfr[ks][kk] = load16(rv, (key * sv2 + 32 * kk + 8 * g) * 2);
+        if (prole) {
+          bfr[ks][kk] = load16(rk, (key * sk2 + 32 * kk + 8 * g) * 2);
+          km = fmaxf(km, absmax8<T>(bfr[ks][kk]));
+        } else {
+          bfr[ks][kk] = load16(rv, (key * sv2 + 32 * kk + 8 * g) * 2);
+        }
       }
+    }
+    if (prole) {
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) km = fmaxf(km, __shfl_xor(km, o, 64));
+      ekw = tile_exp(km);
+      const float fk = ldexpf(1.f, ekw);
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) bfr[ks][kk] = to_f16x8s<T>(bfr[ks][kk], fk);
     }
   }
   // S layout: lane (g, li) element j holds q = qh + 4 g + j, key = kw + 16 ks + li
@@ -690,8 +828,13 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
 #pragma unroll
   for (int j = 0; j < 4; ++j) cb[j] = (slope / scale) * (float)(li - 4 * g - j);
   // bias in use (negated for query chunks wholly below this wave's keys in
-  // non-causal mode)
-  f32x4 cbx = cb;
+  // non-causal mode). S comes out of the MFMA scaled by 2^(eq + ekw) (eq: the
+  // Q16 tile's exponent): cbx carries that factor and sc = scale 2^-(eq + ekw)
+  // removes it; the dK accumulators hold 2^eq times the sum.
+  int eq = 0;
+  float sfac = ldexpf(1.f, ekw);  // 2^(eq + ekw)
+  f32x4 cbx = cb * sfac;
+  float sc = ldexpf(scale, -ekw);
   float slx = slope;
   // Padding mask: a dropped key's P and dS column is zero, so its dK / dV
   // rows are zero and the other keys' rows do not depend on it. The kernel
@@ -760,7 +903,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
       f32x4 wv;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        float s = fmaf(s_[ks][j], scale, tterm);
+        float s = fmaf(s_[ks][j], sc, tterm);
         if constexpr (DIAG && !kCausal) {
           const int dkq = (kw + 16 * ks + li) - (qh + 4 * g + j);
           if (dkq > 0) s = fmaf(-2.f * slope, (float)dkq, s);
@@ -826,9 +969,26 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
     const bool need = needc(c), full = need && fullc(c);
     f32x4 (*xw)[64] = sm.x[c & 1][grp];
     uint32_t pa[2][2], pb[2][2];
+    if ((c & 1) == 0) {
+      // a new Q16 tile: its exponent (both roles track it)
+      const int eqt = qexp_h[(qbase >> 6) + it];
+      if (eqt != eq) {
+        const float f = ldexpf(1.f, eqt - eq);
+        sfac *= f;
+        sc = ldexpf(sc, eq - eqt);
+        if constexpr (kCausal) cbx *= f;
+        if (!prole) {
+#pragma unroll
+          for (int ds = 0; ds < DS; ++ds)
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) acc[ds][ks] *= f;
+        }
+        eq = eqt;
+      }
+    }
     if constexpr (!kCausal) {
       const bool above = kw > qc + 31;
-      cbx = above ? -cb : cb;
+      cbx = (above ? -cb : cb) * sfac;
       slx = above ? -slope : slope;
     }
     if (prole && need) {
@@ -895,7 +1055,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
 
   T* __restrict__ outp = prole ? (T*)a.dv + b * a.sdv[0] + h * a.sdv[1] : (T*)a.dk + b * a.sdk[0] + h * a.sdk[1];
   const int64_t ostr = prole ? a.sdv[2] : a.sdk[2];
-  const float osc = prole ? 1.f : scale * dsc.y;  // dK: dS's 2^k undone (exact)
+  const float osc = prole ? 1.f : ldexpf(scale, -(kh + eq));  // dK: dS's 2^kh and Q16's 2^eq undone (exact)
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
     const int key = kw + 16 * ks + li;
@@ -917,11 +1077,46 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
 // ============================================================================
 bool attn_mfma_supported(int D) { return D == 64 || D == 128; }
 
-size_t attn_mfma_workspace(int64_t B, int64_t H, int64_t T, int64_t D) {
-  const size_t rows = (size_t)(B * H * T);
+// Backward workspace: per-row stats (float2), the fp16 copies of Q and K
+// ([B*H][T][D] each), per-tile exponents of K16 and Q16 and V row-norm maxima
+// ([B*H][nt] each, nt = ceil(T / 64)), and the per-head dS bound (B*H words);
+// each part 256-byte aligned.
+struct BwdWs {
+  float2* stats;
+  f16* q16;
+  f16* k16;
+  int* kexp;
+  int* qexp;
+  float* vnrm;
+  unsigned* bmax;
+  size_t bytes;
+};
+static BwdWs bwd_ws(void* base, int64_t B, int64_t H, int64_t T, int64_t D) {
   auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
-  return al(rows * sizeof(float2)) + 2 * al(rows * (size_t)D * sizeof(f16)) + al(rows * sizeof(float)) +
-         al((size_t)(B * H) * sizeof(float2));
+  const size_t rows = (size_t)(B * H * T), tiles = (size_t)(B * H) * (size_t)((T + 63) / 64);
+  char* p = reinterpret_cast<char*>(base);
+  BwdWs w;
+  size_t o = 0;
+  w.stats = reinterpret_cast<float2*>(p + o);
+  o += al(rows * sizeof(float2));
+  w.q16 = reinterpret_cast<f16*>(p + o);
+  o += al(rows * (size_t)D * sizeof(f16));
+  w.k16 = reinterpret_cast<f16*>(p + o);
+  o += al(rows * (size_t)D * sizeof(f16));
+  w.kexp = reinterpret_cast<int*>(p + o);
+  o += al(tiles * sizeof(int));
+  w.qexp = reinterpret_cast<int*>(p + o);
+  o += al(tiles * sizeof(int));
+  w.vnrm = reinterpret_cast<float*>(p + o);
+  o += al(tiles * sizeof(float));
+  w.bmax = reinterpret_cast<unsigned*>(p + o);
+  o += al((size_t)(B * H) * sizeof(unsigned));
+  w.bytes = o;
+  return w;
+}
+
+size_t attn_mfma_workspace(int64_t B, int64_t H, int64_t T, int64_t D) {
+  return bwd_ws(nullptr, B, H, T, D).bytes;
 }
 
 namespace {
@@ -945,25 +1140,24 @@ template <typename T, int D, int MODE> int launch_fwd(const AttnArgs& a, hipStre
 
 template <typename T, int D, int MODE>
 int launch_bwd(const AttnArgs& a, void* ws, hipStream_t st) {
+  const BwdWs w = bwd_ws(ws, a.B, a.H, a.T, a.D);
   const int64_t rows = (int64_t)a.B * a.H * a.T;
-  auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
-  float2* stats = reinterpret_cast<float2*>(ws);
-  f16* q16 = reinterpret_cast<f16*>(reinterpret_cast<char*>(ws) + al(rows * sizeof(float2)));
-  f16* k16 = reinterpret_cast<f16*>(reinterpret_cast<char*>(q16) + al(rows * D * sizeof(f16)));
-  float* dmax = reinterpret_cast<float*>(reinterpret_cast<char*>(k16) + al(rows * D * sizeof(f16)));
-  float2* dscale = reinterpret_cast<float2*>(reinterpret_cast<char*>(dmax) + al(rows * sizeof(float)));
-  constexpr int rpb = 256 / (D / 8);
-  hipLaunchKernelGGL((attn_bwd_prep_k<T, D>), dim3((unsigned)((rows + rpb - 1) / rpb)), dim3(256), 0, st, a,
-                     k16, dmax);
+  const int64_t tiles = (int64_t)a.B * a.H * ((a.T + 63) / 64);
+  // prep: K16 + per-tile exponents and V norms, clears the dS bounds
+  hipLaunchKernelGGL((attn_bwd_prep_k<T, D>), dim3((unsigned)tiles), dim3(256), 0, st, a, w.k16, w.kexp,
+                     w.vnrm, w.bmax);
   if (int rc = check_launch("kat_attn_bwd (prep)")) return rc;
-  hipLaunchKernelGGL(attn_bwd_dscale_k, dim3((unsigned)(a.B * a.H)), dim3(256), 0, st, dmax, a.T, dscale);
-  if (int rc = check_launch("kat_attn_bwd (dscale)")) return rc;
-  // dq also writes stats and q16, which the dK / dV kernel reads
+  // dq also writes stats, q16 and qexp and raises the dS bounds, which the
+  // dK / dV kernel reads
   const int64_t nt = (int64_t)((a.T + kBM - 1) / kBM) * a.B * a.H;
-  hipLaunchKernelGGL((attn_bwd_dq_k<T, D, MODE>), dim3((unsigned)nt), dim3(256), 0, st, a, stats, q16, k16,
-                     dscale);
+  hipLaunchKernelGGL((attn_bwd_dq_k<T, D, MODE>), dim3((unsigned)nt), dim3(256), 0, st, a, w.stats, w.q16,
+                     w.k16, w.kexp, w.qexp, w.vnrm, w.bmax);
   if (int rc = check_launch("kat_attn_bwd (dq, mfma)")) return rc;
-  hipLaunchKernelGGL((attn_bwd_dkv_k<T, D, MODE>), dim3((unsigned)nt), dim3(512), 0, st, a, stats, q16, dscale);
+  hipLaunchKernelGGL(attn_bwd_stscale_k, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, st, w.stats,
+                     w.bmax, a.T, rows);
+  if (int rc = check_launch("kat_attn_bwd (stats scale)")) return rc;
+  hipLaunchKernelGGL((attn_bwd_dkv_k<T, D, MODE>), dim3((unsigned)nt), dim3(512), 0, st, a, w.stats, w.q16,
+                     w.qexp, w.bmax);
   return check_launch("kat_attn_bwd (dkv, mfma)");
 }
 
@@ -986,7 +1180,7 @@ template <typename T> int attn_fwd_mfma(const AttnArgs& a, hipStream_t st) {
 }
 
 template <typename T> int attn_bwd_mfma(const AttnArgs& a, void* ws, hipStream_t st) {
-  if ((int64_t)((a.T + kBM - 1) / kBM) * a.B * a.H > 0x7fffffffLL || !offsets_ok(a, true)) return KAT_EUNSUPPORTED;
+  if ((int64_t)((a.T + 63) / 64) * a.B * a.H > 0x7fffffffLL || !offsets_ok(a, true)) return KAT_EUNSUPPORTED;
   if (a.D == 128) KAT_MODE_SWITCH(a, return (launch_bwd<T, 128, MODE>(a, ws, st)));
   if (a.D == 64) KAT_MODE_SWITCH(a, return (launch_bwd<T, 64, MODE>(a, ws, st)));
   return KAT_EUNSUPPORTED;

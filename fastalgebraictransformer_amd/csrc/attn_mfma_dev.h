@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
+
 #include "kat_common.h"
 
 namespace kat {
@@ -67,6 +69,54 @@ template <> __device__ __forceinline__ i16x8 to_f16x8<bf16>(const i16x8& v) {
     o[e] = pack2_f16(fminf(fmaxf(lo, -65504.f), 65504.f), fminf(fmaxf(hi, -65504.f), 65504.f));
   }
   return __builtin_bit_cast(i16x8, o);
+}
+
+// fp16 copy of 8 elements of T multiplied by f (a power of two chosen by
+// tile_exp, so the product is exact); clamped to +-65504 as a guard.
+template <typename T> __device__ __forceinline__ i16x8 to_f16x8s(const i16x8& v, float f) {
+  const VecT<T, 8> x = __builtin_bit_cast(VecT<T, 8>, v);
+  u32x4 o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float lo = (float)x.v[2 * e] * f, hi = (float)x.v[2 * e + 1] * f;
+    o[e] = pack2_f16(fminf(fmaxf(lo, -65504.f), 65504.f), fminf(fmaxf(hi, -65504.f), 65504.f));
+  }
+  return __builtin_bit_cast(i16x8, o);
+}
+
+// largest |element| of 8 elements of T
+template <typename T> __device__ __forceinline__ float absmax8(const i16x8& v) {
+  const VecT<T, 8> x = __builtin_bit_cast(VecT<T, 8>, v);
+  float m = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf((float)x.v[e]));
+  return m;
+}
+
+// Power-of-two exponent for the fp16 copy of a 64-row tile whose largest
+// magnitude is m. bf16 -> fp16 is exact for magnitudes in [2^-14, 65504]; a
+// tile with m in [2^-6, 2^15) is copied unscaled (its elements below 2^-14
+// are then at least 2^-8 below m, where fp16's subnormal spacing 2^-24 is
+// far below bf16's own rounding of m), any other tile is scaled so that
+// m 2^e lies in [2^14, 2^15). e is clamped to [-40, 40], which covers tiles
+// with m in [2^-46, 2^55]; zero and non-finite m give 0.
+__device__ __forceinline__ int tile_exp(float m) {
+  if (m >= 0x1p-6f && m < 0x1p15f) return 0;
+  if (!(m > 0.f) || !(m <= 3.4e38f)) return 0;
+  int E;
+  (void)frexpf(m, &E);  // m = f 2^E, f in [0.5, 1)
+  return std::min(40, std::max(-40, 15 - E));
+}
+
+// Power-of-two exponent k for an fp16 operand whose magnitudes are bounded by
+// b: b 2^k lies in [2^13, 2^14), a quarter of fp16's range, so that values
+// reach fp16's subnormal range only 27 binades below the bound. Clamped to
+// [-100, 100]; zero or non-finite b gives 0.
+__device__ __forceinline__ int ds_exp(float b) {
+  if (!(b > 0.f) || !(b <= 3.4e38f)) return 0;
+  int E;
+  (void)frexpf(b, &E);
+  return std::min(100, std::max(-100, 14 - E));
 }
 
 __device__ __forceinline__ i16x8 pack_frag(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {

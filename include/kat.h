@@ -167,10 +167,14 @@ size_t kat_attn_bwd_workspace_size(int64_t B, int64_t H, int64_t T, int64_t D, i
  *   dv = P^T dO.
  * strides: 24 int64 = (b, h, t) strides of q, k, v, out, dout, dq, dk, dv.
  * Replaces the host wrapper + the dq and dkv launches at backward.py:273-341
- * (kernels backward.py:62-158 and 165-266). Deterministic (no atomics). On the
- * MFMA path dS enters its products in fp16, scaled per (b, h) by a power of two
- * taken from max |dout| of the head, so the gradients are exactly linear in the
- * scale of dout (2^-e dout gives 2^-e times the gradients). */
+ * (kernels backward.py:62-158 and 165-266). Deterministic. On the MFMA path
+ * dS, and the copies of Q and K its products take, enter the MFMA in fp16,
+ * each with a power-of-two scale chosen from the data (per 64-row tile for Q
+ * and K, from a bound on |dS| per row and per head for dS) and undone
+ * exactly: the gradients are exactly equivariant under power-of-two scalings
+ * of q, k, v and dout, and per-tile maxima of |q| and |k| in [2^-46, 2^55]
+ * are covered. The dS bounds assume (out, L) are the forward's outputs for
+ * (q, k, v), as the reference's derivation does. */
 int kat_attn_bwd(const void* q, const void* k, const void* v, const void* out,
                  const float* L, const void* dout, void* dq, void* dk, void* dv,
                  const float* slopes, void* workspace, size_t workspace_bytes, int64_t B,

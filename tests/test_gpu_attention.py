@@ -256,3 +256,80 @@ def test_mfma_backward_is_invariant_to_the_upstream_gradient_scale(gpu, D, maske
         rq, rk, rv = O.attention_bwd(q, k, v, o, L, do, slopes, scale, dtype=torch.float32)
         for name, gt, r in zip(("dq", "dk", "dv"), base, (rq, rk, rv)):
             assert_lowp(gt, r, torch.bfloat16, name)
+
+
+# ------------------------------------------------- input magnitude range ----
+# The MFMA backward rounds dS, and copies of Q and K, to fp16 (range 2^-14 ..
+# 65504). Each copy carries a power-of-two scale chosen from the data (per
+# 64-row tile for Q and K, per row and per head for dS), so inputs far outside
+# N(0, 1) must still meet the bar. Outputs scale with the inputs: each check
+# divides got and ref by the known factor of that output and applies the
+# unit-scale bar, 2e-2 + 1/2 ulp.
+
+def _scaled_check(q, k, v, do, slopes, scale, factors):
+    o, L, dq, dk, dv = _run(q, k, v, do, slopes.to(dev), scale)
+    for t in (o, L, dq, dk, dv):
+        assert bool(torch.isfinite(t).all())
+    ro, rL = O.attention_fwd(q, k, v, slopes, scale, dtype=torch.float32)
+    rq, rk, rv = O.attention_bwd(q, k, v, o, L, do, slopes, scale, dtype=torch.float32)
+    assert _rel_max(L, rL) <= 1e-2
+    for name, got, ref in (("o", o, ro), ("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
+        f = factors[name]
+        got = got.detach().to("cpu", torch.float64) / f
+        ref = ref.detach().to("cpu", torch.float64) / f
+        err = (got - ref).abs()
+        excess = float((err - (2e-2 + 0.5 * _ulp(ref, q.dtype))).max())
+        print(f"{name}: max err (unit scale) {float(err.max()):.3e}, relL2 "
+              f"{float((got - ref).norm() / ref.norm()):.3e}")
+        assert excess <= 0, (name, float(err.max()), excess)
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("case", ["v1e4", "do1e-6", "q1e5_k1e-5", "qk1e-4", "combined", "v1e3_do1e2"])
+def test_mfma_backward_input_range_bf16(gpu, D, case, monkeypatch):
+    _pin_mfma(monkeypatch, D)
+    B, H, T = 1, 2, 300
+    q, k, v, do = (t.float() for t in _inputs(41 + D, B, H, T, D, torch.float32))
+    fq, fk, fv, fd = {"v1e4": (1, 1, 1e4, 1), "do1e-6": (1, 1, 1, 1e-6),
+                      "q1e5_k1e-5": (1e5, 1e-5, 1, 1), "qk1e-4": (1e-4, 1e-4, 1, 1),
+                      "combined": (1e5, 1e-5, 1e4, 1e-6), "v1e3_do1e2": (1, 1, 1e3, 1e2)}[case]
+    q, k, v, do = ((t * f).to(torch.bfloat16) for t, f in ((q, fq), (k, fk), (v, fv), (do, fd)))
+    slopes = F.compute_alibi_slopes(H)
+    scale = 1.0 / math.sqrt(D)
+    # s = scale q.k changes only for qk1e-4 (where it shrinks to ~1e-9, the bias alone)
+    factors = {"o": fv, "dq": fv * fd * fk, "dk": fv * fd * fq, "dv": fd}
+    _scaled_check(q, k, v, do, slopes, scale, factors)
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_mfma_backward_input_range_fp16(gpu, D, monkeypatch):
+    _pin_mfma(monkeypatch, D)
+    B, H, T = 1, 2, 300
+    q, k, v, do = _inputs(43 + D, B, H, T, D, torch.float32)
+    fq, fk, fv, fd = 2.0 ** 6, 2.0 ** -6, 2.0 ** 8, 2.0 ** -12
+    q, k, v, do = ((t * f).to(torch.float16) for t, f in ((q, fq), (k, fk), (v, fv), (do, fd)))
+    slopes = F.compute_alibi_slopes(H)
+    scale = 1.0 / math.sqrt(D)
+    _scaled_check(q, k, v, do, slopes, scale,
+                  {"o": fv, "dq": fv * fd * fk, "dk": fv * fd * fq, "dv": fd})
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_mfma_attention_is_exactly_equivariant_to_power_of_two_scales(gpu, D, monkeypatch):
+    # inputs on a grid of 1/16 are exact in fp16 at every scale used below, so
+    # the fp16 copies hold the same significands whatever their exponent: then
+    # q 2^16, k 2^-16, v 2^13 and dO 2^-20 must give o 2^13, dq 2^-23, dk 2^9
+    # and dv 2^-20 times the unit-scale results, bit for bit -- every scale the
+    # kernels pick is a power of two that cancels exactly
+    _pin_mfma(monkeypatch, D)
+    B, H, T = 2, 3, 200
+    g = torch.Generator().manual_seed(53 + D)
+    base = [torch.round(torch.randn(B, H, T, D, generator=g) * 16) / 16 for _ in range(4)]
+    slopes = F.compute_alibi_slopes(H).to(dev)
+    scale = 1.0 / math.sqrt(D)
+    unit = _run(*(t.to(torch.bfloat16).to(dev) for t in base), slopes, scale)
+    sf = (2.0 ** 16, 2.0 ** -16, 2.0 ** 13, 2.0 ** -20)
+    scaled = _run(*((t * f).to(torch.bfloat16).to(dev) for t, f in zip(base, sf)), slopes, scale)
+    for name, u, s_, f in zip(("o", "L", "dq", "dk", "dv"), unit, scaled,
+                              (2.0 ** 13, 1.0, 2.0 ** -23, 2.0 ** 9, 2.0 ** -20)):
+        assert torch.equal(s_.float(), u.float() * f), name

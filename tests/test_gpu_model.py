@@ -143,5 +143,10 @@ def test_bf16_training_tracks_cpu_fp32(gpu):
         opt_g.step()
         lg.append(loss.item())
     assert lg[-1] < 0.7 * lg[0], lg
-    for a, b in zip(lc, lg):
-        assert abs(a - b) <= 0.05 * a, (lc, lg)
+    # The first steps track the fp32 run closely (measured < 0.3%), which a
+    # wrong or missing gradient term would break at once. Later steps of this
+    # memorise-one-batch run amplify bf16 rounding chaotically: over 8 seeds the
+    # final losses differed from the fp32 run by -14% .. +7%, with random signs,
+    # so they only have to stay within 20%.
+    for i, (a, b) in enumerate(zip(lc, lg)):
+        assert abs(a - b) <= (0.01 if i < 10 else 0.2) * a, (i, lc, lg)
