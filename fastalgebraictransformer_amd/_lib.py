@@ -54,6 +54,8 @@ _SIGNATURES = {
     "kat_attn_decode_workspace_size": ([_I64, _I64, _I64, _I64, _INT], _SZ),
     "kat_attn_decode": ([_P, _P, _P, _P, _P, _P, _P, _P, _SZ, _I64, _I64, _I64, _I64, _I64P, _F,
                          _F, _INT, _P], _INT),
+    "kat_attn_decode_noalloc": ([_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64P, _F, _F,
+                                 _INT, _P], _INT),
     "kat_probe_mfma_bf16": ([_P, _INT, _INT, ctypes.POINTER(ctypes.c_double), _P], _INT),
 }
 

@@ -17,6 +17,7 @@
 // kernel adds the chunks in a fixed order (deterministic) and normalises.
 
 #include <algorithm>
+#include <mutex>
 
 #include "kat_common.h"
 #include "kat_internal.h"
@@ -204,12 +205,14 @@ extern "C" size_t kat_attn_decode_workspace_size(int64_t B, int64_t H, int64_t T
   return (size_t)(B * H) * (size_t)splits * (size_t)(D + 1) * sizeof(float);
 }
 
-extern "C" int kat_attn_decode(const void* q, const void* k, const void* v, void* out, float* L,
-                               const float* slopes, const int32_t* lengths, void* workspace,
-                               size_t workspace_bytes, int64_t B, int64_t H, int64_t T, int64_t D,
-                               const int64_t* strides, float scale, float eps, int dtype,
-                               void* stream) {
-  const char* nm = "kat_attn_decode";
+// Argument checks and launch shared by kat_attn_decode and
+// kat_attn_decode_noalloc. get_part(need) returns the partials buffer for
+// `need` bytes, or nullptr after recording an error.
+template <typename GetPart>
+static int decode_impl(const char* nm, const void* q, const void* k, const void* v, void* out, float* L,
+                       const float* slopes, const int32_t* lengths, int64_t B, int64_t H, int64_t T,
+                       int64_t D, const int64_t* strides, float scale, float eps, int dtype, void* stream,
+                       GetPart get_part) {
   if (B < 0 || H < 0 || T < 0 || D < 0) return fail(KAT_EINVAL, "%s: negative size", nm);
   if (B * H > 0xffffLL * 0x7fffLL || T > 0x3fffffffLL)
     return fail(KAT_EUNSUPPORTED, "%s: B*H or T too large", nm);
@@ -246,9 +249,8 @@ extern "C" int kat_attn_decode(const void* q, const void* k, const void* v, void
   a.eps = eps;
   decode_split(B, H, std::max<int64_t>(T, 1), decode_rpp((int)D, dtype), a.splits, a.chunk);
   const size_t need = (size_t)(B * H) * (size_t)a.splits * (size_t)(D + 1) * sizeof(float);
-  if (!workspace || workspace_bytes < need)
-    return fail(KAT_EINVAL, "%s: workspace %zu bytes < required %zu", nm, workspace_bytes, need);
-  float* part = reinterpret_cast<float*>(workspace);
+  float* part = get_part(need);
+  if (!part) return KAT_EINVAL;  // get_part recorded the message
   const hipStream_t st = as_stream(stream);
   switch (dtype) {
     case KAT_F32: return decode_d<float>(a, part, st);
@@ -256,4 +258,74 @@ extern "C" int kat_attn_decode(const void* q, const void* k, const void* v, void
     case KAT_F16: return decode_d<f16>(a, part, st);
   }
   return fail(KAT_EUNSUPPORTED, "%s: unsupported dtype %d", nm, dtype);
+}
+
+extern "C" int kat_attn_decode(const void* q, const void* k, const void* v, void* out, float* L,
+                               const float* slopes, const int32_t* lengths, void* workspace,
+                               size_t workspace_bytes, int64_t B, int64_t H, int64_t T, int64_t D,
+                               const int64_t* strides, float scale, float eps, int dtype,
+                               void* stream) {
+  const char* nm = "kat_attn_decode";
+  return decode_impl(nm, q, k, v, out, L, slopes, lengths, B, H, T, D, strides, scale, eps, dtype,
+                     stream, [&](size_t need) -> float* {
+                       if (!workspace || workspace_bytes < need) {
+                         fail(KAT_EINVAL, "%s: workspace %zu bytes < required %zu", nm, workspace_bytes,
+                              need);
+                         return nullptr;
+                       }
+                       return reinterpret_cast<float*>(workspace);
+                     });
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free decode: the partials live in a fixed device array of the
+// library (one copy per GPU, held until the process ends) instead of a
+// caller's workspace. `scratch` names a host-side stand-in; its device
+// address on the current GPU comes from hipGetSymbolAddress, looked up once
+// per device on the first call and kept.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) float scratch[KAT_DECODE_SCRATCH_BYTES / sizeof(float)];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxDevices] = {};
+
+// device address of `scratch` on the current device, or nullptr (error recorded)
+float* device_scratch(const char* nm) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    fail(KAT_EHIP, "%s: no current HIP device", nm);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      fail(KAT_EHIP, "%s: hipGetSymbolAddress(scratch) on device %d: %s", nm, dev, hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = static_cast<float*>(p);
+  }
+  return g_scratch_ptr[dev];
+}
+}  // namespace
+
+extern "C" int kat_attn_decode_noalloc(const void* q, const void* k, const void* v, void* out, float* L,
+                                       const float* slopes, const int32_t* lengths, int64_t B, int64_t H,
+                                       int64_t T, int64_t D, const int64_t* strides, float scale,
+                                       float eps, int dtype, void* stream) {
+  const char* nm = "kat_attn_decode_noalloc";
+  return decode_impl(nm, q, k, v, out, L, slopes, lengths, B, H, T, D, strides, scale, eps, dtype,
+                     stream, [&](size_t need) -> float* {
+                       if (need > (size_t)KAT_DECODE_SCRATCH_BYTES) {
+                         fail(KAT_EUNSUPPORTED,
+                              "%s: the partials need %zu bytes, more than the %zu-byte scratch array "
+                              "(B*H*splits*(D+1) floats; use kat_attn_decode with a workspace)",
+                              nm, need, (size_t)KAT_DECODE_SCRATCH_BYTES);
+                         return nullptr;
+                       }
+                       return device_scratch(nm);
+                     });
 }

@@ -227,6 +227,25 @@ int kat_attn_decode(const void* q, const void* k, const void* v, void* out, floa
                     size_t workspace_bytes, int64_t B, int64_t H, int64_t T, int64_t D,
                     const int64_t* strides, float scale, float eps, int dtype, void* stream);
 
+/* Allocation-free variant of kat_attn_decode. No counterpart in the
+ * reference; it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments, semantics and results as kat_attn_decode (bit for bit), but
+ * the split-KV partials live in a fixed device array of the library,
+ * KAT_DECODE_SCRATCH_BYTES per GPU, held until the process ends, instead of
+ * a caller's workspace. Calls whose partials (B*H*splits*(D+1) floats, with
+ * splits as kat_attn_decode picks them; kat_attn_decode_workspace_size gives
+ * the byte count) exceed the array fail with KAT_EUNSUPPORTED. The call
+ * allocates nothing; the first call on a device looks up the array's device
+ * address (hipGetSymbolAddress) once. Every call on one GPU shares that
+ * GPU's array: calls that overlap in time on one GPU (different streams or
+ * host threads) race; calls ordered on one stream do not. */
+#define KAT_DECODE_SCRATCH_BYTES ((size_t)8 << 20)
+int kat_attn_decode_noalloc(const void* q, const void* k, const void* v, void* out, float* L,
+                            const float* slopes, const int32_t* lengths, int64_t B, int64_t H,
+                            int64_t T, int64_t D, const int64_t* strides, float scale, float eps,
+                            int dtype, void* stream);
+
 /* ----------------------------------------------------------------------
  * Measurement helper (no counterpart in the reference; used by bench.py to
  * report a measured MFMA rate beside the spec peak). `blocks` x 256 threads
