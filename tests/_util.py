@@ -54,3 +54,31 @@ def assert_rel(out, ref, rel, what="", floor_frac=1e-6):
 
 def max_abs(a, b):
     return float((a.detach().to("cpu", torch.float64) - b.detach().to("cpu", torch.float64)).abs().max())
+
+
+def lowp_ulp(ref, dtype):
+    """Spacing of ``dtype`` (bf16 or fp16) numbers at |ref|."""
+    if dtype == torch.float16:
+        a = ref.abs().to(torch.float64).clamp_min(2.0 ** -14)
+        return torch.pow(2.0, torch.floor(torch.log2(a)) - 10)
+    return bf16_ulp(ref)
+
+
+def check_lowp(got, ref, dtype, name, bar=2e-2, n_ulp=0.5, rel_l2=5e-3):
+    """Low-precision attention bar: elementwise |got - ref| <= bar +
+    n_ulp * ulp_dtype(ref) (the north-star 2e-2 max-abs plus the output's own
+    rounding to dtype), and, where the reference is not ~0 (rms > 1e-3), a
+    relative L2 error ||got - ref|| / ||ref|| <= rel_l2, which a systematic
+    error of a few tenths of a percent would break even where the elementwise
+    bar is loose. Returns (max error, relative L2 error)."""
+    got = got.detach().to("cpu", torch.float64)
+    ref = ref.detach().to("cpu", torch.float64)
+    err = (got - ref).abs()
+    worst = float((err - (bar + n_ulp * lowp_ulp(ref, dtype))).max())
+    rn = float(ref.norm())
+    rl2 = float((got - ref).norm()) / max(rn, 1e-300)
+    assert worst <= 0, (f"{name}: max err {float(err.max()):.3e} (max|ref| "
+                        f"{float(ref.abs().max()):.3e}) exceeds {bar} + {n_ulp} ulp by {worst:.3e}")
+    if rn > 1e-3 * ref.numel() ** 0.5:
+        assert rl2 <= rel_l2, f"{name}: relative L2 error {rl2:.3e} > {rel_l2}"
+    return float(err.max()), rl2

@@ -3,11 +3,11 @@ oracle. Tolerances (written next to each check):
   * fp32 (tiled fp32 kernels): <= 1e-5 of max|ref| on outputs and gradients;
     the reference bars (tests.py:210-211) are 1e-3 / 1e-2 max-abs;
   * bf16 / fp16 (MFMA kernels, fp32 accumulation): 2e-2 max-abs on o, dq,
-    dk, dv on top of the output's own quantisation:
-    elementwise |got - ref| <= 2e-2 + 1 ulp(ref) of the output dtype. The
-    outputs are stored in the input dtype (as the reference does), and for
-    |x| >= 4 half a bf16 ulp alone is >= 1.6e-2, so a bare 2e-2 bar cannot be
-    met by any bf16 result there. L (fp32) within 1e-2 relative.
+    dk, dv on top of the output's own rounding:
+    elementwise |got - ref| <= 2e-2 + 1/2 ulp(ref) of the output dtype (the
+    outputs are stored in the input dtype, as the reference does, and for
+    |x| >= 4 half a bf16 ulp alone is >= 1.6e-2), plus a relative L2 error
+    <= 5e-3 per tensor (check_lowp). L (fp32) within 1e-2 relative.
 """
 
 import math
@@ -19,7 +19,7 @@ import torch
 
 import fastalgebraictransformer_amd as F
 import oracle as O
-from _util import bf16_ulp, golden, max_abs
+from _util import check_lowp, golden, lowp_ulp, max_abs
 
 pytestmark = pytest.mark.gpu
 dev = "cuda"
@@ -49,21 +49,13 @@ def _rel_max(a, b):
 
 
 def _ulp(ref, dtype):
-    if dtype == torch.float16:
-        a = ref.abs().to(torch.float64).clamp_min(2.0 ** -14)
-        return torch.pow(2.0, torch.floor(torch.log2(a)) - 10)
-    return bf16_ulp(ref)
+    return lowp_ulp(ref, dtype)
 
 
 def assert_lowp(got, ref, dtype, name, bar=2e-2):
-    """|got - ref| <= bar + 1 ulp_dtype(ref), elementwise."""
-    got = got.detach().to("cpu", torch.float64)
-    ref = ref.detach().to("cpu", torch.float64)
-    err = (got - ref).abs()
-    excess = err - (bar + _ulp(ref, dtype))
-    worst = float(excess.max())
-    assert worst <= 0, (f"{name}: max err {float(err.max()):.3e} (max|ref| "
-                        f"{float(ref.abs().max()):.3e}) exceeds 2e-2 + 1 ulp by {worst:.3e}")
+    """check_lowp: |got - ref| <= bar + 1/2 ulp_dtype(ref) elementwise, and
+    relative L2 <= 5e-3."""
+    return check_lowp(got, ref, dtype, name, bar=bar)
 
 
 # ----------------------------------------------------------------- fp32 ----
@@ -109,22 +101,24 @@ def test_reference_shapes_fp32(gpu, B, H, T, D):
 
 # ------------------------------------------------------------ bf16 / fp16 ----
 
-def _check_lowp(o, L, dq, dk, dv, q, k, v, do, slopes, scale, sel=None):
+def _check_lowp(o, L, dq, dk, dv, q, k, v, do, slopes, scale, sel=None, chunk=None):
     """Compare against the fp32-upcast oracle on the same (rounded) inputs;
-    ``sel`` restricts the oracle to a subset of (b, h) pairs."""
+    ``sel`` restricts the oracle to one (b, h) pair. Returns the achieved
+    (max error, relative L2) per output."""
     if sel is not None:
         b, h = sel
         q, k, v, do = (t[b:b + 1, h:h + 1] for t in (q, k, v, do))
         o, L, dq, dk, dv = (t[b:b + 1, h:h + 1] for t in (o, L, dq, dk, dv))
         slopes = slopes[h:h + 1]
     dt = q.dtype
-    ro, rL = O.attention_fwd(q, k, v, slopes, scale, dtype=torch.float32)
-    assert_lowp(o, ro, dt, "o")
+    ro, rL = O.attention_fwd(q, k, v, slopes, scale, dtype=torch.float32, chunk=chunk)
+    res = {"o": assert_lowp(o, ro, dt, "o")}
     assert _rel_max(L, rL) <= 1e-2, ("L", _rel_max(L, rL))
     # backward from the GPU forward's own O and L, as the autograd path does
-    rq, rk, rv = O.attention_bwd(q, k, v, o, L, do, slopes, scale, dtype=torch.float32)
+    rq, rk, rv = O.attention_bwd(q, k, v, o, L, do, slopes, scale, dtype=torch.float32, chunk=chunk)
     for name, got, ref in (("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
-        assert_lowp(got, ref, dt, name)
+        res[name] = assert_lowp(got, ref, dt, name)
+    return res
 
 
 def _pin_mfma(monkeypatch, D):
@@ -156,20 +150,20 @@ def test_lowp_shapes(gpu, dtype, B, H, T, D, monkeypatch):
     _check_lowp(o, L, dq, dk, dv, q, k, v, do, slopes, scale)
 
 
-def test_config3_bf16_sampled_heads(gpu, monkeypatch):
-    # B=4, H=16, S=4096, D=128 bf16; slopes 2^(-(i+1)/2); heads are independent,
-    # so the oracle checks three (b, h) pairs, including the smallest and
-    # largest slope
+def test_config3_bf16_all_heads(gpu, monkeypatch):
+    # B=4, H=16, S=4096, D=128 bf16; slopes 2^(-(i+1)/2): every (b, h) head
+    # against the fp32 oracle (two heads per oracle pass bound its memory)
     B, H, T, D = 4, 16, 4096, 128
     _pin_mfma(monkeypatch, D)
     q, k, v, do = _inputs(3, B, H, T, D, torch.bfloat16)
     slopes = torch.tensor([2.0 ** (-(i + 1) / 2) for i in range(H)], dtype=torch.float32)
     scale = 1.0 / math.sqrt(D)
     o, L, dq, dk, dv = _run(q, k, v, do, slopes.to(dev), scale)
-    for sel in ((0, 0), (2, 7), (3, 15)):
-        _check_lowp(o, L, dq, dk, dv, q, k, v, do, slopes, scale, sel=sel)
     for t in (o, L, dq, dk, dv):
         assert bool(torch.isfinite(t).all())
+    res = _check_lowp(o, L, dq, dk, dv, q, k, v, do, slopes, scale, chunk=2)
+    print("config 3, all 64 heads: " + ", ".join(
+        f"{n} max err {e:.3e} relL2 {r:.3e}" for n, (e, r) in res.items()))
 
 
 def test_mfma_matches_tiled_kernel(gpu, monkeypatch):
