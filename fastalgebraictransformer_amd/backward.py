@@ -18,6 +18,7 @@ from .forward import (  # noqa: F401
     _key_mask_arg,
     _bht_strides,
     _unit_d,
+    _warn_if_tiled,
     compute_alibi_slopes,
     rational_attention_forward,
 )
@@ -30,6 +31,7 @@ def _attn_bwd_into(q, k, v, output, L, grad_output, dq, dk, dv, alibi_slopes, sc
     allocator. ``extended``: kat_attn_bwd_masked (see _attn_fwd_into)."""
     lib = _lib.load()
     B, H, T, D = q.shape
+    _warn_if_tiled((q, k, v, output, grad_output, dq, dk, dv), D, q.dtype)
     slopes = alibi_slopes.to(device=q.device, dtype=torch.float32).contiguous()
     code = _lib.dtype_code(q)
     ws_bytes = lib.kat_attn_bwd_workspace_size(B, H, T, D, code)

@@ -562,7 +562,8 @@ __global__ __launch_bounds__(256) void rsoftmax_bwd_w_k(const T* __restrict__ dy
   }
 }
 
-// Multi-pass block-per-row fallbacks (wide rows, misaligned or odd widths).
+// Multi-pass block-per-row fallbacks (wide rows, misaligned or odd widths);
+// grid-stride over rows.
 template <typename T>
 __global__ __launch_bounds__(256) void rsoftmax_fwd_mp_k(const T* __restrict__ x,
                                                          T* __restrict__ p, int64_t n_rows,
@@ -570,20 +571,21 @@ __global__ __launch_bounds__(256) void rsoftmax_fwd_mp_k(const T* __restrict__ x
                                                          float eps) {
   typedef typename AccT<T>::type A;
   __shared__ A sh[kRowWaves];
-  const int64_t row = blockIdx.x;
-  const T* xr = x + row * ldx;
-  A sum = A(0);
-  for (int c = threadIdx.x; c < n_cols; c += blockDim.x) {
-    const A s = rsig(to_acc(xr[c]));
-    const A s2 = s * s;
-    sum += s2 * s2;
-  }
-  sum = block_sum(sum, sh);
-  const A inv = A(1) / (sum + A(eps));
-  for (int c = threadIdx.x; c < n_cols; c += blockDim.x) {
-    const A s = rsig(to_acc(xr[c]));
-    const A s2 = s * s;
-    p[row * ldp + c] = from_acc<T>(s2 * s2 * inv);
+  for (int64_t row = blockIdx.x; row < n_rows; row += gridDim.x) {
+    const T* xr = x + row * ldx;
+    A sum = A(0);
+    for (int c = threadIdx.x; c < n_cols; c += blockDim.x) {
+      const A s = rsig(to_acc(xr[c]));
+      const A s2 = s * s;
+      sum += s2 * s2;
+    }
+    sum = block_sum(sum, sh);
+    const A inv = A(1) / (sum + A(eps));
+    for (int c = threadIdx.x; c < n_cols; c += blockDim.x) {
+      const A s = rsig(to_acc(xr[c]));
+      const A s2 = s * s;
+      p[row * ldp + c] = from_acc<T>(s2 * s2 * inv);
+    }
   }
 }
 
@@ -596,19 +598,20 @@ __global__ __launch_bounds__(256) void rsoftmax_bwd_mp_k(const T* __restrict__ d
                                                          int64_t ldp, int64_t lddx, float eps) {
   typedef typename AccT<T>::type A;
   __shared__ A sh[kRowWaves];
-  const int64_t row = blockIdx.x;
-  A dot = A(0);
-  for (int c = threadIdx.x; c < n_cols; c += blockDim.x)
-    dot += to_acc(dy[row * lddy + c]) * to_acc(p[row * ldp + c]);
-  dot = block_sum(dot, sh);
   const A e = A(eps);
-  for (int c = threadIdx.x; c < n_cols; c += blockDim.x) {
-    const A xx = to_acc(x[row * ldx + c]);
-    const A den = fabs(xx) + A(1);
-    const A sig = A(0.5) * (xx / den + A(1));
-    const A g = A(2) / (den * den * (sig + e));
-    dx[row * lddx + c] =
-        from_acc<T>(to_acc(p[row * ldp + c]) * g * (to_acc(dy[row * lddy + c]) - dot));
+  for (int64_t row = blockIdx.x; row < n_rows; row += gridDim.x) {
+    A dot = A(0);
+    for (int c = threadIdx.x; c < n_cols; c += blockDim.x)
+      dot += to_acc(dy[row * lddy + c]) * to_acc(p[row * ldp + c]);
+    dot = block_sum(dot, sh);
+    for (int c = threadIdx.x; c < n_cols; c += blockDim.x) {
+      const A xx = to_acc(x[row * ldx + c]);
+      const A den = fabs(xx) + A(1);
+      const A sig = A(0.5) * (xx / den + A(1));
+      const A g = A(2) / (den * den * (sig + e));
+      dx[row * lddx + c] =
+          from_acc<T>(to_acc(p[row * ldp + c]) * g * (to_acc(dy[row * lddy + c]) - dot));
+    }
   }
 }
 
@@ -850,24 +853,25 @@ __global__ __launch_bounds__(256) void men_fwd_mp_k(const T* __restrict__ x, con
   typedef std::conditional_t<kAdd, R, T> RT;
   const RT* r = reinterpret_cast<const RT*>(rp);
   __shared__ A sh[kRowWaves];
-  const int64_t row = blockIdx.x;
-  auto xin = [&](int c) -> T {
-    if constexpr (kAdd) return from_acc<T>(to_acc(x[row * ldx + c]) + to_acc(r[row * ldr + c]));
-    else return x[row * ldx + c];
-  };
-  A s = A(0);
-  for (int c = threadIdx.x; c < n_cols; c += blockDim.x) {
-    const T xv = xin(c);
-    if constexpr (kAdd) h[row * ldh + c] = xv;
-    s += fabs(to_acc(xv));
-  }
-  s = block_sum(s, sh);
-  const A mean = s / A(n_cols);
-  const A inv = A(1) / (mean + A(eps));
-  if (threadIdx.x == 0) mu[row] = (float)mean;
-  for (int c = threadIdx.x; c < n_cols; c += blockDim.x) {
-    const A wv = w_is_f32 ? (A)((const float*)wp)[c] : to_acc(((const T*)wp)[c]);
-    y[row * ldy + c] = narrow_to<Y>(to_acc(xin(c)) * inv * wv);
+  for (int64_t row = blockIdx.x; row < n_rows; row += gridDim.x) {
+    auto xin = [&](int c) -> T {
+      if constexpr (kAdd) return from_acc<T>(to_acc(x[row * ldx + c]) + to_acc(r[row * ldr + c]));
+      else return x[row * ldx + c];
+    };
+    A s = A(0);
+    for (int c = threadIdx.x; c < n_cols; c += blockDim.x) {
+      const T xv = xin(c);
+      if constexpr (kAdd) h[row * ldh + c] = xv;
+      s += fabs(to_acc(xv));
+    }
+    s = block_sum(s, sh);
+    const A mean = s / A(n_cols);
+    const A inv = A(1) / (mean + A(eps));
+    if (threadIdx.x == 0) mu[row] = (float)mean;
+    for (int c = threadIdx.x; c < n_cols; c += blockDim.x) {
+      const A wv = w_is_f32 ? (A)((const float*)wp)[c] : to_acc(((const T*)wp)[c]);
+      y[row * ldy + c] = narrow_to<Y>(to_acc(xin(c)) * inv * wv);
+    }
   }
 }
 
@@ -956,6 +960,12 @@ constexpr int kRowBlocksPerCU = 8;
 static inline int64_t row_grid(int64_t rows, int per_cu) {
   const int64_t cap = std::min<int64_t>((int64_t)per_cu * num_cus(), (rows + 3) / 4);
   return std::max<int64_t>(1, std::min<int64_t>(rows, cap));
+}
+
+// grid of the one-block-per-row kernels, which walk rows with a grid stride
+// (so row counts past 2^31 stay covered)
+static inline unsigned mp_grid(int64_t rows) {
+  return (unsigned)std::max<int64_t>(1, std::min<int64_t>(rows, (int64_t)1 << 30));
 }
 
 static inline int pick_nch(int64_t n_cols, int per) {
@@ -1075,7 +1085,7 @@ static int rsoftmax_fwd_t(const T* x, T* p, int64_t rows, int64_t cols, int64_t 
     KAT_NCH_SWITCH(nch, hipLaunchKernelGGL((rsoftmax_fwd_k<T, N>), dim3((unsigned)blocks),
                                            dim3(256), 0, st, x, p, rows, (int)cols, ldx, ldp, eps));
   } else {
-    hipLaunchKernelGGL((rsoftmax_fwd_mp_k<T>), dim3((unsigned)rows), dim3(256), 0, st, x, p, rows,
+    hipLaunchKernelGGL((rsoftmax_fwd_mp_k<T>), dim3(mp_grid(rows)), dim3(256), 0, st, x, p, rows,
                        (int)cols, ldx, ldp, eps);
   }
   return check_launch("kat_rsoftmax_fwd");
@@ -1101,7 +1111,7 @@ static int rsoftmax_bwd_t(const T* dy, const T* x, const T* p, T* dx, int64_t ro
                                            dim3(256), 0, st, dy, x, p, dx, rows, (int)cols, lddy,
                                            ldx, ldp, lddx, eps));
   } else {
-    hipLaunchKernelGGL((rsoftmax_bwd_mp_k<T>), dim3((unsigned)rows), dim3(256), 0, st, dy, x, p,
+    hipLaunchKernelGGL((rsoftmax_bwd_mp_k<T>), dim3(mp_grid(rows)), dim3(256), 0, st, dy, x, p,
                        dx, rows, (int)cols, lddy, ldx, ldp, lddx, eps);
   }
   return check_launch("kat_rsoftmax_bwd");
@@ -1132,7 +1142,7 @@ static int men_fwd_t(const T* x, const W* w, Y* y, float* mu, int64_t rows, int6
                            w, y, mu, rows, (int)cols, ldx, ldy, eps, (const void*)r, h, ldr, ldh);
     });
   } else {
-    hipLaunchKernelGGL((men_fwd_mp_k<T, R, Y>), dim3((unsigned)rows), dim3(256), 0, st, x,
+    hipLaunchKernelGGL((men_fwd_mp_k<T, R, Y>), dim3(mp_grid(rows)), dim3(256), 0, st, x,
                        (const void*)w, (int)std::is_same<W, float>::value, y, mu, rows, (int)cols,
                        ldx, ldy, eps, (const void*)r, h, ldr, ldh);
   }

@@ -8,6 +8,8 @@ head dims it covers, an fp32 tiled kernel otherwise.
 """
 
 import math
+import os
+import warnings
 
 import torch
 
@@ -40,6 +42,30 @@ def _unit_d(t):
     return t if t.stride(-1) == 1 or t.shape[-1] == 1 else t.contiguous()
 
 
+_WARNED = set()
+
+
+def _warn_if_tiled(tensors, D, dtype):
+    """bf16 / fp16 attention runs on the MFMA kernels when the head dim is 64
+    or 128 and every [B, H, T, D] operand has 16-byte aligned rows; otherwise
+    libkat falls back to the fp32 tiled kernels, which are correct but about
+    an order of magnitude slower. Warn once per reason, so a model with
+    another head dim (or a misaligned view) does not lose that silently."""
+    if dtype not in (torch.bfloat16, torch.float16) or os.environ.get("KAT_ATTN_IMPL") == "tiled":
+        return
+    if D not in (64, 128):
+        reason = f"head dim {D} (the MFMA kernels cover 64 and 128)"
+    elif any(t.data_ptr() % 16 or any((st * t.element_size()) % 16 for st in t.stride()[:3])
+             for t in tensors):
+        reason = "rows not 16-byte aligned (a view with an odd offset or stride)"
+    else:
+        return
+    if reason not in _WARNED:
+        _WARNED.add(reason)
+        warnings.warn(f"rational attention in {dtype}: {reason}; running the fp32 tiled "
+                      "kernels, about 10x slower than the MFMA path", RuntimeWarning, stacklevel=3)
+
+
 def _key_mask_arg(key_mask, B, T, device):
     """The padding mask as a uint8 [B, T] device tensor (nonzero = attend), or None."""
     if key_mask is None:
@@ -56,6 +82,7 @@ def _attn_fwd_into(q, k, v, out, L, alibi_slopes, scale, causal, eps, key_mask=N
     honours ``causal``; otherwise kat_attn_fwd, always causal as the reference."""
     lib = _lib.load()
     B, H, T, D = q.shape
+    _warn_if_tiled((q, k, v, out), D, q.dtype)
     slopes = alibi_slopes.to(device=q.device, dtype=torch.float32).contiguous()
     assert slopes.numel() == H, "alibi_slopes must have n_heads entries"
     strides = _lib.i64_array(_bht_strides(q) + _bht_strides(k) + _bht_strides(v) +

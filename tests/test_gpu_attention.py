@@ -327,3 +327,20 @@ def test_mfma_attention_is_exactly_equivariant_to_power_of_two_scales(gpu, D, mo
     for name, u, s_, f in zip(("o", "L", "dq", "dk", "dv"), unit, scaled,
                               (2.0 ** 13, 1.0, 2.0 ** -23, 2.0 ** 9, 2.0 ** -20)):
         assert torch.equal(s_.float(), u.float() * f), name
+
+
+def test_tiled_fallback_warns_once(gpu):
+    # a bf16 call outside the MFMA kernels' envelope (here D = 32) runs the
+    # fp32 tiled kernels; the wrapper says so, once per reason
+    import warnings
+    from fastalgebraictransformer_amd import forward as fw
+    fw._WARNED.clear()
+    q, k, v, _ = _inputs(5, 1, 2, 40, 32, torch.bfloat16)
+    slopes = F.compute_alibi_slopes(2).to(dev)
+    with pytest.warns(RuntimeWarning, match="head dim 32"):
+        F.rational_attention_forward(q, k, v, slopes, 0.17)
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
+        F.rational_attention_forward(q, k, v, slopes, 0.17)
+        q2, k2, v2, _ = _inputs(6, 1, 2, 40, 128, torch.bfloat16)
+        F.rational_attention_forward(q2, k2, v2, slopes, 0.09)  # covered: no warning
