@@ -735,7 +735,11 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_k(AttnArgs a, float2* __re
 // The P role also forms w = (t r)^2 t of every score and passes it to the D role
 // through LDS, lane to lane (both roles hold the scores of a 16-query half in
 // the same MFMA C layout), so dS = w (4 cinv dP - 4 cinv Delta) costs the D role
-// one FMA and one multiply. 64-query Q16 / dO tiles and their stats stream
+// one FMA and one multiply. (Passing t instead and forming w in the D role,
+// from r = min(t, 2 - t), splits the VALU work evenly between the waves but
+// costs two more operations per score and measured 1-2% slower: the SIMD's
+// instruction issue, not either wave's chain, bounds this kernel.)
+// 64-query Q16 / dO tiles and their stats stream
 // through LDS; a tile is worked in two 32-query chunks with one barrier each:
 //   phase 1: P role S, P, w of chunk c                    | barrier
 //   phase 2: P role dV(c); D role dP(c + 1), dS(c), dK(c)
@@ -963,13 +967,19 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
     m1(std::false_type{}, 0, dpA[0], sm.o[0]);
     m1(std::false_type{}, 16, dpA[1], sm.o[0]);
   }
-  auto step = [&](int c, f32x4 (&pcur)[2][2], f32x4 (&pnext)[2][2]) __attribute__((always_inline)) {
-    const int it = c >> 1, buf = it & 1, r0 = 32 * (c & 1);
+  // chunk c of the loop, with CM = c % 4 known at compile time (the loop is
+  // unrolled by four), so that the tile buffer, the rows within it and the
+  // exchange buffer -- and with them every LDS address -- are a per-lane
+  // register plus an immediate
+  auto step = [&](int c, auto cm_tag, f32x4 (&pcur)[2][2], f32x4 (&pnext)[2][2]) __attribute__((always_inline)) {
+    constexpr int CM = decltype(cm_tag)::value;
+    constexpr int buf = CM >> 1, r0 = 32 * (CM & 1);
+    const int it = c >> 1;
     const int qc = qbase + 32 * c;
     const bool need = needc(c), full = need && fullc(c);
-    f32x4 (*xw)[64] = sm.x[c & 1][grp];
+    f32x4 (*xw)[64] = sm.x[CM & 1][grp];
     uint32_t pa[2][2], pb[2][2];
-    if ((c & 1) == 0) {
+    if constexpr ((CM & 1) == 0) {
       // a new Q16 tile: its exponent (both roles track it)
       const int eqt = qexp_h[(qbase >> 6) + it];
       if (eqt != eq) {
@@ -1003,7 +1013,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
         vp_(std::true_type{}, qc + 16, r0 + 16, sB, sm.st[buf], xw, 2, pb);
       }
     }
-    if ((c & 1) == 0) {
+    if constexpr ((CM & 1) == 0) {
       // every wave has left the previous tile: its buffer takes the next one
       __syncthreads();
       if (it + 1 < n_it) issue(buf ^ 1, qbase + (it + 1) * kBN);
@@ -1021,8 +1031,8 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
         for (int u = 0; u < 4; ++u) wv[u] = xw[u][lane];
       }
       if (needc(c + 1)) {
-        const int c1 = c + 1, r1 = 32 * (c1 & 1);
-        const short* os1 = sm.o[(c1 >> 1) & 1];
+        constexpr int r1 = 32 * ((CM + 1) & 1);
+        const short* os1 = sm.o[((CM + 1) >> 1) & 1];
         m1(std::false_type{}, r1, pnext[0], os1);
         m1(std::false_type{}, r1 + 16, pnext[1], os1);
       }
@@ -1038,7 +1048,11 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
           for (int ks = 0; ks < 2; ++ks) {
             float dv[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) dv[j] = wv[2 * hh + ks][j] * fmaf(pcur[hh][ks][j], c4v[j], ndv[j]);
+            for (int j = 0; j < 4; ++j) {
+              // w = t^3 r^2 from t alone: r = 1 / (|s| + 1) equals t for s < 0
+              // and 2 - t for s >= 0, i.e. min(t, 2 - t) (exact given t)
+              dv[j] = wv[2 * hh + ks][j] * fmaf(pcur[hh][ks][j], c4v[j], ndv[j]);
+            }
             dp[ks][0] = pack2_f16(dv[0], dv[1]);
             dp[ks][1] = pack2_f16(dv[2], dv[3]);
           }
@@ -1047,10 +1061,15 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
       }
     }
   };
-  // unrolled by two: the D role's dP registers alternate
-  for (int c = 0; c < n_ch; c += 2) {
-    step(c, dpA, dpB);
-    if (c + 1 < n_ch) step(c + 1, dpB, dpA);
+  // unrolled by four (two tiles): static buffers, and the D role's dP
+  // registers alternate; n_ch is even
+  for (int c = 0; c < n_ch; c += 4) {
+    step(c, std::integral_constant<int, 0>{}, dpA, dpB);
+    step(c + 1, std::integral_constant<int, 1>{}, dpB, dpA);
+    if (c + 2 < n_ch) {
+      step(c + 2, std::integral_constant<int, 2>{}, dpA, dpB);
+      step(c + 3, std::integral_constant<int, 3>{}, dpB, dpA);
+    }
   }
 
   T* __restrict__ outp = prole ? (T*)a.dv + b * a.sdv[0] + h * a.sdv[1] : (T*)a.dk + b * a.sdk[0] + h * a.sdk[1];
