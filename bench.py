@@ -14,7 +14,12 @@ throughput 7*B*H*S^2*D / step time in TFLOP/s. The same JSON line carries:
                  by reading (not writing) a 512 MB buffer, so no dirty lines
                  of the flush are written back inside the timed region;
   * cpu_baseline -- the CPU oracle (fp32) on a bounded sample of the same
-                 workload (one (b, h) head), on this host's cores;
+                 workload (one (b, h) head), on this host's cores; and
+    cpu_baselines -- the same for the fused ops (the full config-2 shapes)
+                 and the config-4 training step (one block on a
+                 2-row batch slice plus embed / head / loss, extrapolated);
+  * config5_attention -- fwd+bwd of the 1.3 B model's attention shape
+                 (B=2, H=16, S=8192, D=128, bf16);
   * attention_variants -- fwd+bwd of the padding-mask / non-causal attention
                  extension at the same shape (right-padded batch, non-causal,
                  both), TFLOP/s over the (query, key) pairs each attends;
@@ -23,13 +28,14 @@ throughput 7*B*H*S^2*D / step time in TFLOP/s. The same JSON line carries:
                  cache against the reference's re-run-the-prefix loop;
   * device     -- CU count, a measured bf16 MFMA loop rate (beside the 2.5 PF
                  spec peak) and a measured 1 GiB device-copy bandwidth;
-  * model_step -- one training step (bf16 autocast forward + loss + backward,
-                 no optimizer) of the 109.5 M-parameter model at batch 16 x 2048
-                 (reported, not the metric): tokens/s and MFU; with --model-large
-                 also the 1.3 B-parameter model at batch 2 x 8192.
+  * model_step / model_step_large -- one training step (bf16 autocast
+                 forward + loss + backward, no optimizer) of the 109.5 M-parameter
+                 model at batch 16 x 2048 and of the 1.3 B-parameter model at
+                 batch 2 x 8192 (reported, not the metric): tokens/s and MFU.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-fused]
-                       [--no-variants] [--no-decode] [--no-model] [--model-large]
+                       [--no-variants] [--no-decode] [--no-model] [--no-model-large]
+                       [--no-config5]
        python bench.py --copy-calibration   (one plain 1 GiB device copy, for
                                              scaling HBM byte counters)
 """
@@ -48,12 +54,24 @@ METRIC = "attn fwd+bwd TFLOP/s (% MFMA peak) at S=4096; fused-op HBM GB/s (% pea
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
 
-# HBM bytes per call at the benchmark shape, from rocprofv3 FETCH_SIZE and
-# WRITE_SIZE passes (sum over the call's kernels), each scaled by what the same
-# counter reads for a plain 1 GiB copy (python bench.py --copy-calibration:
-# FETCH_SIZE x 2.0, WRITE_SIZE x 1.0). Summary and commands:
-# profiles/attention_bench_hbm_traffic.md
-MEASURED_TRAFFIC_BYTES = {"kat_attn_fwd": 745.8 * 2 ** 20, "kat_attn_bwd": 1985.5 * 2 ** 20}
+# HBM bytes per call at the benchmark shape come from the committed rocprofv3
+# summary profiles/attention_bench_hbm_traffic.md: FETCH_SIZE and WRITE_SIZE
+# passes over this bench (summed over the call's kernels), each scaled by what
+# the same counter reads for a plain copy of known size. Its lines
+# "traffic <call> <bytes>" are read here.
+TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "attention_bench_hbm_traffic.md")
+
+
+def measured_traffic():
+    out = {}
+    try:
+        for line in open(TRAFFIC_SUMMARY):
+            parts = line.split()
+            if len(parts) == 3 and parts[0] == "traffic":
+                out[parts[1]] = int(parts[2])
+    except OSError:
+        pass
+    return out
 
 
 def attention_inputs(torch, B, H, T, D, dev, seed=0):
@@ -405,13 +423,98 @@ def cpu_model():
     return "unknown"
 
 
+def _cpu_threads(torch):
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    return cores
+
+
+def cpu_baselines(torch):
+    """The CPU oracle (fp32 on the bf16-rounded inputs) on the other measured
+    workloads, on this host's cores: the fused ops fwd+bwd at the full config-2
+    shapes, and the config-4 training step extrapolated from one
+    AlgebraicBlock fwd+bwd on a 2-row batch slice at T = 2048 (the reference's
+    CPU attention, torch norm and SwiGLU formulas) plus the embedding, head and
+    loss on the same slice."""
+    import oracle as O
+    cores = _cpu_threads(torch)
+    g = torch.Generator().manual_seed(1)
+    bf = torch.bfloat16
+    res = {}
+
+    def timed(fn):
+        t0 = time.perf_counter()
+        fn()
+        return time.perf_counter() - t0
+
+    def rowop(name, rows, cols, nbytes, fn, reps=3):
+        ts = sorted(timed(fn) for _ in range(reps))
+        t = ts[len(ts) // 2]
+        res[name] = {"value": round(nbytes / t / 1e9, 2), "unit": "GB/s", "cores": cores,
+                     "kind": "port",
+                     "sample": f"the full [{rows}, {cols}] shape, oracle fp32 fwd+bwd, median of "
+                               f"{reps} ({t:.2f} s); the GPU line's algorithmic bytes"}
+
+    N, C = 16384, 4096
+    x = torch.randn(N, C, generator=g).to(bf)
+    w = 1 + 0.02 * torch.randn(C, generator=g)
+    dy = torch.randn(N, C, generator=g).to(bf)
+
+    def norm():
+        _, mu = O.mean_error_norm_fwd(x, w, dtype=torch.float32)
+        O.mean_error_norm_bwd(dy, x, w, mu, dtype=torch.float32)
+    rowop("mean_error_norm", N, C, (2 * N * C * 2 + C * 4 + N * 4) + (3 * N * C * 2 + 2 * C * 4 + N * 4),
+          norm)
+    del x, dy
+    N, C = 16384, 11008
+    ga, va, dy2 = (torch.randn(N, C, generator=g).to(bf) for _ in range(3))
+
+    def swiglu():
+        O.swiglu_fwd(ga, va, dtype=torch.float32)
+        O.swiglu_bwd(dy2, ga, va, dtype=torch.float32)
+    rowop("rational_swiglu", N, C, 8 * N * C * 2, swiglu)
+    del ga, va, dy2
+    N, C = 4096, 4096
+    sx = (2 * torch.randn(N, C, generator=g)).to(bf)
+    dy3 = torch.randn(N, C, generator=g).to(bf)
+
+    def softmax():
+        p = O.rational_softmax_fwd(sx, dtype=torch.float32)
+        O.rational_softmax_bwd(dy3, sx, p, dtype=torch.float32)
+    rowop("rational_softmax", N, C, 6 * N * C * 2, softmax)
+
+    # config 4: one block on 2 x 2048 tokens, then embedding + head + loss
+    from fastalgebraictransformer_amd.algebraic_model import AlgebraicBlock
+    torch.manual_seed(0)
+    blk = AlgebraicBlock(768, 12, 2048, dropout=0.0)
+    xb = torch.randn(2, 2048, 768, generator=g, requires_grad=True)
+
+    def block():
+        blk(xb).backward(torch.ones(2, 2048, 768))
+    tb = timed(block)
+    emb = torch.nn.Embedding(32000, 768)
+    ids = torch.randint(0, 32000, (2, 2048), generator=g)
+
+    def head():
+        h = emb(ids)
+        logits = torch.nn.functional.linear(h, emb.weight)
+        torch.nn.functional.cross_entropy(logits.view(-1, 32000), ids.view(-1)).backward()
+    th = timed(head)
+    step = 8 * (12 * tb + th)  # 16 rows = 8 slices of 2; 12 blocks
+    res["model_step"] = {"value": round(16 * 2048 / step, 1), "unit": "tokens/s", "cores": cores,
+                         "kind": "port",
+                         "sample": f"EXTRAPOLATION: AlgebraicTransformerLM(32000, 768, 12, 12) step at "
+                                   f"16 x 2048 = 8 x (12 x one block fwd+bwd on 2 x 2048 tokens "
+                                   f"[{tb:.2f} s] + embedding/head/loss on 2 x 2048 [{th:.2f} s]), fp32"}
+    return res
+
+
 def cpu_baseline(torch, S=4096, D=128, reps=3):
     """CPU oracle (fp32) forward + backward of one (b, h) head of the workload
     (heads are independent, so this is an exact 1/64 slice), on every core this
     process may run on."""
     import oracle as O
-    cores = len(os.sched_getaffinity(0))
-    torch.set_num_threads(cores)
+    cores = _cpu_threads(torch)
     g = torch.Generator().manual_seed(0)
     q, k, v, do = (torch.randn(1, 1, S, D, generator=g).to(torch.bfloat16) for _ in range(4))
     slopes = torch.tensor([2.0 ** -0.5])
@@ -443,8 +546,10 @@ def main():
     ap.add_argument("--no-decode", action="store_true",
                     help="skip the KV-cache decode attention and generate() timings")
     ap.add_argument("--no-model", action="store_true", help="skip the model training step")
-    ap.add_argument("--model-large", action="store_true",
-                    help="also time the ~1.3B model step (batch 2 x 8192, ~55 GB; reported only)")
+    ap.add_argument("--no-model-large", action="store_true",
+                    help="skip the ~1.3B model step (batch 2 x 8192, ~47 GB; reported only)")
+    ap.add_argument("--no-config5", action="store_true",
+                    help="skip the attention fwd+bwd at the 1.3B model's shape (B=2, H=16, S=8192)")
     ap.add_argument("--no-device", action="store_true", help="skip the MFMA / copy probes")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain device-to-device copy of 1 GiB (3 times): the "
@@ -498,13 +603,21 @@ def main():
         "roofline": {"bound": "mfma", "call": dom, "achieved": round(ach, 2),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(ach / PEAK_BF16_TFLOPS, 4),
-                     "traffic": round(MEASURED_TRAFFIC_BYTES[dom])},
+                     "traffic": measured_traffic().get(dom)},
         "kernels": {"kat_attn_fwd": {"ms": round(att["fwd_ms"], 4), "median_ms": round(att["fwd_median_ms"], 4),
                                      "TFLOPs": round(fwd_tf, 2), "algorithmic_flops": att["flops_fwd"]},
                     "kat_attn_bwd": {"ms": round(att["bwd_ms"], 4), "median_ms": round(att["bwd_median_ms"], 4),
                                      "TFLOPs": round(bwd_tf, 2), "algorithmic_flops": att["flops_bwd"]}},
         "frac_mfma_peak_step": round(value / PEAK_BF16_TFLOPS, 4),
     }
+    if not args.no_config5:
+        a5 = bench_attention(torch, F, 10, 3, B=2, H=16, T=8192, D=128)
+        t5 = a5["flops_step"] / (a5["ms"] * 1e-3) / 1e12
+        line["config5_attention"] = {
+            "shape": {"B": 2, "H": 16, "S": 8192, "D": 128}, "dtype": "bf16", "steps": 10,
+            "ms_per_step": round(a5["ms"], 4), "TFLOPs": round(t5, 2),
+            "frac_mfma_peak": round(t5 / PEAK_BF16_TFLOPS, 4),
+            "fwd_ms": round(a5["fwd_ms"], 4), "bwd_ms": round(a5["bwd_ms"], 4)}
     if not args.no_variants:
         line["attention_variants"] = bench_attention_variants(torch, F)
     if not args.no_decode:
@@ -517,11 +630,12 @@ def main():
         line["device"] = device_info(torch, _lib.load())
     if not args.no_model:
         line["model_step"] = bench_model_step(torch, "small")
-    if args.model_large:
+    if not args.no_model_large:
         line["model_step_large"] = bench_model_step(torch, "large", steps=3, warmup=1)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(torch)
         line["cpu_baseline"]["value"] = round(line["cpu_baseline"]["value"], 5)
+        line["cpu_baselines"] = cpu_baselines(torch)
     print(json.dumps(line), flush=True)
 
 
