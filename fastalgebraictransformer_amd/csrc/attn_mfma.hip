@@ -1,17 +1,21 @@
 // bf16 / fp16 MFMA rational attention for gfx950 (CDNA4).
 //
-// Three kernels carry the attention math, plus two streaming passes:
+// The attention math runs in three MFMA kernels, beside two streaming passes:
 //   attn_fwd_k         O, L      query-tile blocks; K, V tiles stream through LDS
-//   attn_bwd_prep_k    fp16 copy of K, per-tile exponents and V row norms
-//   attn_bwd_dq_k      dQ        query-tile blocks; fp16 K and V tiles stream; also
-//                                Delta, the row stats and the fp16 copy of Q
-//   attn_bwd_stscale_k scales the row stats by the head's dS exponent
+//   attn_bwd_prep_k    fp16 copies of Q and K with per-tile exponents, Delta and
+//                                the row stats, the parts of each head's dS bound
+//   attn_bwd_stscale_k the head's dS exponent; scales the row stats by it
 //   attn_bwd_dkv_k     dK, dV    key-tile blocks; fp16 Q and dO tiles stream; the
-//                                waves split into a dV role and a dK role
+//                                waves split into a dV role and a dK role; the dK
+//                                role also stores the fp16 dS it computes
+//   attn_bwd_dq_k      dQ        query-tile blocks: dQ = dS K over the stored dS
 // Every output element is written by one wave, so results are deterministic
-// (the only atomic is a max over non-negative floats, which is order-free).
+// (no atomics). The backward computes S, P and dS once: 5 MFMA units for the 5
+// of the algorithm (S, dP, dV, dK, dQ).
 //
-// Common structure. Each wave owns 32 rows (queries, or keys for dK/dV) whose
+// Common structure of the forward and dK/dV kernels (the dQ kernel is a plain
+// streaming GEMM, described at it). Each wave owns 32 rows (queries, or keys
+// for dK/dV) whose
 // operand fragments stay in VGPRs as the B operand of v_mfma_f32_16x16x32; the
 // streamed side is staged 64 rows at a time by LDS-DMA into a swizzled,
 // double-buffered LDS tile and read as the A operand, either row-wise
@@ -42,12 +46,12 @@
 //     of the MFMA scaled by both tiles' factors, which the bias and the scale
 //     applied to it absorb; an accumulator is rescaled when a new tile brings
 //     another exponent.
-//   * dS in the dQ kernel: per query row, from the bound
-//     w |dP - Delta_i| <= 1.11 (||dO_i||_2 max_j ||v_j||_2 + |Delta_i|)
-//     (w = t^3 r^2 <= 1.11), so that the scaled dS stays below 2^14.
-//   * dS in the dK / dV kernel: per head (dK sums over rows), from the largest
-//     row bound 4 cinv_i w |dP - Delta_i| = p g |dP - Delta_i| with p g <= 4
-//     (p <= 1 when L is the forward's row sum).
+//   * dS (one copy, which both dK and dQ take): per head, 2^kh with kh from
+//     the bound 4 cinv_i w |dP_ij - Delta_i| <= min(4.1, 1.125 4 cinv_i)
+//     (||dO_i||_2 ||v_j||_2 + |Delta_i|) (w = t^3 r^2 <= 1.11, and
+//     4 cinv_i w = p g <= 4 when L is the forward's row sum), maximised over
+//     the head, so that every scaled dS stays below 2^14 and reaches fp16's
+//     subnormal range only 27 binades below the head's largest.
 // So the gradients are exactly equivariant under power-of-two scalings of q,
 // k, v and dO, and dO's scale (a training step's is ~1e-5 .. 1e-7 per element)
 // does not move dS into fp16's subnormal range.
@@ -57,6 +61,7 @@
 // whose p <= (r / 2)^4 / L is itself negligible.
 
 #include <algorithm>
+#include <cstdlib>
 #include <type_traits>
 
 #include "attn_common.h"
@@ -309,25 +314,44 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_k(AttnArgs a) {
   }
 }
 
+// Everything the backward's MFMA kernels take besides the inputs (the
+// workspace, laid out by bwd_ws below).
+struct BwdWs {
+  float2* stats;  // per row (4 cinv, -4 cinv Delta) [B*H][T], then x 2^kh
+  f16* q16;       // fp16 copies [B*H][T][D], scaled per 64-row tile
+  f16* k16;
+  int* kexp;      // per 64-row tile [B*H][nt]: the copies' exponents
+  int* qexp;
+  float* vnrm;    // per tile: max_j ||v_j||_2
+  float* abnd;    // per tile: max_i c_i ||dO_i||_2    (c_i = min(4.1, 1.125 * 4 cinv_i))
+  float* bbnd;    // per tile: max_i c_i |Delta_i|
+  int* khead;     // per head [B*H]: dS exponent kh
+  f16* dst;       // dS^T tiles of a group of heads (layout at attn_bwd_dkv_k)
+  int group;      // heads per dK / dV + dQ launch pair (the dS^T tiles' capacity)
+  size_t bytes;
+};
+
 // ============================================================================
-// Backward prep, one block per 64-row tile of one (b, h):
-//   k16   the fp16 copy of K scaled by 2^kexp, kexp = tile_exp(max |k| of the
-//         tile) (exact: a power of two), [B*H][T][D];
-//   kexp  that exponent per tile, [B*H][nt] (nt = ceil(T / 64));
-//   vnrm  the largest row norm ||v_j||_2 of the tile's V rows, [B*H][nt];
-//   bmax  cleared for the head by its tile-0 block (the dQ kernel raises it
-//         with atomicMax to the head's bound on |dS|).
-// A row's LPR = D / 8 lanes are consecutive lanes of one wave; the block
-// covers its 64 rows in NP passes of 256 / LPR rows.
+// Backward prep, one block per 64-row tile of one (b, h). Streams every input
+// row once:
+//   k16, q16  fp16 copies of K and Q scaled by 2^kexp / 2^qexp, the tile's
+//             tile_exp of max |x| (exact: a power of two);
+//   stats     (4 cinv_i, -4 cinv_i Delta_i), Delta_i = <dO_i, O_i>,
+//             4 cinv_i = 1 / (4 (L_i + eps));
+//   vnrm, abnd, bbnd  the tile's parts of the head's bound on |dS|:
+//             |dS_ij| = 4 cinv_i w |dP_ij - Delta_i| with w = t^3 r^2 <= 1.11 and
+//             4 cinv_i w = p g <= 4 (p <= 1 when L is the forward's row sum), and
+//             |dP_ij - Delta_i| <= ||dO_i||_2 ||v_j||_2 + |Delta_i|, so
+//             |dS_ij| <= abnd_max vnrm_max + bbnd_max over the head.
+// A row's LPR = D / 8 lanes are consecutive lanes of one wave; the block covers
+// its 64 rows in NP passes of 256 / LPR rows.
 // ============================================================================
 template <typename T, int D>
-__global__ __launch_bounds__(256) void attn_bwd_prep_k(AttnArgs a, f16* __restrict__ k16,
-                                                       int* __restrict__ kexp, float* __restrict__ vnrm,
-                                                       unsigned* __restrict__ bmax) {
+__global__ __launch_bounds__(256) void attn_bwd_prep_k(AttnArgs a, BwdWs ws) {
   constexpr int LPR = D / 8;
   constexpr int RPP = 256 / LPR;
   constexpr int NP = 64 / RPP;
-  __shared__ float red[2][4];
+  __shared__ float red[5][4];
   const int nt = (a.T + 63) / 64;
   const int bh = (int)(blockIdx.x / (unsigned)nt), t = (int)blockIdx.x - bh * nt;
   const int b = bh / a.H, h = bh - b * a.H;
@@ -335,388 +359,299 @@ __global__ __launch_bounds__(256) void attn_bwd_prep_k(AttnArgs a, f16* __restri
   const int sub = tid % LPR, d = 8 * sub;
   const T* kp = (const T*)a.k + b * a.sk[0] + h * a.sk[1];
   const T* vp = (const T*)a.v + b * a.sv[0] + h * a.sv[1];
-  i16x8 kv[NP];
-  float km = 0.f, vm = 0.f;
+  const T* qp = (const T*)a.q + b * a.sq[0] + h * a.sq[1];
+  const T* op = (const T*)a.o + b * a.so[0] + h * a.so[1];
+  const T* dop = (const T*)a.dout + b * a.sdo[0] + h * a.sdo[1];
+  const float* Lp = a.L + b * a.sl[0] + h * a.sl[1];
+  i16x8 kv[NP], qv[NP];
+  float km = 0.f, qm = 0.f, vm = 0.f, am = 0.f, bm = 0.f;
 #pragma unroll
   for (int u = 0; u < NP; ++u) {
     const int row = 64 * t + RPP * u + tid / LPR;
-    kv[u] = i16x8{0, 0, 0, 0, 0, 0, 0, 0};
-    float vs = 0.f;
+    kv[u] = qv[u] = i16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    float vs = 0.f, dsum = 0.f, dsq = 0.f;
     if (row < a.T) {
       kv[u] = *reinterpret_cast<const i16x8*>(kp + (int64_t)row * a.sk[2] + d);
+      qv[u] = *reinterpret_cast<const i16x8*>(qp + (int64_t)row * a.sq[2] + d);
       const VecT<T, 8> v8 = *reinterpret_cast<const VecT<T, 8>*>(vp + (int64_t)row * a.sv[2] + d);
+      const VecT<T, 8> o8 = *reinterpret_cast<const VecT<T, 8>*>(op + (int64_t)row * a.so[2] + d);
+      const VecT<T, 8> g8 = *reinterpret_cast<const VecT<T, 8>*>(dop + (int64_t)row * a.sdo[2] + d);
       km = fmaxf(km, absmax8<T>(kv[u]));
+      qm = fmaxf(qm, absmax8<T>(qv[u]));
 #pragma unroll
-      for (int e = 0; e < 8; ++e) vs = fmaf((float)v8.v[e], (float)v8.v[e], vs);
+      for (int e = 0; e < 8; ++e) {
+        vs = fmaf((float)v8.v[e], (float)v8.v[e], vs);
+        dsum = fmaf((float)g8.v[e], (float)o8.v[e], dsum);
+        dsq = fmaf((float)g8.v[e], (float)g8.v[e], dsq);
+      }
     }
 #pragma unroll
-    for (int o = LPR / 2; o > 0; o >>= 1) vs += __shfl_xor(vs, o, 64);
+    for (int o = LPR / 2; o > 0; o >>= 1) {
+      vs += __shfl_xor(vs, o, 64);
+      dsum += __shfl_xor(dsum, o, 64);
+      dsq += __shfl_xor(dsq, o, 64);
+    }
     vm = fmaxf(vm, sqrtf(vs));
+    if (row < a.T) {
+      const float c4u = 1.f / (4.f * (Lp[(int64_t)row * a.sl[2]] + a.eps));
+      if (sub == 0) ws.stats[(int64_t)bh * a.T + row] = make_float2(c4u, -c4u * dsum);
+      const float cw = fminf(4.1f, 1.125f * c4u);
+      am = fmaxf(am, cw * sqrtf(dsq));
+      bm = fmaxf(bm, cw * fabsf(dsum));
+    }
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
     km = fmaxf(km, __shfl_xor(km, o, 64));
+    qm = fmaxf(qm, __shfl_xor(qm, o, 64));
     vm = fmaxf(vm, __shfl_xor(vm, o, 64));
+    am = fmaxf(am, __shfl_xor(am, o, 64));
+    bm = fmaxf(bm, __shfl_xor(bm, o, 64));
   }
   if (lane == 0) {
     red[0][w] = km;
-    red[1][w] = vm;
+    red[1][w] = qm;
+    red[2][w] = vm;
+    red[3][w] = am;
+    red[4][w] = bm;
   }
   __syncthreads();
-  km = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
-  vm = fmaxf(fmaxf(red[1][0], red[1][1]), fmaxf(red[1][2], red[1][3]));
-  const int e = tile_exp(km);
-  const float f = ldexpf(1.f, e);
-  f16* kq = k16 + (int64_t)bh * a.T * D;
+  float m[5];
+#pragma unroll
+  for (int i = 0; i < 5; ++i) m[i] = fmaxf(fmaxf(red[i][0], red[i][1]), fmaxf(red[i][2], red[i][3]));
+  const int ek = tile_exp(m[0]), eq = tile_exp(m[1]);
+  const float fk = ldexpf(1.f, ek), fq = ldexpf(1.f, eq);
+  f16* kq = ws.k16 + (int64_t)bh * a.T * D;
+  f16* qq = ws.q16 + (int64_t)bh * a.T * D;
 #pragma unroll
   for (int u = 0; u < NP; ++u) {
     const int row = 64 * t + RPP * u + tid / LPR;
-    if (row < a.T) *reinterpret_cast<i16x8*>(kq + (int64_t)row * D + d) = to_f16x8s<T>(kv[u], f);
+    if (row < a.T) {
+      *reinterpret_cast<i16x8*>(kq + (int64_t)row * D + d) = to_f16x8s<T>(kv[u], fk);
+      *reinterpret_cast<i16x8*>(qq + (int64_t)row * D + d) = to_f16x8s<T>(qv[u], fq);
+    }
   }
   if (tid == 0) {
-    kexp[blockIdx.x] = e;
-    vnrm[blockIdx.x] = vm;
-    if (t == 0) bmax[bh] = 0u;
+    ws.kexp[blockIdx.x] = ek;
+    ws.qexp[blockIdx.x] = eq;
+    ws.vnrm[blockIdx.x] = m[2];
+    ws.abnd[blockIdx.x] = m[3];
+    ws.bbnd[blockIdx.x] = m[4];
   }
 }
 
-// Scale of the dK / dV kernel's dS: 2^kh with kh = ds_exp(the head's bound on
-// |dS|, raised by the dQ kernel). The per-row stats (4 cinv, -4 cinv Delta)
-// are multiplied by 2^kh in place (exact), so dS = w (stats.x dP + stats.y)
-// comes out scaled; one thread per row.
-__device__ __forceinline__ int head_dsexp(const unsigned* bmax, int bh) {
-  return ds_exp(__uint_as_float(bmax[bh]));
-}
-
-__global__ __launch_bounds__(256) void attn_bwd_stscale_k(float2* __restrict__ stats,
-                                                          const unsigned* __restrict__ bmax,
-                                                          int T, int64_t rows) {
-  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (r >= rows) return;
-  const float f = ldexpf(1.f, head_dsexp(bmax, (int)(r / T)));
-  const float2 s = stats[r];
-  stats[r] = make_float2(s.x * f, s.y * f);
+// The head's dS exponent kh = ds_exp(abnd_max vnrm_max + bbnd_max) (maxima over
+// the head's tiles), so that every 2^kh dS of the head lies below 2^14; the
+// per-row stats are multiplied by 2^kh in place (exact), so that
+// dS = w (stats.x dP + stats.y) comes out scaled. Blocks of 256 rows of one
+// head; each reduces the head's tile values itself (no atomics, no ordering
+// between blocks) and the head's first block records kh.
+__global__ __launch_bounds__(256) void attn_bwd_stscale_k(BwdWs ws, int T, int cpb) {
+  __shared__ float red[3][4];
+  const int nt = (T + 63) / 64;
+  const int bh = (int)(blockIdx.x / (unsigned)cpb), ch = (int)blockIdx.x - bh * cpb;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  float vm = 0.f, am = 0.f, bm = 0.f;
+  for (int i = tid; i < nt; i += 256) {
+    const int64_t x = (int64_t)bh * nt + i;
+    vm = fmaxf(vm, ws.vnrm[x]);
+    am = fmaxf(am, ws.abnd[x]);
+    bm = fmaxf(bm, ws.bbnd[x]);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    vm = fmaxf(vm, __shfl_xor(vm, o, 64));
+    am = fmaxf(am, __shfl_xor(am, o, 64));
+    bm = fmaxf(bm, __shfl_xor(bm, o, 64));
+  }
+  if (lane == 0) {
+    red[0][w] = vm;
+    red[1][w] = am;
+    red[2][w] = bm;
+  }
+  __syncthreads();
+  vm = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+  am = fmaxf(fmaxf(red[1][0], red[1][1]), fmaxf(red[1][2], red[1][3]));
+  bm = fmaxf(fmaxf(red[2][0], red[2][1]), fmaxf(red[2][2], red[2][3]));
+  const int kh = ds_exp(fmaf(am, vm, bm));
+  if (ch == 0 && tid == 0) ws.khead[bh] = kh;
+  const int r = 256 * ch + tid;
+  if (r < T) {
+    const float f = ldexpf(1.f, kh);
+    const int64_t x = (int64_t)bh * T + r;
+    const float2 s = ws.stats[x];
+    ws.stats[x] = make_float2(s.x * f, s.y * f);
+  }
 }
 
 // ============================================================================
-// dQ: mirrors the forward (128 queries per block, 2 blocks per CU).
-//   S^T  = K16 Q16^T (+bias)  A = K16 (LDS rows)         B = Q16^T (VGPRs)
-//   dP^T = V dO^T             A = V   (LDS rows)         B = dO^T  (VGPRs)
-//   dQ^T += K16^T dS^T        A = K16^T (LDS transposed) B = dS^T  (from S^T, dP^T)
-// Each block also forms, for its own query rows, Delta_i = <dO_i, O_i> and
-// stats_i = (4 cinv_i, -4 cinv_i Delta_i), and writes stats, the fp16 copy of
-// Q (per-tile exponents in qexp) and the rows' dS bound (atomicMax into bmax)
-// for the dK / dV kernel, which runs after it.
+// dS^T tiles. The dK / dV kernel stores the fp16 dS it feeds its dK product
+// (2^kh dS, zero where a key is masked or past its query) for every 64-key x
+// 64-query tile (kt, qt) the backward touches: 64 key rows of 64 query columns,
+// row-major, 8 KB. Tiles are grouped by the dQ kernel's blocks of kQB query
+// tiles so that each dQ block streams one contiguous run: a head's runs follow
+// each other by query block qb, and within a run come, key tile by key tile
+// (kt = 0 .. the block's last, causal; every kt otherwise), the block's kQB
+// query tiles side by side (in causal mode the tiles with kt > qt inside a
+// run are not written and not read). Within each 32-query half of a tile the
+// columns follow the dK kernel's MFMA operand order: column 8 g + 4 h + j
+// holds query 16 h + 4 g + j.
 // ============================================================================
+constexpr int kQB = 4;  // 64-query tiles per dQ block
+
+__host__ __device__ inline int64_t ds_run_base(int qb, int nt, bool causal) {
+  return causal ? (int64_t)kQB * kQB * qb * (qb + 1) / 2 : (int64_t)qb * kQB * nt;
+}
+__host__ __device__ inline int64_t ds_tiles_per_head(int nt, bool causal) {
+  const int nqb = (nt + kQB - 1) / kQB;
+  return ds_run_base(nqb - 1, nt, causal) + (int64_t)kQB * nt;
+}
+__device__ __forceinline__ int64_t ds_tile(int kt, int qt, int nt, bool causal) {
+  return ds_run_base(qt / kQB, nt, causal) + (int64_t)kt * kQB + qt % kQB;
+}
+// query (0..31, within its half-tile) of column c of the half-tile
+__device__ __forceinline__ int ds_col_query(int c) { return 16 * ((c >> 2) & 1) + 4 * (c >> 3) + (c & 3); }
+
+// ============================================================================
+// dQ from the stored dS: 256 queries (kQB 64-query tiles) per block, 8 waves x
+// 32 queries, one block per CU; per 64-key tile
+//   dQ^T[d][q] += K16^T[d][key] dS^T[key][q]   A = K16^T (LDS transposed)
+//                                              B = dS^T  (LDS transposed)
+// A plain GEMM, bound by streaming the stored dS once: the block's dS run is
+// contiguous and read with non-temporal LDS-DMA, 32 KB per key tile beside the
+// 16 KB K16 tile, three key tiles deep (two in flight while one is worked).
+// Each XCD works its heads one after another (head-major) so that the K16
+// tiles its blocks share stay in its L2. dS carries the head's 2^kh and K16
+// its tile's 2^ek: the accumulators are rescaled when ek changes and the
+// epilogue multiplies by scale 2^-(kh + ek) (exact). Blocks cover the heads
+// bh0 .. bh0 + G - 1 (the dS tiles in the workspace).
+// ============================================================================
+constexpr int kDqW = 8;                 // waves per dQ block
+constexpr int kDqM = kQB * 64;          // queries per dQ block
+
+template <int D> struct DqSmem {
+  short k[3][kBN * D];          // K16 tiles
+  short s[3][kQB][64 * 64];     // dS^T tiles of the block's query tiles
+};
+
 template <typename T, int D, int MODE>
-__global__ __launch_bounds__(256, 2) void attn_bwd_dq_k(AttnArgs a, float2* __restrict__ stats,
-                                                        f16* __restrict__ q16, const f16* __restrict__ k16,
-                                                        const int* __restrict__ kexp, int* __restrict__ qexp,
-                                                        const float* __restrict__ vnrm,
-                                                        unsigned* __restrict__ bmax) {
+__global__ __launch_bounds__(512, 1) void attn_bwd_dq_k(AttnArgs a, const f16* __restrict__ k16,
+                                                        const int* __restrict__ kexp,
+                                                        const int* __restrict__ khead,
+                                                        const f16* __restrict__ dst, int bh0, int G) {
   typedef Mfma<T> M;
-  constexpr int KK = D / 32;
   constexpr int DS = D / 16;
   constexpr bool kCausal = (MODE & kModeCausal) != 0;
-  constexpr bool kKM = (MODE & kModeKeyMask) != 0;
-  __shared__ short sk[2][kBN * D];
-  __shared__ short sv[2][kBN * D];
+  typedef TileDma<D, kDqW> KDma;
+  typedef TileDma<64, kDqW, 64 * kQB> SDma;   // the kQB tiles of a key tile as one 256-row tile
+  constexpr int NDMA = KDma::SEGS + SDma::SEGS;  // DMA instructions per wave per key tile
+  __shared__ DqSmem<D> sm;
 
   const int T_ = a.T, H = a.H;
-  int bh, rank;
-  block_order((int)blockIdx.x, a.B * H, bh, rank);
-  const int n_qt = (T_ + kBM - 1) / kBM;
-  const int q0 = (n_qt - 1 - rank) * kBM;
+  const int n_qb = (T_ + kDqM - 1) / kDqM;
+  // head-major per XCD (block i runs on XCD i % 8): XCD x works heads x, x + 8,
+  // ... in turn, each head's blocks longest (most key tiles) first
+  int bl, rank;
+  if ((G & 7) == 0) {
+    const int x = (int)blockIdx.x & 7, slot = (int)blockIdx.x >> 3;
+    const int hi = slot / n_qb;
+    rank = slot - hi * n_qb;
+    bl = x + 8 * hi;
+  } else {
+    bl = (int)blockIdx.x / n_qb;
+    rank = (int)blockIdx.x - bl * n_qb;
+  }
+  const int bh = bh0 + bl;
+  const int qb = n_qb - 1 - rank;
+  const int q0 = qb * kDqM;
   const int b = bh / H, h = bh - b * H;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 4, li = lane & 15;
-  const int qw = q0 + kRows * w;
-
-  const T* qp = (const T*)a.q + b * a.sq[0] + h * a.sq[1];
+  const int nt = (T_ + 63) / 64;
+  const int qt0 = q0 >> 6;                  // the block's first 64-query tile
+  const int qtw = qt0 + (w >> 1);           // this wave's tile (columns 32 (w & 1) ..)
   const f16* kp = k16 + (int64_t)bh * T_ * D;
-  const T* vp = (const T*)a.v + b * a.sv[0] + h * a.sv[1];
-  const T* dop = (const T*)a.dout + b * a.sdo[0] + h * a.sdo[1];
-  const T* op = (const T*)a.o + b * a.so[0] + h * a.so[1];
-  const uint32_t sq2 = (uint32_t)a.sq[2], sv2 = (uint32_t)a.sv[2], sdo2 = (uint32_t)a.sdo[2];
-  const uint32_t so2 = (uint32_t)a.so[2];
-  const uint32_t kbytes = row_bytes(T_, D, D), vbytes = row_bytes(T_, sv2, D);
-  const float slope = a.slopes[h];
-  const float scale = a.scale;
-  const int nt = (T_ + 63) / 64;  // 64-row tiles of the head
+  const uint32_t kbytes = row_bytes(T_, D, D);
+  const f16* run = dst + ((int64_t)bl * ds_tiles_per_head(nt, kCausal) + ds_run_base(qb, nt, kCausal)) * 4096;
   const int* kexp_h = kexp + (int64_t)bh * nt;
-  const float* Lp = a.L + b * a.sl[0] + h * a.sl[1];
-  __shared__ float xq[kNW];  // max |q| per wave, for the Q16 tile exponents
+  const int n_kt = kCausal ? std::min(qt0 + kQB, nt) : nt;
 
-  // Range of the fp16 dS (dQ part): row q's dS enters dQ^T += K16^T dS^T as
-  // 2^k_q w (dP - Delta_q), w = t^3 r^2 <= 1.11, with k_q = ds_exp of a bound
-  // on it: |dP - Delta_q| <= ||dO_q||_2 max_j ||v_j||_2 + |Delta_q|. The row
-  // scale is undone per lane in the epilogue (dQ's columns are its queries),
-  // with the factor 4 cinv_q = 1 / (4 (L_q + eps)) the dS of the reference
-  // carries: dS = 4 cinv_q w (dP - Delta_q).
-  i16x8 qf[2][KK], dof[2][KK];
-  float c4[2], nc4d[2];  // 2^k_q and -2^k_q Delta_q for q = qw + 16 qs + li
-  float qmax = 0.f;
-  {
-    const __amdgpu_buffer_rsrc_t rq = rsrc(qp, row_bytes(T_, sq2, D));
-    const __amdgpu_buffer_rsrc_t rd = rsrc(dop, row_bytes(T_, sdo2, D));
-    const __amdgpu_buffer_rsrc_t ro = rsrc(op, row_bytes(T_, so2, D));
-    float mv = 0.f;  // max_j ||v_j||_2 of the head
-    for (int i = lane; i < nt; i += 64) mv = fmaxf(mv, vnrm[(int64_t)bh * nt + i]);
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mv = fmaxf(mv, __shfl_xor(mv, o, 64));
-    float bk = 0.f;  // the dK / dV kernel's bound on |dS| over this wave's rows
-#pragma unroll
-    for (int qs = 0; qs < 2; ++qs) {
-      const int qrow = qw + 16 * qs + li;
-      // Delta and ||dO||^2: lane (g, li) sums 32 of the row's D products, then across g
-      float dsum = 0.f, dsq = 0.f;
-#pragma unroll
-      for (int kk = 0; kk < KK; ++kk) {
-        qf[qs][kk] = load16(rq, ((uint32_t)qrow * sq2 + 32 * kk + 8 * g) * 2);
-        qmax = fmaxf(qmax, absmax8<T>(qf[qs][kk]));
-        dof[qs][kk] = load16(rd, ((uint32_t)qrow * sdo2 + 32 * kk + 8 * g) * 2);
-        const i16x8 ov = load16(ro, ((uint32_t)qrow * so2 + 32 * kk + 8 * g) * 2);
-        const VecT<T, 8> o8 = __builtin_bit_cast(VecT<T, 8>, ov), g8 = __builtin_bit_cast(VecT<T, 8>, dof[qs][kk]);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          dsum = fmaf((float)g8.v[e], (float)o8.v[e], dsum);
-          dsq = fmaf((float)g8.v[e], (float)g8.v[e], dsq);
-        }
-      }
-      dsum += __shfl_xor(dsum, 16, 64);
-      dsum += __shfl_xor(dsum, 32, 64);
-      dsq += __shfl_xor(dsq, 16, 64);
-      dsq += __shfl_xor(dsq, 32, 64);
-      const bool ok = qrow < T_;
-      const float dpb = fmaf(sqrtf(dsq), mv, fabsf(dsum));  // bound on |dP - Delta| of the row
-      c4[qs] = ok ? ldexpf(1.f, ds_exp(1.125f * dpb)) : 0.f;
-      nc4d[qs] = -c4[qs] * dsum;
-      if (ok) {
-        const float c4u = 1.f / (4.f * (Lp[(int64_t)qrow * a.sl[2]] + a.eps));
-        if (g == 0) stats[(int64_t)bh * T_ + qrow] = make_float2(c4u, -c4u * dsum);
-        // dK / dV kernel: |dS| = 4 cinv w |dP - Delta| = p g |dP - Delta| with
-        // p g <= 4 (p <= 1 when L is the forward's row sum)
-        bk = fmaxf(bk, fminf(4.1f, 1.125f * c4u) * dpb);
-      }
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      bk = fmaxf(bk, __shfl_xor(bk, o, 64));
-      qmax = fmaxf(qmax, __shfl_xor(qmax, o, 64));
-    }
-    if (lane == 0) {
-      atomicMax(bmax + bh, __float_as_uint(bk));  // non-negative floats order as their bits
-      xq[w] = qmax;
-    }
-  }
-  f32x4 cb;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) cb[j] = (slope / scale) * (float)(4 * g + j - li);
-  // bias in use and key validity of the current tile, as in the forward
-  f32x4 cbx = cb;
-  float sgn = 1.f;
-  // S^T comes out of the MFMA scaled by 2^(ek + eq) (the fp16 copies' tile
-  // exponents): the bias in cbx carries that factor and sc = scale 2^-(ek + eq)
-  // removes it; dqacc holds 2^ek times the sum (ek: the K16 tile in use)
-  int ek = 0;
-  float sc = scale;
-  uint64_t vm = ~0ull;
-  int kcur = 0;
-  const uint8_t* kmb = kKM ? a.km + (int64_t)b * a.skm : nullptr;
-
-  f32x4 dqacc[DS][2];
+  f32x4 acc[DS][2];
 #pragma unroll
   for (int ds = 0; ds < DS; ++ds)
 #pragma unroll
-    for (int qs = 0; qs < 2; ++qs) dqacc[ds][qs] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int qs = 0; qs < 2; ++qs) acc[ds][qs] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  TileDma<D, kNW> dk, dv;
+  KDma dk;
+  SDma dd;
   dk.init(w, lane, D);
-  dv.init(w, lane, sv2);
-
-  // S^T and dP^T of the 16 keys at tile rows hr .. hr + 15
-  auto m1 = [&](int hr, f32x4 (&s_)[2], f32x4 (&p_)[2], const short* ks_, const short* vs_) __attribute__((always_inline)) {
-#pragma unroll
-    for (int qs = 0; qs < 2; ++qs) {
-      s_[qs] = cbx;
-      p_[qs] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk) {
-      const i16x8 kf = lds16(ks_ + soff<D>(hr + li, 32 * kk + 8 * g));
-      const i16x8 vf = lds16(vs_ + soff<D>(hr + li, 32 * kk + 8 * g));
-#pragma unroll
-      for (int qs = 0; qs < 2; ++qs) {
-        s_[qs] = mma_f16(kf, qf[qs][kk], s_[qs]);
-        p_[qs] = M::mma(vf, dof[qs][kk], p_[qs]);
-      }
-    }
+  dd.init(w, lane, 64);
+  auto issue = [&](int buf, int kt) __attribute__((always_inline)) {
+    dk.issue(sm.k[buf], kp, kbytes, kt * kBN, D, w);
+    dd.template issue<true>(&sm.s[buf][0][0], run + (int64_t)kt * kQB * 4096, 8192u * kQB, 0, 64, w);
   };
-  // dS of those scores, packed fp16 as dS^T (MASKED as in the forward)
-  auto vh = [&](auto masked_tag, int kh, const f32x4 (&s_)[2], const f32x4 (&p_)[2], uint32_t (&pk)[2][2]) __attribute__((always_inline)) {
-    constexpr bool MASKED = decltype(masked_tag)::value;
-    constexpr bool kVM = kKM || !kCausal;
-    uint32_t nib = 0;
-    if constexpr (MASKED && kVM) nib = (uint32_t)(vm >> (kh - kcur + 4 * g));
-#pragma unroll
-    for (int qs = 0; qs < 2; ++qs) {
-      const float tterm = (kCausal ? slope : sgn * slope) * (float)(kh - qw - 16 * qs);
-      float d[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        float s = fmaf(s_[qs][j], sc, tterm);
-        if constexpr (MASKED && !kCausal) {
-          const float sd = sgn * (float)((kh + 4 * g + j) - (qw + 16 * qs + li));
-          if (sd > 0.f) s = fmaf(-2.f * slope, sd, s);
-        }
-        const float r = __builtin_amdgcn_rcpf(fabsf(s) + 1.f);
-        const float t = fmaf(s, r, 1.f);
-        const float u = t * r;
-        d[j] = (u * u * t) * fmaf(p_[qs][j], c4[qs], nc4d[qs]);
-        if (MASKED && kCausal && kh + 4 * g + j > qw + 16 * qs + li) d[j] = 0.f;
-        if (MASKED && kVM && !((nib >> j) & 1u)) d[j] = 0.f;
-      }
-      pk[qs][0] = pack2_f16(d[0], d[1]);
-      pk[qs][1] = pack2_f16(d[2], d[3]);
-    }
-  };
-  // dQ^T += K16^T dS^T over the 32 keys at tile rows r0 .. r0 + 31
-  auto m2 = [&](int r0, const uint32_t (&pa)[2][2], const uint32_t (&pb)[2][2], const short* ks_) __attribute__((always_inline)) {
-    i16x8 dsf[2];
-#pragma unroll
-    for (int qs = 0; qs < 2; ++qs) dsf[qs] = pack_frag(pa[qs][0], pa[qs][1], pb[qs][0], pb[qs][1]);
-#pragma unroll
-    for (int ds = 0; ds < DS; ++ds) {
-      const i16x8 kt = frag_tr<D>(ks_, r0, 16 * ds, g, li);
-#pragma unroll
-      for (int qs = 0; qs < 2; ++qs) dqacc[ds][qs] = mma_f16(kt, dsf[qs], dqacc[ds][qs]);
-    }
-  };
-  auto tile = [&](auto masked_tag, int k0, const short* ks_, const short* vs_) __attribute__((always_inline)) {
-    f32x4 sA[2], pA[2], sB[2], pB[2];
-    uint32_t da0[2][2], db0[2][2], da1[2][2], db1[2][2];
-    m1(0, sA, pA, ks_, vs_);
-    m1(16, sB, pB, ks_, vs_);
-    vh(masked_tag, k0, sA, pA, da0);
-    m1(32, sA, pA, ks_, vs_);
-    vh(masked_tag, k0 + 16, sB, pB, db0);
-    m2(0, da0, db0, ks_);
-    m1(48, sB, pB, ks_, vs_);
-    vh(masked_tag, k0 + 32, sA, pA, da1);
-    vh(masked_tag, k0 + 48, sB, pB, db1);
-    m2(32, da1, db1, ks_);
-  };
-  // which variant a tile takes. Causal without a padding mask: below the
-  // diagonal plain, straddling it masked, above it skipped. Otherwise a tile
-  // wholly on one side of the diagonal (causal: below it) with every key valid
-  // takes the plain path, a tile with no valid key is skipped, and any other
-  // tile takes the masked one; non-causal mode switches the bias sign at the
-  // first tile wholly above the diagonal.
-  auto tile_step = [&](int k0, const short* ks_, const short* vs_) __attribute__((always_inline)) {
-    if constexpr (kCausal && !kKM) {
-      if (k0 + kBN - 1 <= qw)
-        tile(std::false_type{}, k0, ks_, vs_);
-      else if (k0 <= qw + kRows - 1)
-        tile(std::true_type{}, k0, ks_, vs_);
-    } else {
-      bool plain;
-      if constexpr (kCausal) {
-        plain = k0 + kBN - 1 <= qw;
-      } else {
-        const bool above = k0 > qw + kRows - 1;
-        if (above && sgn > 0.f) {
-          cbx = -cbx;
-          sgn = -1.f;
-        }
-        plain = above || k0 + kBN - 1 <= qw;
-      }
-      plain = plain && vm == ~0ull;
-      if (vm == 0ull || (kCausal && k0 > qw + kRows - 1)) {
-      } else if (plain) {
-        tile(std::false_type{}, k0, ks_, vs_);
-      } else {
-        tile(std::true_type{}, k0, ks_, vs_);
-      }
-    }
-  };
-
-  const int n_kt = kCausal ? (std::min(q0 + kBM, T_) + kBN - 1) / kBN : (T_ + kBN - 1) / kBN;
-  auto kmbyte = [&](int kt) __attribute__((always_inline)) {
-    const int j = kt * kBN + lane;
-    return (kKM && j < T_) ? (uint32_t)kmb[j] : 0u;
-  };
-  uint32_t kmn = kmbyte(0);
-  dk.issue(sk[0], kp, kbytes, 0, D, w);
-  dv.issue(sv[0], vp, vbytes, 0, sv2, w);
-  dma_wait();
-  __syncthreads();
-  {
-    // Q16 = Q 2^eq with the exponent of this wave's 64-row tile (waves w and
-    // w ^ 1 hold its rows); the dK / dV kernel reads Q16 and qexp per tile
-    const int eq = tile_exp(fmaxf(xq[w], xq[w ^ 1]));
-    const float fq = ldexpf(1.f, eq);
-#pragma unroll
-    for (int qs = 0; qs < 2; ++qs) {
-      const int qrow = qw + 16 * qs + li;
-#pragma unroll
-      for (int kk = 0; kk < KK; ++kk) {
-        qf[qs][kk] = to_f16x8s<T>(qf[qs][kk], fq);
-        if (qrow < T_) *reinterpret_cast<i16x8*>(q16 + ((int64_t)bh * T_ + qrow) * D + 32 * kk + 8 * g) = qf[qs][kk];
-      }
-    }
-    if ((w & 1) == 0 && lane == 0 && qw < T_) qexp[(int64_t)bh * nt + (qw >> 6)] = eq;
-    cbx *= fq;
-    sc = ldexpf(scale, -eq);
+  int ek = 0;
+  issue(0, 0);
+  if (n_kt > 1) {
+    issue(1, 1);
+    __builtin_amdgcn_s_waitcnt(0x0F70 | NDMA);  // vmcnt(NDMA): tile 0 landed
+  } else {
+    dma_wait();
   }
-  // unrolled by two: static buffers (see the forward)
+  __syncthreads();
+  // unrolled by three: static buffers
   auto step = [&](int kt, auto buf_tag) __attribute__((always_inline)) {
     constexpr int buf = decltype(buf_tag)::value;
-    if (kt + 1 < n_kt) {
-      dk.issue(sk[buf ^ 1], kp, kbytes, (kt + 1) * kBN, D, w);
-      dv.issue(sv[buf ^ 1], vp, vbytes, (kt + 1) * kBN, sv2, w);
-    }
-    const int k0 = kt * kBN;
-    kcur = k0;
+    const bool ahead = kt + 2 < n_kt;
+    if (ahead) issue((buf + 2) % 3, kt + 2);
     const int ekt = kexp_h[kt];
     if (ekt != ek) {
-      // a K16 tile with another exponent: rescale the bias, sc and the
-      // accumulated dQ to it (powers of two: exact)
       const float f = ldexpf(1.f, ekt - ek);
-      cbx *= f;
-      sc = ldexpf(sc, ek - ekt);
 #pragma unroll
       for (int ds = 0; ds < DS; ++ds)
 #pragma unroll
-        for (int qs = 0; qs < 2; ++qs) dqacc[ds][qs] *= f;
+        for (int qs = 0; qs < 2; ++qs) acc[ds][qs] *= f;
       ek = ekt;
     }
-    if constexpr (kKM) {
-      vm = __builtin_amdgcn_ballot_w64(kmn != 0u);
-      if (kt + 1 < n_kt) kmn = kmbyte(kt + 1);
-    } else if constexpr (!kCausal) {
-      vm = T_ - k0 >= kBN ? ~0ull : (1ull << (T_ - k0)) - 1ull;
+    if (qtw < nt && (!kCausal || kt <= qtw)) {
+      const short* sd = sm.s[buf][w >> 1];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        i16x8 bq[2];
+#pragma unroll
+        for (int qs = 0; qs < 2; ++qs) bq[qs] = frag_tr<64>(sd, 32 * ks, 32 * (w & 1) + 16 * qs, g, li);
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds) {
+          const i16x8 at = frag_tr<D>(sm.k[buf], 32 * ks, 16 * ds, g, li);
+#pragma unroll
+          for (int qs = 0; qs < 2; ++qs) acc[ds][qs] = mma_f16(at, bq[qs], acc[ds][qs]);
+        }
+      }
     }
-    tile_step(k0, sk[buf], sv[buf]);
-    dma_wait();
+    // tile kt + 1 has landed (each wave waits for its own DMA; loads complete
+    // in order), and every wave is done with tile kt's buffers
+    if (ahead)
+      __builtin_amdgcn_s_waitcnt(0x0F70 | NDMA);
+    else
+      dma_wait();
     __syncthreads();
   };
-  for (int kt = 0; kt < n_kt; kt += 2) {
+  for (int kt = 0; kt < n_kt; kt += 3) {
     step(kt, std::integral_constant<int, 0>{});
     if (kt + 1 < n_kt) step(kt + 1, std::integral_constant<int, 1>{});
+    if (kt + 2 < n_kt) step(kt + 2, std::integral_constant<int, 2>{});
   }
 
   T* __restrict__ dqp = (T*)a.dq + b * a.sdq[0] + h * a.sdq[1];
+  const float osc = ldexpf(a.scale, -(khead[bh] + ek));
 #pragma unroll
   for (int qs = 0; qs < 2; ++qs) {
-    const int qrow = qw + 16 * qs + li;
+    const int qrow = q0 + kRows * w + ds_col_query(16 * qs + li);
     if (qrow < T_) {
       T* row = dqp + (int64_t)qrow * a.sdq[2];
-      // scale 4 cinv_q, with the row's dS exponent and the K16 tile exponent undone
-      const float c4u = 1.f / (4.f * (Lp[(int64_t)qrow * a.sl[2]] + a.eps));
-      const float osc = ldexpf(scale * c4u, -ek) / c4[qs];
 #pragma unroll
       for (int ds = 0; ds < DS; ++ds) {
-        const f32x4 o = dqacc[ds][qs];
+        const f32x4 o = acc[ds][qs];
         *reinterpret_cast<u32x2*>(row + 16 * ds + 4 * g) =
             u32x2{M::pack2(o[0] * osc, o[1] * osc), M::pack2(o[2] * osc, o[3] * osc)};
       }
@@ -758,18 +693,19 @@ template <typename T, int D, int MODE>
 __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float2* __restrict__ stats,
                                                          const f16* __restrict__ q16,
                                                          const int* __restrict__ qexp,
-                                                         const unsigned* __restrict__ bmax) {
+                                                         const int* __restrict__ khead,
+                                                         f16* __restrict__ dst, int bh0, int G) {
   typedef Mfma<T> M;
   constexpr int KK = D / 32;
   constexpr int DS = D / 16;
-  constexpr int NW = 2 * kNW;
   constexpr bool kCausal = (MODE & kModeCausal) != 0;
   constexpr bool kKM = (MODE & kModeKeyMask) != 0;
   __shared__ DkvSmem<D> sm;
 
   const int T_ = a.T, H = a.H;
-  int bh, rank;
-  block_order((int)blockIdx.x, a.B * H, bh, rank);  // rank 0: the first keys (most queries)
+  int bl, rank;
+  block_order((int)blockIdx.x, G, bl, rank);  // rank 0: the first keys (most queries)
+  const int bh = bh0 + bl;
   const int k0 = rank * kBM;
   const int b = bh / H, h = bh - b * H;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -789,10 +725,16 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
   const float slope = a.slopes[h];
   const float scale = a.scale;
   // the stats carry dS's 2^kh (stats.x = 2^kh 4 cinv); P takes 4 cinv / 16 = cinv / 4
-  const int kh = head_dsexp(bmax, bh);
+  const int kh = khead[bh];
   const float p4 = ldexpf(0.25f, -kh);
   const int nt = (T_ + 63) / 64;
   const int* qexp_h = qexp + (int64_t)bh * nt;
+  // D role: where this wave's dS^T goes (lane (g, li) of half-tile row
+  // 16 ks + li, columns 8 g .. 8 g + 7); tiles past the head's last are not kept
+  const int ktg = kw >> 6;
+  const bool dst_ok = ktg < nt;
+  f16* const dsh = dst + (int64_t)bl * ds_tiles_per_head(nt, kCausal) * 4096;
+  const uint32_t dso = (uint32_t)((32 * (grp & 1) + li) * 64 + 8 * g);
 
   // B operands: K16^T (P role) or V^T (D role) fragments; lane (g, li) holds row
   // kw + 16 ks + li, columns 32 kk + 8 g .. +7
@@ -862,17 +804,22 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) acc[ds][ks] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  TileDma<D, NW> dq_, do_;
+  // the P role's waves stage the tiles: the D role's waves then have no loads
+  // in flight inside the loop and never wait for their dS stores
+  TileDma<D, kNW> dq_, do_;
   dq_.init(w, lane, D);
   do_.init(w, lane, sdo2);
   // stats of a 64-query tile: 512 bytes, lanes 0..31 of wave 0
   const uint32_t st_off = (uint32_t)lane * 16u;
   auto issue = [&](int buf, int qrow0) __attribute__((always_inline)) {
-    dq_.issue(sm.q[buf], qp, qbytes, qrow0, D, w);
-    do_.issue(sm.o[buf], dop, obytes, qrow0, sdo2, w);
+    if (prole) {
+      dq_.issue(sm.q[buf], qp, qbytes, qrow0, D, w);
+      do_.issue(sm.o[buf], dop, obytes, qrow0, sdo2, w);
+    }
     if (w == 0 && lane < 32) {
       const uint32_t skip = (uint32_t)qrow0 * 8u;
-      dma16(rsrc_words((const char*)stp + skip, stbytes > skip ? stbytes - skip : 0u), sm.st[buf], st_off);
+      dma16(rsrc_words((const char*)stp + skip, stbytes > skip ? stbytes - skip : 0u), lds_addr(sm.st[buf]),
+            st_off);
     }
   };
 
@@ -960,7 +907,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
     return qbase + 32 * c >= kw + kRows - 1 || (!kCausal && kw > qbase + 32 * c + 31);
   };
   if (n_it > 0) issue(0, qbase);
-  dma_wait();
+  if (prole) dma_wait();
   __syncthreads();
   f32x4 dpA[2][2], dpB[2][2];  // D role: dP of the current and the next chunk
   if (!prole && needc(0)) {
@@ -1018,8 +965,8 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
       __syncthreads();
       if (it + 1 < n_it) issue(buf ^ 1, qbase + (it + 1) * kBN);
     } else {
-      // the next tile has landed (each wave waits for its own DMA)
-      dma_wait();
+      // the next tile has landed (each P-role wave waits for its own DMA)
+      if (prole) dma_wait();
       __syncthreads();
     }
     if (prole) {
@@ -1057,7 +1004,27 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
             dp[ks][1] = pack2_f16(dv[2], dv[3]);
           }
         }
+        if constexpr (kKM) {
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks)
+            if (!kval[ks]) pa[ks][0] = pa[ks][1] = pb[ks][0] = pb[ks][1] = 0u;
+        }
+        // dS^T for the dQ kernel: 16 bytes per lane and ks (streaming stores:
+        // the dQ kernel reads them back only after this kernel)
+        if (dst_ok) {
+          f16* const tb = dsh + ds_tile(ktg, qc >> 6, nt, kCausal) * 4096 + r0;
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks)
+            __builtin_nontemporal_store(pack_frag(pa[ks][0], pa[ks][1], pb[ks][0], pb[ks][1]),
+                                        reinterpret_cast<i16x8*>(tb + dso + 16 * 64 * ks));
+        }
         m2(std::false_type{}, r0, pa, pb, sm.q[buf]);
+      } else if (dst_ok && c < n_ch && (!kCausal || (c >> 1) >= (grp >> 1))) {
+        // a skipped chunk inside a kept tile: its dS is zero
+        f16* const tb = dsh + ds_tile(ktg, qc >> 6, nt, kCausal) * 4096 + r0;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+          __builtin_nontemporal_store(i16x8{0, 0, 0, 0, 0, 0, 0, 0}, reinterpret_cast<i16x8*>(tb + dso + 16 * 64 * ks));
       }
     }
   };
@@ -1096,46 +1063,53 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
 // ============================================================================
 bool attn_mfma_supported(int D) { return D == 64 || D == 128; }
 
-// Backward workspace: per-row stats (float2), the fp16 copies of Q and K
-// ([B*H][T][D] each), per-tile exponents of K16 and Q16 and V row-norm maxima
-// ([B*H][nt] each, nt = ceil(T / 64)), and the per-head dS bound (B*H words);
-// each part 256-byte aligned.
-struct BwdWs {
-  float2* stats;
-  f16* q16;
-  f16* k16;
-  int* kexp;
-  int* qexp;
-  float* vnrm;
-  unsigned* bmax;
-  size_t bytes;
-};
-static BwdWs bwd_ws(void* base, int64_t B, int64_t H, int64_t T, int64_t D) {
+// Backward workspace (each part 256-byte aligned): per-row stats (float2), the
+// fp16 copies of Q and K ([B*H][T][D] each), the per-tile exponents and bound
+// parts ([B*H][nt] each, nt = ceil(T / 64)), the per-head dS exponents, and the
+// dS^T tiles of `group` heads. The group is as many heads as fit ds_cap() bytes
+// of causal tiles (at least one, a multiple of 8 when there are 8 or more, so
+// that heads keep their XCD); a non-causal call, which keeps every tile, takes
+// as many heads as fit the same space (at least one head's full tile set).
+// KAT_ATTN_DS_CAP_BYTES overrides the 2 GiB default (tests use it to run
+// several groups at small sizes).
+static size_t ds_cap() {
+  const char* e = getenv("KAT_ATTN_DS_CAP_BYTES");
+  const long long v = e ? atoll(e) : 0;
+  return v > 0 ? (size_t)v : ((size_t)2 << 30);
+}
+
+static BwdWs bwd_ws(void* base, int64_t B, int64_t H, int64_t T, int64_t D, bool causal) {
   auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
-  const size_t rows = (size_t)(B * H * T), tiles = (size_t)(B * H) * (size_t)((T + 63) / 64);
+  const int64_t BH = B * H;
+  const int nt = (int)((T + 63) / 64);
+  const size_t rows = (size_t)(BH * T), tiles = (size_t)BH * (size_t)nt;
+  const size_t tri = (size_t)ds_tiles_per_head(nt, true) * 8192u, sq = (size_t)ds_tiles_per_head(nt, false) * 8192u;
+  int64_t gc = std::max<int64_t>(1, std::min<int64_t>(BH, (int64_t)(ds_cap() / tri)));
+  if (gc >= 8) gc &= ~(int64_t)7;
+  const size_t ds_bytes = std::max(gc * tri, sq);
+  int64_t gn = std::max<int64_t>(1, std::min<int64_t>(BH, (int64_t)(ds_bytes / sq)));
+  if (gn >= 8) gn &= ~(int64_t)7;
   char* p = reinterpret_cast<char*>(base);
   BwdWs w;
   size_t o = 0;
-  w.stats = reinterpret_cast<float2*>(p + o);
-  o += al(rows * sizeof(float2));
-  w.q16 = reinterpret_cast<f16*>(p + o);
-  o += al(rows * (size_t)D * sizeof(f16));
-  w.k16 = reinterpret_cast<f16*>(p + o);
-  o += al(rows * (size_t)D * sizeof(f16));
-  w.kexp = reinterpret_cast<int*>(p + o);
-  o += al(tiles * sizeof(int));
-  w.qexp = reinterpret_cast<int*>(p + o);
-  o += al(tiles * sizeof(int));
-  w.vnrm = reinterpret_cast<float*>(p + o);
-  o += al(tiles * sizeof(float));
-  w.bmax = reinterpret_cast<unsigned*>(p + o);
-  o += al((size_t)(B * H) * sizeof(unsigned));
+  auto take = [&](size_t n) { char* q = p + o; o += al(n); return q; };
+  w.stats = reinterpret_cast<float2*>(take(rows * sizeof(float2)));
+  w.q16 = reinterpret_cast<f16*>(take(rows * (size_t)D * sizeof(f16)));
+  w.k16 = reinterpret_cast<f16*>(take(rows * (size_t)D * sizeof(f16)));
+  w.kexp = reinterpret_cast<int*>(take(tiles * sizeof(int)));
+  w.qexp = reinterpret_cast<int*>(take(tiles * sizeof(int)));
+  w.vnrm = reinterpret_cast<float*>(take(tiles * sizeof(float)));
+  w.abnd = reinterpret_cast<float*>(take(tiles * sizeof(float)));
+  w.bbnd = reinterpret_cast<float*>(take(tiles * sizeof(float)));
+  w.khead = reinterpret_cast<int*>(take((size_t)BH * sizeof(int)));
+  w.dst = reinterpret_cast<f16*>(take(ds_bytes));
+  w.group = (int)(causal ? gc : gn);
   w.bytes = o;
   return w;
 }
 
 size_t attn_mfma_workspace(int64_t B, int64_t H, int64_t T, int64_t D) {
-  return bwd_ws(nullptr, B, H, T, D).bytes;
+  return bwd_ws(nullptr, B, H, T, D, true).bytes;
 }
 
 namespace {
@@ -1159,25 +1133,28 @@ template <typename T, int D, int MODE> int launch_fwd(const AttnArgs& a, hipStre
 
 template <typename T, int D, int MODE>
 int launch_bwd(const AttnArgs& a, void* ws, hipStream_t st) {
-  const BwdWs w = bwd_ws(ws, a.B, a.H, a.T, a.D);
-  const int64_t rows = (int64_t)a.B * a.H * a.T;
-  const int64_t tiles = (int64_t)a.B * a.H * ((a.T + 63) / 64);
-  // prep: K16 + per-tile exponents and V norms, clears the dS bounds
-  hipLaunchKernelGGL((attn_bwd_prep_k<T, D>), dim3((unsigned)tiles), dim3(256), 0, st, a, w.k16, w.kexp,
-                     w.vnrm, w.bmax);
+  constexpr bool kCausal = (MODE & kModeCausal) != 0;
+  const BwdWs w = bwd_ws(ws, a.B, a.H, a.T, a.D, kCausal);
+  const int BH = a.B * a.H;
+  const int64_t tiles = (int64_t)BH * ((a.T + 63) / 64);
+  // prep: fp16 copies, exponents, Delta and the row stats, the dS bound parts
+  hipLaunchKernelGGL((attn_bwd_prep_k<T, D>), dim3((unsigned)tiles), dim3(256), 0, st, a, w);
   if (int rc = check_launch("kat_attn_bwd (prep)")) return rc;
-  // dq also writes stats, q16 and qexp and raises the dS bounds, which the
-  // dK / dV kernel reads
-  const int64_t nt = (int64_t)((a.T + kBM - 1) / kBM) * a.B * a.H;
-  hipLaunchKernelGGL((attn_bwd_dq_k<T, D, MODE>), dim3((unsigned)nt), dim3(256), 0, st, a, w.stats, w.q16,
-                     w.k16, w.kexp, w.qexp, w.vnrm, w.bmax);
-  if (int rc = check_launch("kat_attn_bwd (dq, mfma)")) return rc;
-  hipLaunchKernelGGL(attn_bwd_stscale_k, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, st, w.stats,
-                     w.bmax, a.T, rows);
+  const int cpb = (a.T + 255) / 256;
+  hipLaunchKernelGGL(attn_bwd_stscale_k, dim3((unsigned)((int64_t)BH * cpb)), dim3(256), 0, st, w, a.T, cpb);
   if (int rc = check_launch("kat_attn_bwd (stats scale)")) return rc;
-  hipLaunchKernelGGL((attn_bwd_dkv_k<T, D, MODE>), dim3((unsigned)nt), dim3(512), 0, st, a, w.stats, w.q16,
-                     w.qexp, w.bmax);
-  return check_launch("kat_attn_bwd (dkv, mfma)");
+  // per group of heads: dK, dV (and the dS^T tiles), then dQ from those tiles
+  const int64_t nb = (a.T + kBM - 1) / kBM, nbq = (a.T + kDqM - 1) / kDqM;
+  for (int bh0 = 0; bh0 < BH; bh0 += w.group) {
+    const int G = std::min(w.group, BH - bh0);
+    hipLaunchKernelGGL((attn_bwd_dkv_k<T, D, MODE>), dim3((unsigned)(nb * G)), dim3(512), 0, st, a, w.stats, w.q16,
+                       w.qexp, w.khead, w.dst, bh0, G);
+    if (int rc = check_launch("kat_attn_bwd (dkv, mfma)")) return rc;
+    hipLaunchKernelGGL((attn_bwd_dq_k<T, D, MODE>), dim3((unsigned)(nbq * G)), dim3(512), 0, st, a, w.k16,
+                       w.kexp, w.khead, w.dst, bh0, G);
+    if (int rc = check_launch("kat_attn_bwd (dq, mfma)")) return rc;
+  }
+  return 0;
 }
 
 }  // namespace

@@ -156,12 +156,24 @@ __device__ __forceinline__ i32x4 rsrc_words(const void* base, uint32_t bytes) {
 // dma_wait() is the s_waitcnt builtin (vmcnt(0), expcnt and lgkmcnt left at
 // their maxima: 0x0F70 in the gfx9 encoding) rather than asm, so the compiler's
 // wait tracking also sees every earlier vector-memory load as complete.
-__device__ __forceinline__ void dma16(const i32x4& r, const void* lds, uint32_t voff) {
-  const uint32_t la = __builtin_amdgcn_readfirstlane(
-      (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)(lds));
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(la), "v"(voff),
-               "s"(r)
-               : "memory");
+// The LDS destination is a 32-bit LDS address (lds_addr of a __shared__ array
+// plus a wave-uniform offset), so that it stays in SGPRs.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)(p);
+}
+// NT: the non-temporal cache policy, for data read once (it is then evicted
+// first from L2 and does not displace tiles other blocks re-read).
+template <bool NT = false>
+__device__ __forceinline__ void dma16(const i32x4& r, uint32_t lds, uint32_t voff) {
+  const uint32_t la = __builtin_amdgcn_readfirstlane(lds);
+  if constexpr (NT)
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds" ::"s"(la), "v"(voff),
+                 "s"(r)
+                 : "memory");
+  else
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(la), "v"(voff),
+                 "s"(r)
+                 : "memory");
 }
 __device__ __forceinline__ void dma_wait() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
@@ -202,13 +214,14 @@ __device__ __forceinline__ i16x8 frag_tr(const short* tile, int r0, int c0, int 
   return i16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
-// Stage a 64-row tile (rows row0 .. row0 + 63 of a [rows][stride] matrix, D
-// columns) into a swizzled LDS tile with the NW waves of the block: each wave
-// issues 64 / RPS / NW DMA segments of RPS rows.
-template <int D, int NW> struct TileDma {
-  static constexpr int CPR = D / 8;           // 16-byte chunks per row
-  static constexpr int RPS = 64 / CPR;        // rows per 1 KB segment
-  static constexpr int SEGS = 64 / RPS / NW;  // segments per wave
+// Stage a ROWS-row tile (rows row0 .. row0 + ROWS - 1 of a [rows][stride]
+// matrix, D columns) into a swizzled LDS tile with the NW waves of the block:
+// each wave issues ROWS / RPS / NW DMA segments of RPS rows.
+template <int D, int NW, int ROWS = 64> struct TileDma {
+  static constexpr int CPR = D / 8;             // 16-byte chunks per row
+  static constexpr int RPS = 64 / CPR;          // rows per 1 KB segment
+  static constexpr int SEGS = ROWS / RPS / NW;  // segments per wave
+  static_assert(SEGS >= 1 && SEGS * RPS * NW == ROWS, "tile rows must split evenly over the waves");
   uint32_t off[SEGS];
   __device__ __forceinline__ void init(int w, int lane, uint32_t stride) {
 #pragma unroll
@@ -219,12 +232,14 @@ template <int D, int NW> struct TileDma {
     }
   }
   // base: first row of the matrix; bytes: its extent; row0: first tile row
+  template <bool NT = false>
   __device__ __forceinline__ void issue(short* tile, const void* base, uint32_t bytes, int row0,
                                         uint32_t stride, int w) const {
     const uint32_t skip = (uint32_t)row0 * stride * 2;
     const i32x4 r = rsrc_words((const char*)base + skip, bytes > skip ? bytes - skip : 0u);
+    const uint32_t l0 = lds_addr(tile) + (uint32_t)(__builtin_amdgcn_readfirstlane(w) * SEGS * RPS * D * 2);
 #pragma unroll
-    for (int u = 0; u < SEGS; ++u) dma16(r, tile + (w * SEGS + u) * RPS * D, off[u]);
+    for (int u = 0; u < SEGS; ++u) dma16<NT>(r, l0 + (uint32_t)(u * RPS * D * 2), off[u]);
   }
 };
 

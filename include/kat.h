@@ -158,7 +158,11 @@ int kat_attn_fwd(const void* q, const void* k, const void* v, void* out, float* 
                  const int64_t* strides, const int64_t* l_strides, float scale, float eps,
                  int causal, int dtype, void* stream);
 
-/* Workspace bytes kat_attn_bwd needs. */
+/* Workspace bytes kat_attn_bwd needs. On the MFMA path it holds, besides
+ * per-row and per-tile values and fp16 copies of Q and K, the fp16 dS tiles
+ * of a group of heads (the causal half of each head's T x T, 64 x 64 tiles;
+ * at most 2 GiB of them, or one head's; KAT_ATTN_DS_CAP_BYTES in the
+ * environment lowers the cap). */
 size_t kat_attn_bwd_workspace_size(int64_t B, int64_t H, int64_t T, int64_t D, int dtype);
 
 /* Gradients of kat_attn_fwd:
@@ -168,10 +172,11 @@ size_t kat_attn_bwd_workspace_size(int64_t B, int64_t H, int64_t T, int64_t D, i
  * strides: 24 int64 = (b, h, t) strides of q, k, v, out, dout, dq, dk, dv.
  * Replaces the host wrapper + the dq and dkv launches at backward.py:273-341
  * (kernels backward.py:62-158 and 165-266). Deterministic. On the MFMA path
- * dS, and the copies of Q and K its products take, enter the MFMA in fp16,
- * each with a power-of-two scale chosen from the data (per 64-row tile for Q
- * and K, from a bound on |dS| per row and per head for dS) and undone
- * exactly: the gradients are exactly equivariant under power-of-two scalings
+ * dS is computed once (by the dK/dV kernel, which stores it for dQ), and it
+ * and the copies of Q and K its products take enter the MFMA in fp16, each
+ * with a power-of-two scale chosen from the data (per 64-row tile for Q and
+ * K, from a bound on |dS| per head for dS) and undone exactly: the gradients
+ * are exactly equivariant under power-of-two scalings
  * of q, k, v and dout, and per-tile maxima of |q| and |k| in [2^-46, 2^55]
  * are covered. The dS bounds assume (out, L) are the forward's outputs for
  * (q, k, v), as the reference's derivation does. */

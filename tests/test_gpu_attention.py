@@ -344,3 +344,44 @@ def test_tiled_fallback_warns_once(gpu):
         F.rational_attention_forward(q, k, v, slopes, 0.17)
         q2, k2, v2, _ = _inputs(6, 1, 2, 40, 128, torch.bfloat16)
         F.rational_attention_forward(q2, k2, v2, slopes, 0.09)  # covered: no warning
+
+
+@pytest.mark.parametrize("mode", ["plain", "masked", "noncausal"])
+@pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 128), (torch.float16, 64)])
+def test_mfma_backward_head_groups_are_bit_identical(gpu, mode, dtype, D, monkeypatch):
+    # the backward keeps the dS^T tiles of one group of heads at a time in the
+    # workspace (dK/dV stores them, dQ reads them back); a small cap
+    # (KAT_ATTN_DS_CAP_BYTES) splits the heads into several groups, the last
+    # one short. The arithmetic per head is the same, so the gradients must be
+    # equal bit for bit to the one-group run.
+    from fastalgebraictransformer_amd.backward import _attn_bwd_into
+    from fastalgebraictransformer_amd.forward import _attn_fwd_into, _key_mask_arg
+    _pin_mfma(monkeypatch, D)
+    B, H, T = 2, 5, 300
+    q, k, v, do = _inputs(91 + D, B, H, T, D, dtype)
+    slopes = F.compute_alibi_slopes(H).to(dev)
+    scale = 1.0 / math.sqrt(D)
+    km, causal, ext = None, True, False
+    if mode != "plain":
+        ext, causal = True, mode == "masked"
+        m = torch.ones(B, T, dtype=torch.int32)
+        m[0, :70] = 0
+        m[1, 5::7] = 0
+        km = _key_mask_arg(m, B, T, dev)
+    o = torch.empty_like(q)
+    L = torch.empty(B, H, T, dtype=torch.float32, device=dev)
+    _attn_fwd_into(q, k, v, o, L, slopes, scale, causal, 1e-6, km, extended=ext)
+    runs = []
+    nt = (T + 63) // 64
+    for cap in (None, 3 * nt * nt * 8192):  # 3 heads of square (non-causal) tiles
+        if cap is None:
+            monkeypatch.delenv("KAT_ATTN_DS_CAP_BYTES", raising=False)
+        else:
+            monkeypatch.setenv("KAT_ATTN_DS_CAP_BYTES", str(cap))
+        g = [torch.full_like(q, float("nan")) for _ in range(3)]
+        _attn_bwd_into(q, k, v, o, L, do, *g, slopes, scale, causal, 1e-6, km, extended=ext)
+        torch.cuda.synchronize()
+        runs.append(g)
+    for name, a, b in zip(("dq", "dk", "dv"), *runs):
+        assert bool(torch.isfinite(a).all()), name
+        assert torch.equal(a, b), name
