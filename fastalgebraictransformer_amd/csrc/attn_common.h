@@ -43,7 +43,7 @@ template <typename T> int attn_bwd_generic(const AttnArgs& a, const float* delta
 // The backward runs its own prep pass; ws holds attn_mfma_workspace() bytes:
 // per-row stats (float2), fp16 copies of Q and K ([B*H][T][D] each), per-tile
 // exponents and dS-bound parts, per-head dS exponents, and the fp16 dS tiles
-// of a group of heads (at most 2 GiB of them, or one head's).
+// of a group of heads (at most 4 GiB of them, or one head's).
 template <typename T> int attn_fwd_mfma(const AttnArgs& a, hipStream_t st);
 template <typename T> int attn_bwd_mfma(const AttnArgs& a, void* ws, hipStream_t st);
 bool attn_mfma_supported(int D);

@@ -1070,12 +1070,12 @@ bool attn_mfma_supported(int D) { return D == 64 || D == 128; }
 // of causal tiles (at least one, a multiple of 8 when there are 8 or more, so
 // that heads keep their XCD); a non-causal call, which keeps every tile, takes
 // as many heads as fit the same space (at least one head's full tile set).
-// KAT_ATTN_DS_CAP_BYTES overrides the 2 GiB default (tests use it to run
+// KAT_ATTN_DS_CAP_BYTES overrides the 4 GiB default (tests use it to run
 // several groups at small sizes).
 static size_t ds_cap() {
   const char* e = getenv("KAT_ATTN_DS_CAP_BYTES");
   const long long v = e ? atoll(e) : 0;
-  return v > 0 ? (size_t)v : ((size_t)2 << 30);
+  return v > 0 ? (size_t)v : ((size_t)4 << 30);
 }
 
 static BwdWs bwd_ws(void* base, int64_t B, int64_t H, int64_t T, int64_t D, bool causal) {

@@ -161,7 +161,7 @@ int kat_attn_fwd(const void* q, const void* k, const void* v, void* out, float* 
 /* Workspace bytes kat_attn_bwd needs. On the MFMA path it holds, besides
  * per-row and per-tile values and fp16 copies of Q and K, the fp16 dS tiles
  * of a group of heads (the causal half of each head's T x T, 64 x 64 tiles;
- * at most 2 GiB of them, or one head's; KAT_ATTN_DS_CAP_BYTES in the
+ * at most 4 GiB of them, or one head's; KAT_ATTN_DS_CAP_BYTES in the
  * environment lowers the cap). */
 size_t kat_attn_bwd_workspace_size(int64_t B, int64_t H, int64_t T, int64_t D, int dtype);
 
