@@ -53,6 +53,20 @@ template <typename A> __device__ __forceinline__ A rsig(A x) {
   return A(0.5) * (x / (fabs(x) + A(1)) + A(1));
 }
 
+// a / b in the per-element maps of data of type T. bf16 / fp16 data (results
+// rounded to 8 or 11 significand bits) take v_rcp_f32 (1 ulp) and a multiply,
+// ~10 instructions fewer than the IEEE divide; fp32 / fp64 data keep the IEEE
+// divide (the reference's Triton `/` on fp32 is itself an approximate divide).
+template <typename T, typename A> __device__ __forceinline__ A ediv(A a, A b) {
+  if constexpr (sizeof(T) == 2 && sizeof(A) == 4)
+    return a * __builtin_amdgcn_rcpf(b);
+  else
+    return a / b;
+}
+template <typename T, typename A> __device__ __forceinline__ A rsig_t(A x) {
+  return A(0.5) * (ediv<T>(x, fabs(x) + A(1)) + A(1));
+}
+
 // ---------------------------------------------------------------------------
 // Wavefront (64-lane) butterfly reduction through cross-lane shuffles.
 // ---------------------------------------------------------------------------

@@ -42,8 +42,7 @@ template <typename T> struct Raw {
 // plain stores runs 1 read + 1 write in 43.8 us and 2 reads + 1 write in
 // 61.8 us, against 46.2 / 64.7 us with non-temporal stores and 47.5 / 69.9 us
 // with plain loads; the norm, residual-norm and SwiGLU steps gain 2-7% from the
-// plain stores. st_vec_nt keeps the non-temporal store for the softmax, whose
-// kernels measured slightly faster with it.
+// plain stores, the softmax step 3%.
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 template <typename T, int V>
 __device__ __forceinline__ VecT<T, V> ld_vec(const T* __restrict__ p) {
@@ -54,10 +53,6 @@ __device__ __forceinline__ VecT<T, V> ld_vec(const T* __restrict__ p) {
 template <typename T, int V>
 __device__ __forceinline__ void st_vec(T* __restrict__ p, const VecT<T, V>& v) {
   *reinterpret_cast<u32x4_t*>(p) = __builtin_bit_cast(u32x4_t, v);
-}
-template <typename T, int V>
-__device__ __forceinline__ void st_vec_nt(T* __restrict__ p, const VecT<T, V>& v) {
-  __builtin_nontemporal_store(__builtin_bit_cast(u32x4_t, v), reinterpret_cast<u32x4_t*>(p));
 }
 template <typename T, int V> __device__ __forceinline__ VecT<T, V> zero_vec() {
   VecT<T, V> z;
@@ -166,7 +161,7 @@ __global__ __launch_bounds__(kEwThreads) void swiglu_fwd_k(
       for (int i = 0; i < V; ++i) {
         const A gg = to_acc(gr[u].v[i]);
         const A vv = to_acc(vr[u].v[i]);
-        out.v[i] = from_acc<T>(gg * rsig(gg) * vv);  // fused_ops.py:224-227
+        out.v[i] = from_acc<T>(gg * rsig_t<T>(gg) * vv);  // fused_ops.py:224-227
       }
       st_vec<T, V>(o + row[u] * ldo + col[u], out);
     }
@@ -205,8 +200,8 @@ __global__ __launch_bounds__(kEwThreads) void swiglu_bwd_k(
         const A vv = to_acc(vr[u].v[i]);
         // fused_ops.py:276-285
         const A den = fabs(gg) + A(1);
-        const A sig = A(0.5) * (gg / den + A(1));
-        const A sd = A(0.5) / (den * den);
+        const A sig = A(0.5) * (ediv<T>(gg, den) + A(1));
+        const A sd = ediv<T>(A(0.5), den * den);
         ov.v[i] = from_acc<T>(y * gg * sig);
         og.v[i] = from_acc<T>(y * vv * (sig + gg * sd));
       }
@@ -241,7 +236,7 @@ __global__ __launch_bounds__(kEwThreads) void swiglu_fwd_scalar_k(
     for (int u = 0; u < kEwUnroll; ++u) {
       const int64_t c = c0 + u * kEwThreads;
       const A gg = to_acc(gr[u]), vv = to_acc(vr[u]);
-      if (c < cols) o[r * ldo + c] = from_acc<T>(gg * rsig(gg) * vv);  // fused_ops.py:224-227
+      if (c < cols) o[r * ldo + c] = from_acc<T>(gg * rsig_t<T>(gg) * vv);  // fused_ops.py:224-227
     }
   }
 }
@@ -268,8 +263,8 @@ __global__ __launch_bounds__(kEwThreads) void swiglu_bwd_scalar_k(
       const int64_t c = c0 + u * kEwThreads;
       const A y = to_acc(yr[u]), gg = to_acc(gr[u]), vv = to_acc(vr[u]);
       const A den = fabs(gg) + A(1);  // fused_ops.py:276-285
-      const A sig = A(0.5) * (gg / den + A(1));
-      const A sd = A(0.5) / (den * den);
+      const A sig = A(0.5) * (ediv<T>(gg, den) + A(1));
+      const A sd = ediv<T>(A(0.5), den * den);
       if (c < cols) {
         dv[r * lddv + c] = from_acc<T>(y * gg * sig);
         dg[r * lddg + c] = from_acc<T>(y * vv * (sig + gg * sd));
@@ -349,6 +344,21 @@ __device__ __forceinline__ void load_weight(const W* __restrict__ w, int n_cols,
   }
 }
 
+// g = 2 / ((|x| + 1)^2 (sigma(x) + eps)), the softmax backward's derivative
+// factor (fused_ops.py:179-187). With den = |x| + 1, sigma(x) + eps =
+// (0.5 (x + den) + eps den) / den, so g = 2 / (den (0.5 (x + den) + eps den)):
+// one reciprocal for bf16 / fp16 data; fp32 / fp64 data keep the reference's
+// form with IEEE divides.
+template <typename T, typename A> __device__ __forceinline__ A rsm_g(A x, A e) {
+  const A den = fabs(x) + A(1);
+  if constexpr (sizeof(T) == 2 && sizeof(A) == 4) {
+    return A(2) * __builtin_amdgcn_rcpf(den * fmaf(e, den, A(0.5) * (x + den)));
+  } else {
+    const A sig = A(0.5) * (x / den + A(1));
+    return A(2) / (den * den * (sig + e));
+  }
+}
+
 template <typename T, int NCH>
 __global__ __launch_bounds__(256) void rsoftmax_fwd_k(const T* __restrict__ x, T* __restrict__ p,
                                                       int64_t n_rows, int n_cols, int64_t ldx,
@@ -374,7 +384,7 @@ __global__ __launch_bounds__(256) void rsoftmax_fwd_k(const T* __restrict__ x, T
       const bool in = ((int)threadIdx.x + 256 * k) * V < n_cols;
 #pragma unroll
       for (int i = 0; i < V; ++i) {
-        const A sg = rsig(to_acc(cur[k].v[i]));  // fused_ops.py:81-86
+        const A sg = rsig_t<T>(to_acc(cur[k].v[i]));  // fused_ops.py:81-86
         const A s2 = sg * sg;
         f[k][i] = s2 * s2;
         sum += in ? f[k][i] : A(0);
@@ -390,7 +400,7 @@ __global__ __launch_bounds__(256) void rsoftmax_fwd_k(const T* __restrict__ x, T
         VecT<T, V> o;
 #pragma unroll
         for (int i = 0; i < V; ++i) o.v[i] = from_acc<T>(f[k][i] * inv);  // fused_ops.py:104
-        st_vec_nt<T, V>(pr + col, o);
+        st_vec<T, V>(pr + col, o);
       }
     }
 #pragma unroll
@@ -449,12 +459,10 @@ __global__ __launch_bounds__(256) void rsoftmax_bwd_k(const T* __restrict__ dy,
 #pragma unroll
         for (int i = 0; i < V; ++i) {
           const A xx = to_acc(cx[k].v[i]);
-          const A den = fabs(xx) + A(1);  // fused_ops.py:179-187
-          const A sig = A(0.5) * (xx / den + A(1));
-          const A g = A(2) / (den * den * (sig + e));
+          const A g = rsm_g<T>(xx, e);  // fused_ops.py:179-187
           o.v[i] = from_acc<T>(to_acc(cp[k].v[i]) * g * (to_acc(cy[k].v[i]) - dot));
         }
-        st_vec_nt<T, V>(dx + row * lddx + col, o);
+        st_vec<T, V>(dx + row * lddx + col, o);
       }
     }
 #pragma unroll
@@ -505,7 +513,7 @@ __global__ __launch_bounds__(256) void rsoftmax_fwd_w_k(const T* __restrict__ x,
     const bool in = (lane + 64 * k) * V < n_cols;
 #pragma unroll
     for (int i = 0; i < V; ++i) {
-      const A sg = rsig(to_acc(cur[k].v[i]));  // fused_ops.py:81-86
+      const A sg = rsig_t<T>(to_acc(cur[k].v[i]));  // fused_ops.py:81-86
       const A s2 = sg * sg;
       f[k][i] = s2 * s2;
       sum += in ? f[k][i] : A(0);
@@ -524,7 +532,7 @@ __global__ __launch_bounds__(256) void rsoftmax_fwd_w_k(const T* __restrict__ x,
 #pragma unroll
   for (int k = 0; k < NCH; ++k) {
     const int col = (lane + 64 * k) * V;
-    if (col < n_cols) st_vec_nt<T, V>(pr + col, o[k]);
+    if (col < n_cols) st_vec<T, V>(pr + col, o[k]);
   }
 }
 
@@ -559,15 +567,13 @@ __global__ __launch_bounds__(256) void rsoftmax_bwd_w_k(const T* __restrict__ dy
 #pragma unroll
     for (int i = 0; i < V; ++i) {
       const A xx = to_acc(cx[k].v[i]);
-      const A den = fabs(xx) + A(1);  // fused_ops.py:179-187
-      const A sig = A(0.5) * (xx / den + A(1));
-      const A g = A(2) / (den * den * (sig + e));
+      const A g = rsm_g<T>(xx, e);  // fused_ops.py:179-187
       o[k].v[i] = from_acc<T>(to_acc(cp[k].v[i]) * g * (to_acc(cy[k].v[i]) - dot));
     }
 #pragma unroll
   for (int k = 0; k < NCH; ++k) {
     const int col = (lane + 64 * k) * V;
-    if (col < n_cols) st_vec_nt<T, V>(dx + row * lddx + col, o[k]);
+    if (col < n_cols) st_vec<T, V>(dx + row * lddx + col, o[k]);
   }
 }
 
@@ -584,14 +590,14 @@ __global__ __launch_bounds__(256) void rsoftmax_fwd_mp_k(const T* __restrict__ x
     const T* xr = x + row * ldx;
     A sum = A(0);
     for (int c = threadIdx.x; c < n_cols; c += blockDim.x) {
-      const A s = rsig(to_acc(xr[c]));
+      const A s = rsig_t<T>(to_acc(xr[c]));
       const A s2 = s * s;
       sum += s2 * s2;
     }
     sum = block_sum(sum, sh);
     const A inv = A(1) / (sum + A(eps));
     for (int c = threadIdx.x; c < n_cols; c += blockDim.x) {
-      const A s = rsig(to_acc(xr[c]));
+      const A s = rsig_t<T>(to_acc(xr[c]));
       const A s2 = s * s;
       p[row * ldp + c] = from_acc<T>(s2 * s2 * inv);
     }
@@ -615,9 +621,7 @@ __global__ __launch_bounds__(256) void rsoftmax_bwd_mp_k(const T* __restrict__ d
     dot = block_sum(dot, sh);
     for (int c = threadIdx.x; c < n_cols; c += blockDim.x) {
       const A xx = to_acc(x[row * ldx + c]);
-      const A den = fabs(xx) + A(1);
-      const A sig = A(0.5) * (xx / den + A(1));
-      const A g = A(2) / (den * den * (sig + e));
+      const A g = rsm_g<T>(xx, e);  // fused_ops.py:179-187
       dx[row * lddx + c] =
           from_acc<T>(to_acc(p[row * ldp + c]) * g * (to_acc(dy[row * lddy + c]) - dot));
     }
