@@ -371,11 +371,13 @@ __global__ __launch_bounds__(256) void attn_bwd_prep_k(AttnArgs a, BwdWs ws) {
     kv[u] = qv[u] = i16x8{0, 0, 0, 0, 0, 0, 0, 0};
     float vs = 0.f, dsum = 0.f, dsq = 0.f;
     if (row < a.T) {
-      kv[u] = *reinterpret_cast<const i16x8*>(kp + (int64_t)row * a.sk[2] + d);
-      qv[u] = *reinterpret_cast<const i16x8*>(qp + (int64_t)row * a.sq[2] + d);
-      const VecT<T, 8> v8 = *reinterpret_cast<const VecT<T, 8>*>(vp + (int64_t)row * a.sv[2] + d);
-      const VecT<T, 8> o8 = *reinterpret_cast<const VecT<T, 8>*>(op + (int64_t)row * a.so[2] + d);
-      const VecT<T, 8> g8 = *reinterpret_cast<const VecT<T, 8>*>(dop + (int64_t)row * a.sdo[2] + d);
+      // every input row is read once here: non-temporal loads (streamed, not
+      // kept in L2)
+      kv[u] = ld_nt16(kp + (int64_t)row * a.sk[2] + d);
+      qv[u] = ld_nt16(qp + (int64_t)row * a.sq[2] + d);
+      const VecT<T, 8> v8 = __builtin_bit_cast(VecT<T, 8>, ld_nt16(vp + (int64_t)row * a.sv[2] + d));
+      const VecT<T, 8> o8 = __builtin_bit_cast(VecT<T, 8>, ld_nt16(op + (int64_t)row * a.so[2] + d));
+      const VecT<T, 8> g8 = __builtin_bit_cast(VecT<T, 8>, ld_nt16(dop + (int64_t)row * a.sdo[2] + d));
       km = fmaxf(km, absmax8<T>(kv[u]));
       qm = fmaxf(qm, absmax8<T>(qv[u]));
 #pragma unroll

@@ -197,6 +197,11 @@ template <int D> __device__ __forceinline__ int soff(int row, int col) {
 
 __device__ __forceinline__ i16x8 lds16(const short* p) { return *reinterpret_cast<const i16x8*>(p); }
 
+// 16-byte non-temporal global load (data read once)
+template <typename T> __device__ __forceinline__ i16x8 ld_nt16(const T* p) {
+  return __builtin_bit_cast(i16x8, __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(p)));
+}
+
 // Transposing LDS read (ds_read_b64_tr_b16): within each 16-lane group, result
 // lane i element j is element i % 4 of the 8 bytes addressed by lane i / 4 + 4 j.
 __device__ __forceinline__ i16x4 lds_tr(const short* p) {
