@@ -385,3 +385,32 @@ def test_mfma_backward_head_groups_are_bit_identical(gpu, mode, dtype, D, monkey
     for name, a, b in zip(("dq", "dk", "dv"), *runs):
         assert bool(torch.isfinite(a).all()), name
         assert torch.equal(a, b), name
+
+
+def test_mfma_long_sequence_matches_fp32_tiled(gpu, monkeypatch):
+    # T = 16384: the backward's stored dS tiles grow as T^2 (2176 x 16 tiles
+    # per head here); the MFMA path against the fp32 tiled kernels on the same
+    # (bf16-rounded) inputs, an independent implementation, at the bf16 bar;
+    # and one head per dS group (a 1-byte cap) must give the same bits
+    B, H, T, D = 1, 2, 16384, 128
+    q, k, v, do = _inputs(101, B, H, T, D, torch.bfloat16)
+    slopes = F.compute_alibi_slopes(H).to(dev)
+    scale = 1.0 / math.sqrt(D)
+    _pin_mfma(monkeypatch, D)
+    o_m, L_m = F.rational_attention_forward(q, k, v, slopes, scale)
+    g_m = F.rational_attention_backward(q, k, v, o_m, L_m, do, slopes, scale)
+    monkeypatch.setenv("KAT_ATTN_DS_CAP_BYTES", "1")
+    g_1 = F.rational_attention_backward(q, k, v, o_m, L_m, do, slopes, scale)
+    monkeypatch.delenv("KAT_ATTN_DS_CAP_BYTES")
+    for a, b, n in zip(g_m, g_1, ("dq", "dk", "dv")):
+        assert torch.equal(a, b), n
+    monkeypatch.setenv("KAT_ATTN_IMPL", "tiled")
+    f32 = [t.float() for t in (q, k, v, do)]
+    o_t, L_t = F.rational_attention_forward(f32[0], f32[1], f32[2], slopes, scale)
+    g_t = F.rational_attention_backward(f32[0], f32[1], f32[2], o_m.float(), L_m, f32[3], slopes, scale)
+    torch.cuda.synchronize()
+    assert _rel_max(L_m, L_t) <= 1e-3
+    errs = {"o": assert_lowp(o_m, o_t, torch.bfloat16, "o")}
+    for n, x, y in zip(("dq", "dk", "dv"), g_m, g_t):
+        errs[n] = assert_lowp(x, y, torch.bfloat16, n)
+    print("T = 16384 vs fp32 tiled: " + ", ".join(f"{n} {e:.3e} / {r:.3e}" for n, (e, r) in errs.items()))
