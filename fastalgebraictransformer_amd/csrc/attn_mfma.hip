@@ -499,7 +499,7 @@ __global__ __launch_bounds__(256) void attn_bwd_stscale_k(BwdWs ws, int T, int c
 // columns follow the dK kernel's MFMA operand order: column 8 g + 4 h + j
 // holds query 16 h + 4 g + j.
 // ============================================================================
-constexpr int kQB = 4;  // 64-query tiles per dQ block
+constexpr int kQB = 8;  // 64-query tiles per dQ block
 
 __host__ __device__ inline int64_t ds_run_base(int qb, int nt, bool causal) {
   return causal ? (int64_t)kQB * kQB * qb * (qb + 1) / 2 : (int64_t)qb * kQB * nt;
@@ -515,40 +515,46 @@ __device__ __forceinline__ int64_t ds_tile(int kt, int qt, int nt, bool causal) 
 __device__ __forceinline__ int ds_col_query(int c) { return 16 * ((c >> 2) & 1) + 4 * (c >> 3) + (c & 3); }
 
 // ============================================================================
-// dQ from the stored dS: 256 queries (kQB 64-query tiles) per block, 8 waves x
-// 32 queries, one block per CU; per 64-key tile
+// dQ from the stored dS: 512 queries (kQB 64-query tiles) per block, 8 waves,
+// each owning one 64-query tile, one block per CU; per 32-key half of a key
+// tile
 //   dQ^T[d][q] += K16^T[d][key] dS^T[key][q]   A = K16^T (LDS transposed)
 //                                              B = dS^T  (LDS transposed)
-// A plain GEMM, bound by streaming the stored dS once: the block's dS run is
-// contiguous and read with non-temporal LDS-DMA, 32 KB per key tile beside the
-// 16 KB K16 tile, three key tiles deep (two in flight while one is worked).
-// Blocks take the forward's order (heads pinned to XCDs, longest blocks first
-// across the XCD's heads): ordering each XCD's heads one after another instead,
-// to keep a head's K16 tiles in L2, left a tail of long blocks that started
-// last (285 vs 241 us at config 3). dS carries the head's 2^kh and K16
+// A plain GEMM, bound by streaming the stored dS once. Each wave stages its
+// own dS rows (from the block's contiguous run, non-temporal LDS-DMA) and the
+// block shares the K16 rows, 32 keys per stage, four stages deep (three in
+// flight while one is worked); a stage issues the same number of DMA
+// instructions per wave whatever it holds (rows a wave does not need come
+// through an empty resource: zeros, no memory access), so that one vmcnt value
+// waits for the oldest stage. Each K16 fragment read from LDS feeds four
+// MFMAs. Blocks take the forward's order (heads pinned to XCDs, longest
+// blocks first across the XCD's heads). dS carries the head's 2^kh and K16
 // its tile's 2^ek: the accumulators are rescaled when ek changes and the
 // epilogue multiplies by scale 2^-(kh + ek) (exact). Blocks cover the heads
 // bh0 .. bh0 + G - 1 (the dS tiles in the workspace).
 // ============================================================================
-constexpr int kDqW = 8;                 // waves per dQ block
-constexpr int kDqM = kQB * 64;          // queries per dQ block
+constexpr int kDqW = kQB;           // waves per dQ block, one 64-query tile each
+constexpr int kDqM = kQB * 64;      // queries per dQ block
+constexpr int kDqS = 4;             // stages (32 keys each)
 
 template <int D> struct DqSmem {
-  short k[3][kBN * D];          // K16 tiles
-  short s[3][kQB][64 * 64];     // dS^T tiles of the block's query tiles
+  short k[kDqS][32 * D];          // K16 rows
+  short s[kDqS][kDqW][32 * 64];   // each wave's dS^T rows
 };
 
 template <typename T, int D, int MODE>
-__global__ __launch_bounds__(512, 1) void attn_bwd_dq_k(AttnArgs a, const f16* __restrict__ k16,
-                                                        const int* __restrict__ kexp,
-                                                        const int* __restrict__ khead,
-                                                        const f16* __restrict__ dst, int bh0, int G) {
+__global__ __launch_bounds__(64 * kDqW, 1) void attn_bwd_dq_k(AttnArgs a, const f16* __restrict__ k16,
+                                                              const int* __restrict__ kexp,
+                                                              const int* __restrict__ khead,
+                                                              const f16* __restrict__ dst, int bh0, int G) {
   typedef Mfma<T> M;
   constexpr int DS = D / 16;
   constexpr bool kCausal = (MODE & kModeCausal) != 0;
-  typedef TileDma<D, kDqW> KDma;
-  typedef TileDma<64, kDqW, 64 * kQB> SDma;   // the kQB tiles of a key tile as one 256-row tile
-  constexpr int NDMA = KDma::SEGS + SDma::SEGS;  // DMA instructions per wave per key tile
+  // K16 rows: 1 KB DMA segments over the first KW waves (all 8 at D = 128,
+  // 4 at D = 64); dS rows: each wave its own
+  constexpr int KW = std::min(kDqW, 32 * D / 512);
+  typedef TileDma<D, KW, 32> KDma;
+  typedef TileDma<64, 1, 32> SDma;
   __shared__ DqSmem<D> sm;
 
   const int T_ = a.T, H = a.H;
@@ -562,90 +568,105 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dq_k(AttnArgs a, const f16* _
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 4, li = lane & 15;
   const int nt = (T_ + 63) / 64;
-  const int qt0 = q0 >> 6;                  // the block's first 64-query tile
-  const int qtw = qt0 + (w >> 1);           // this wave's tile (columns 32 (w & 1) ..)
+  const int qtw = (q0 >> 6) + w;            // this wave's 64-query tile
+  const bool wact = qtw < nt;
   const f16* kp = k16 + (int64_t)bh * T_ * D;
   const uint32_t kbytes = row_bytes(T_, D, D);
   const f16* run = dst + ((int64_t)bl * ds_tiles_per_head(nt, kCausal) + ds_run_base(qb, nt, kCausal)) * 4096;
   const int* kexp_h = kexp + (int64_t)bh * nt;
-  const int n_kt = kCausal ? std::min(qt0 + kQB, nt) : nt;
+  const int n_kt = kCausal ? std::min((q0 >> 6) + kDqW, nt) : nt;
+  const int n_st = 2 * n_kt;                // stages: 32-key halves
+  const bool kw_ = w < KW;
+  const int ndma = (kw_ ? KDma::SEGS : 0) + SDma::SEGS;  // this wave's DMA per stage
 
-  f32x4 acc[DS][2];
+  f32x4 acc[DS][4];  // [d subtile][16-query column group]
 #pragma unroll
   for (int ds = 0; ds < DS; ++ds)
 #pragma unroll
-    for (int qs = 0; qs < 2; ++qs) acc[ds][qs] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int qc = 0; qc < 4; ++qc) acc[ds][qc] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   KDma dk;
-  SDma dd;
-  dk.init(w, lane, D);
-  dd.init(w, lane, 64);
-  auto issue = [&](int buf, int kt) __attribute__((always_inline)) {
-    dk.issue(sm.k[buf], kp, kbytes, kt * kBN, D, w);
-    dd.template issue<true>(&sm.s[buf][0][0], run + (int64_t)kt * kQB * 4096, 8192u * kQB, 0, 64, w);
+  SDma dd;  // the wave's own dS rows
+  dk.init(kw_ ? w : 0, lane, D);
+  dd.init(0, lane, 64);
+  auto tile_in = [&](int kt) __attribute__((always_inline)) { return wact && (!kCausal || kt <= qtw); };
+  // stage st: rows 32 (st & 1) .. of key tile st >> 1
+  auto issue = [&](int buf, int st) __attribute__((always_inline)) {
+    const int kt = st >> 1;
+    if (kw_) dk.issue(sm.k[buf], kp, kbytes, 32 * st, D, w);
+    const bool have = tile_in(kt);
+    dd.template issue<true>(sm.s[buf][w], run + (have ? ((int64_t)kt * kQB + w) * 4096 : 0), have ? 8192u : 0u,
+                            32 * (st & 1), 64, 0);
+  };
+  // stage st has landed when at most the stages issued after it are in flight
+  // (loads complete in order); the count is an immediate
+  auto wait_for = [&](int st) __attribute__((always_inline)) {
+    const int after = std::min(n_st - 1 - st, kDqS - 2) * ndma;
+    switch (after) {
+      case 2 * (KDma::SEGS + SDma::SEGS): __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * (KDma::SEGS + SDma::SEGS))); break;
+      case KDma::SEGS + SDma::SEGS: __builtin_amdgcn_s_waitcnt(0x0F70 | (KDma::SEGS + SDma::SEGS)); break;
+      case 2 * SDma::SEGS: __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * SDma::SEGS)); break;
+      case SDma::SEGS: __builtin_amdgcn_s_waitcnt(0x0F70 | SDma::SEGS); break;
+      default: dma_wait();
+    }
   };
   int ek = 0;
-  issue(0, 0);
-  if (n_kt > 1) {
-    issue(1, 1);
-    __builtin_amdgcn_s_waitcnt(0x0F70 | NDMA);  // vmcnt(NDMA): tile 0 landed
-  } else {
-    dma_wait();
-  }
+  for (int st = 0; st < kDqS - 1; ++st)
+    if (st < n_st) issue(st, st);
+  wait_for(0);
   __syncthreads();
-  // unrolled by three: static buffers
-  auto step = [&](int kt, auto buf_tag) __attribute__((always_inline)) {
+  // unrolled by four: static buffers
+  auto step = [&](int st, auto buf_tag) __attribute__((always_inline)) {
     constexpr int buf = decltype(buf_tag)::value;
-    const bool ahead = kt + 2 < n_kt;
-    if (ahead) issue((buf + 2) % 3, kt + 2);
-    const int ekt = kexp_h[kt];
-    if (ekt != ek) {
-      const float f = ldexpf(1.f, ekt - ek);
+    if (st + kDqS - 1 < n_st) issue((buf + kDqS - 1) % kDqS, st + kDqS - 1);
+    const int kt = st >> 1;
+    if constexpr ((buf & 1) == 0) {
+      const int ekt = kexp_h[kt];
+      if (ekt != ek) {
+        const float f = ldexpf(1.f, ekt - ek);
 #pragma unroll
-      for (int ds = 0; ds < DS; ++ds)
+        for (int ds = 0; ds < DS; ++ds)
 #pragma unroll
-        for (int qs = 0; qs < 2; ++qs) acc[ds][qs] *= f;
-      ek = ekt;
-    }
-    if (qtw < nt && (!kCausal || kt <= qtw)) {
-      const short* sd = sm.s[buf][w >> 1];
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        i16x8 bq[2];
-#pragma unroll
-        for (int qs = 0; qs < 2; ++qs) bq[qs] = frag_tr<64>(sd, 32 * ks, 32 * (w & 1) + 16 * qs, g, li);
-#pragma unroll
-        for (int ds = 0; ds < DS; ++ds) {
-          const i16x8 at = frag_tr<D>(sm.k[buf], 32 * ks, 16 * ds, g, li);
-#pragma unroll
-          for (int qs = 0; qs < 2; ++qs) acc[ds][qs] = mma_f16(at, bq[qs], acc[ds][qs]);
-        }
+          for (int qc = 0; qc < 4; ++qc) acc[ds][qc] *= f;
+        ek = ekt;
       }
     }
-    // tile kt + 1 has landed (each wave waits for its own DMA; loads complete
-    // in order), and every wave is done with tile kt's buffers
-    if (ahead)
-      __builtin_amdgcn_s_waitcnt(0x0F70 | NDMA);
-    else
-      dma_wait();
+    if (tile_in(kt)) {
+      const short* sd = sm.s[buf][w];
+      i16x8 bq[4];
+#pragma unroll
+      for (int qc = 0; qc < 4; ++qc) bq[qc] = frag_tr<64>(sd, 0, 16 * qc, g, li);
+#pragma unroll
+      for (int ds = 0; ds < DS; ++ds) {
+        const i16x8 at = frag_tr<D>(sm.k[buf], 0, 16 * ds, g, li);
+#pragma unroll
+        for (int qc = 0; qc < 4; ++qc) acc[ds][qc] = mma_f16(at, bq[qc], acc[ds][qc]);
+      }
+    }
+    // the next stage has landed, and every wave is done with this stage's buffers
+    if (st + 1 < n_st) wait_for(st + 1);
     __syncthreads();
   };
-  for (int kt = 0; kt < n_kt; kt += 3) {
-    step(kt, std::integral_constant<int, 0>{});
-    if (kt + 1 < n_kt) step(kt + 1, std::integral_constant<int, 1>{});
-    if (kt + 2 < n_kt) step(kt + 2, std::integral_constant<int, 2>{});
+  for (int st = 0; st < n_st; st += 4) {
+    step(st, std::integral_constant<int, 0>{});
+    step(st + 1, std::integral_constant<int, 1>{});
+    if (st + 2 < n_st) {
+      step(st + 2, std::integral_constant<int, 2>{});
+      step(st + 3, std::integral_constant<int, 3>{});
+    }
   }
 
   T* __restrict__ dqp = (T*)a.dq + b * a.sdq[0] + h * a.sdq[1];
   const float osc = ldexpf(a.scale, -(khead[bh] + ek));
 #pragma unroll
-  for (int qs = 0; qs < 2; ++qs) {
-    const int qrow = q0 + kRows * w + ds_col_query(16 * qs + li);
+  for (int qc = 0; qc < 4; ++qc) {
+    // column 16 qc + li of the tile: half (qc >> 1), column 16 (qc & 1) + li in it
+    const int qrow = 64 * qtw + 32 * (qc >> 1) + ds_col_query(16 * (qc & 1) + li);
     if (qrow < T_) {
       T* row = dqp + (int64_t)qrow * a.sdq[2];
 #pragma unroll
       for (int ds = 0; ds < DS; ++ds) {
-        const f32x4 o = acc[ds][qs];
+        const f32x4 o = acc[ds][qc];
         *reinterpret_cast<u32x2*>(row + 16 * ds + 4 * g) =
             u32x2{M::pack2(o[0] * osc, o[1] * osc), M::pack2(o[2] * osc, o[3] * osc)};
       }
@@ -1144,7 +1165,7 @@ int launch_bwd(const AttnArgs& a, void* ws, hipStream_t st) {
     hipLaunchKernelGGL((attn_bwd_dkv_k<T, D, MODE>), dim3((unsigned)(nb * G)), dim3(512), 0, st, a, w.stats, w.q16,
                        w.qexp, w.khead, w.dst, bh0, G);
     if (int rc = check_launch("kat_attn_bwd (dkv, mfma)")) return rc;
-    hipLaunchKernelGGL((attn_bwd_dq_k<T, D, MODE>), dim3((unsigned)(nbq * G)), dim3(512), 0, st, a, w.k16,
+    hipLaunchKernelGGL((attn_bwd_dq_k<T, D, MODE>), dim3((unsigned)(nbq * G)), dim3(64 * kDqW), 0, st, a, w.k16,
                        w.kexp, w.khead, w.dst, bh0, G);
     if (int rc = check_launch("kat_attn_bwd (dq, mfma)")) return rc;
   }

@@ -373,7 +373,8 @@ def test_mfma_backward_head_groups_are_bit_identical(gpu, mode, dtype, D, monkey
     _attn_fwd_into(q, k, v, o, L, slopes, scale, causal, 1e-6, km, extended=ext)
     runs = []
     nt = (T + 63) // 64
-    for cap in (None, 3 * nt * nt * 8192):  # 3 heads of square (non-causal) tiles
+    # T < 512: one dQ block (8 query tiles) per head, 8 x nt dS tiles of 8 KB
+    for cap in (None, 3 * 8 * nt * 8192):  # groups of 3, 3, 3, 1 heads
         if cap is None:
             monkeypatch.delenv("KAT_ATTN_DS_CAP_BYTES", raising=False)
         else:
@@ -388,7 +389,7 @@ def test_mfma_backward_head_groups_are_bit_identical(gpu, mode, dtype, D, monkey
 
 
 def test_mfma_long_sequence_matches_fp32_tiled(gpu, monkeypatch):
-    # T = 16384: the backward's stored dS tiles grow as T^2 (2176 x 16 tiles
+    # T = 16384: the backward's stored dS tiles grow as T^2 (33792 tiles
     # per head here); the MFMA path against the fp32 tiled kernels on the same
     # (bf16-rounded) inputs, an independent implementation, at the bf16 bar;
     # and one head per dS group (a 1-byte cap) must give the same bits
