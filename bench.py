@@ -241,6 +241,22 @@ def device_info(torch, lib):
         if rc != 0:
             raise RuntimeError("kat_probe_mfma_bf16 failed")
         best = max(best, flops.value / (e0.elapsed_time(e1) * 1e-3) / 1e12)
+    # the same loop on random operands, two waves per SIMD, ~4 ms per launch so
+    # that the clock settles: the MFMA rate real (toggling) data sustains
+    rblocks, riters = cus, 10000
+    rout = torch.empty(rblocks * 512, dtype=torch.float32, device=dev)
+    rates = []
+    for _ in range(3):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        rc = lib.kat_probe_mfma_bf16_random(ctypes.c_void_p(rout.data_ptr()), rblocks, riters,
+                                            ctypes.byref(flops), stream)
+        e1.record()
+        torch.cuda.synchronize()
+        if rc != 0:
+            raise RuntimeError("kat_probe_mfma_bf16_random failed")
+        rates.append(flops.value / (e0.elapsed_time(e1) * 1e-3) / 1e12)
+    rand_tflops = sorted(rates)[1]
     n = 1 << 29
     x = torch.ones(n, dtype=torch.bfloat16, device=dev)
     y = torch.empty_like(x)
@@ -254,9 +270,10 @@ def device_info(torch, lib):
         torch.cuda.synchronize()
         ts.append(e0.elapsed_time(e1))
     copy_gbs = 4 * n / (min(ts) * 1e-3) / 1e9  # 2 bytes read + 2 written per element
-    del x, y, out
+    del x, y, out, rout
     return {"name": props.name, "arch": getattr(props, "gcnArchName", ""), "cus": cus,
             "mfma_bf16_loop_tflops": round(best, 1),
+            "mfma_bf16_random_operand_loop_tflops": round(rand_tflops, 1),
             "mfma_bf16_spec_tflops": PEAK_BF16_TFLOPS, "copy_1GiB_GBs": round(copy_gbs, 1),
             "hbm_spec_GBs": PEAK_HBM_GBS}
 

@@ -57,6 +57,7 @@ _SIGNATURES = {
     "kat_attn_decode_noalloc": ([_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64P, _F, _F,
                                  _INT, _P], _INT),
     "kat_probe_mfma_bf16": ([_P, _INT, _INT, ctypes.POINTER(ctypes.c_double), _P], _INT),
+    "kat_probe_mfma_bf16_random": ([_P, _INT, _INT, ctypes.POINTER(ctypes.c_double), _P], _INT),
 }
 
 EXPORTED = tuple(_SIGNATURES)

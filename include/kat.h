@@ -260,6 +260,14 @@ int kat_attn_decode_noalloc(const void* q, const void* k, const void* v, void* o
  * ---------------------------------------------------------------------- */
 int kat_probe_mfma_bf16(float* out, int blocks, int iters, double* flops, void* stream);
 
+/* The same loop on random bf16 operands (eight operand pairs per lane, uniform
+ * in [-1, 1), taken in turn) with two waves per SIMD: `blocks` x 512 threads,
+ * `out` receives blocks * 512 floats. Data that toggles like real operands
+ * draws more power than the low-entropy operands above, and the sustained rate
+ * is what the chip's power management allows (no counterpart in the
+ * reference; bench.py reports it beside the spec peak). */
+int kat_probe_mfma_bf16_random(float* out, int blocks, int iters, double* flops, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
