@@ -898,15 +898,26 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
     i16x8 bf2[2];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) bf2[ks] = pack_frag(pa[ks][0], pa[ks][1], pb[ks][0], pb[ks][1]);
+    i16x8 at[DS];
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds) at[ds] = frag_tr<D>(as_, r0, 16 * ds, g, li);
 #pragma unroll
     for (int ds = 0; ds < DS; ++ds) {
-      const i16x8 at = frag_tr<D>(as_, r0, 16 * ds, g, li);
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        if constexpr (P) acc[ds][ks] = M::mma(at, bf2[ks], acc[ds][ks]);
-        else acc[ds][ks] = mma_f16(at, bf2[ks], acc[ds][ks]);
+        if constexpr (P) acc[ds][ks] = M::mma(at[ds], bf2[ks], acc[ds][ks]);
+        else acc[ds][ks] = mma_f16(at[ds], bf2[ks], acc[ds][ks]);
       }
     }
+    // the transposed reads run one pair of d-subtiles ahead of the MFMAs that
+    // take them (0x100: LDS reads, 0x008: MFMA)
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+    for (int st = 0; st < DS / 2 - 1; ++st) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
   };
 
   // chunk c: queries qbase + 32 c .. +31, tile (c / 2) in buffer (c / 2) & 1,
@@ -987,11 +998,12 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
     if (prole) {
       if (need) m2(std::true_type{}, r0, pa, pb, sm.o[buf]);
     } else {
+      // w of this chunk (read whether or not the chunk is needed: the buffer
+      // always exists, and a conditional read leaves the compiler zeroing the
+      // registers on the other path every chunk)
       f32x4 wv[4];
-      if (need) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) wv[u] = xw[u][lane];
-      }
+      for (int u = 0; u < 4; ++u) wv[u] = xw[u][lane];
       if (needc(c + 1)) {
         constexpr int r1 = 32 * ((CM + 1) & 1);
         const short* os1 = sm.o[((CM + 1) >> 1) & 1];
