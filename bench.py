@@ -26,8 +26,10 @@ throughput 7*B*H*S^2*D / step time in TFLOP/s. The same JSON line carries:
   * decode     -- kat_attn_decode over bf16 KV caches (us per call, HBM GB/s
                  of the K and V bytes) and generate() tokens/s with the KV
                  cache against the reference's re-run-the-prefix loop;
-  * device     -- CU count, a measured bf16 MFMA loop rate (beside the 2.5 PF
-                 spec peak) and a measured 1 GiB device-copy bandwidth;
+  * device     -- CU count, measured bf16 MFMA loop rates (fixed and random
+                 operands, beside the 2.5 PF spec peak), a measured 1 GiB
+                 device-copy bandwidth, and power_scaling: equal-work
+                 attention blocks on 64 vs 256 CUs (the clock drop under load);
   * model_step / model_step_large -- one training step (bf16 autocast
                  forward + loss + backward, no optimizer) of the 109.5 M-parameter
                  model at batch 16 x 2048 and of the 1.3 B-parameter model at
@@ -276,6 +278,43 @@ def device_info(torch, lib):
             "mfma_bf16_random_operand_loop_tflops": round(rand_tflops, 1),
             "mfma_bf16_spec_tflops": PEAK_BF16_TFLOPS, "copy_1GiB_GBs": round(copy_gbs, 1),
             "hbm_spec_GBs": PEAK_HBM_GBS}
+
+
+def power_scaling(torch, F):
+    """The same attention blocks on more of the chip: the non-causal forward
+    (kat_attn_fwd_masked, every 128-query block attends all 8192 keys, so all
+    blocks do equal work) with 1, 4 and 8 heads: 64 blocks (64 CUs busy, one
+    block each), 256 (every CU, one block each) and 512 (two per CU, the
+    attention kernels' occupancy). Each size runs 30 calls back to back (a few
+    ms, enough for the clock to settle). With a clock independent of load the
+    first two would take equal time; the ratio is the slowdown the chip's
+    power management imposes when every CU is busy."""
+    from fastalgebraictransformer_amd import forward as FW
+    dev = torch.device("cuda:0")
+    T, D = 8192, 128
+    res = {}
+    for BH in (1, 4, 8):
+        g = torch.Generator().manual_seed(0)
+        q, k, v = (torch.randn(1, BH, T, D, generator=g).to(torch.bfloat16).to(dev) for _ in range(3))
+        slopes = torch.full((BH,), 2.0 ** -8, device=dev)
+        o = torch.empty_like(q)
+        L = torch.empty(1, BH, T, device=dev)
+        call = lambda: FW._attn_fwd_into(q, k, v, o, L, slopes, 1 / math.sqrt(D), False, 1e-6,
+                                         extended=True)
+        for _ in range(3):
+            call()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        n = 30
+        e0.record()
+        for _ in range(n):
+            call()
+        e1.record()
+        torch.cuda.synchronize()
+        res[f"blocks_{BH * T // 128}"] = round(e0.elapsed_time(e1) / n, 4)
+    return {"workload": "non-causal bf16 forward, T=8192, D=128, 128 queries per block",
+            "ms_per_call": res,
+            "slowdown_256_vs_64_cus": round(res["blocks_256"] / res["blocks_64"], 3)}
 
 
 MODEL_CONFIGS = {
@@ -645,6 +684,7 @@ def main():
                                  for kk, vv in r.items()} for k, r in fused.items()}
     if not args.no_device:
         line["device"] = device_info(torch, _lib.load())
+        line["device"]["power_scaling"] = power_scaling(torch, F)
     if not args.no_model:
         line["model_step"] = bench_model_step(torch, "small")
     if not args.no_model_large:
