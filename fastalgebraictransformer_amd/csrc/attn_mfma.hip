@@ -1088,7 +1088,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
 // ============================================================================
 // Launchers
 // ============================================================================
-bool attn_mfma_supported(int D) { return D == 64 || D == 128; }
+bool attn_mfma_supported(int D) { return D == 32 || D == 64 || D == 128; }
 
 // Backward workspace (each part 256-byte aligned): per-row stats (float2), the
 // fp16 copies of Q and K ([B*H][T][D] each), the per-tile exponents and bound
@@ -1199,6 +1199,7 @@ template <typename T> int attn_fwd_mfma(const AttnArgs& a, hipStream_t st) {
   if ((int64_t)((a.T + kBM - 1) / kBM) * a.B * a.H > 0x7fffffffLL || !offsets_ok(a, false)) return KAT_EUNSUPPORTED;
   if (a.D == 128) KAT_MODE_SWITCH(a, return (launch_fwd<T, 128, MODE>(a, st)));
   if (a.D == 64) KAT_MODE_SWITCH(a, return (launch_fwd<T, 64, MODE>(a, st)));
+  if (a.D == 32) KAT_MODE_SWITCH(a, return (launch_fwd<T, 32, MODE>(a, st)));
   return KAT_EUNSUPPORTED;
 }
 
@@ -1206,6 +1207,7 @@ template <typename T> int attn_bwd_mfma(const AttnArgs& a, void* ws, hipStream_t
   if ((int64_t)((a.T + 63) / 64) * a.B * a.H > 0x7fffffffLL || !offsets_ok(a, true)) return KAT_EUNSUPPORTED;
   if (a.D == 128) KAT_MODE_SWITCH(a, return (launch_bwd<T, 128, MODE>(a, ws, st)));
   if (a.D == 64) KAT_MODE_SWITCH(a, return (launch_bwd<T, 64, MODE>(a, ws, st)));
+  if (a.D == 32) KAT_MODE_SWITCH(a, return (launch_bwd<T, 32, MODE>(a, ws, st)));
   return KAT_EUNSUPPORTED;
 }
 

@@ -186,9 +186,15 @@ __device__ __forceinline__ void dma_wait() { __builtin_amdgcn_s_waitcnt(0x0F70);
 // swizzles on gfx950. Under it these maps leave both reads conflict-free: the
 // row fragments (rows r0 + lane % 16, chunk lane / 16 (+ const)) and the
 // transposed fragments (rows r0 + 4 (lane / 16) + lane % 16 / 4, two chunks).
+// D = 32 (rows of 4 chunks, 64 bytes: rows four apart share banks): images
+// 0, 0, 2, 1, so the four rows of a bank group take four different chunks in
+// the row reads, and rows 0-3 and 4-7 take disjoint chunk pairs in the
+// transposed reads.
 // ---------------------------------------------------------------------------
 template <int D> __device__ __forceinline__ int swz(int row) {
-  constexpr int i0 = D == 128 ? 8 : 1, i1 = D == 128 ? 3 : 2, i2 = D == 128 ? 5 : 4, i3 = D == 128 ? 11 : 5;
+  static_assert(D == 32 || D == 64 || D == 128, "swizzle defined for D = 32, 64, 128");
+  constexpr int i0 = D == 128 ? 8 : D == 64 ? 1 : 0, i1 = D == 128 ? 3 : D == 64 ? 2 : 0,
+                i2 = D == 128 ? 5 : D == 64 ? 4 : 2, i3 = D == 128 ? 11 : D == 64 ? 5 : 1;
   return ((row & 1) ? i0 : 0) ^ ((row & 2) ? i1 : 0) ^ ((row & 4) ? i2 : 0) ^ ((row & 8) ? i3 : 0);
 }
 template <int D> __device__ __forceinline__ int soff(int row, int col) {

@@ -46,15 +46,15 @@ _WARNED = set()
 
 
 def _warn_if_tiled(tensors, D, dtype):
-    """bf16 / fp16 attention runs on the MFMA kernels when the head dim is 64
-    or 128 and every [B, H, T, D] operand has 16-byte aligned rows; otherwise
+    """bf16 / fp16 attention runs on the MFMA kernels when the head dim is 32,
+    64 or 128 and every [B, H, T, D] operand has 16-byte aligned rows; otherwise
     libkat falls back to the fp32 tiled kernels, which are correct but about
     an order of magnitude slower. Warn once per reason, so a model with
     another head dim (or a misaligned view) does not lose that silently."""
     if dtype not in (torch.bfloat16, torch.float16) or os.environ.get("KAT_ATTN_IMPL") == "tiled":
         return
-    if D not in (64, 128):
-        reason = f"head dim {D} (the MFMA kernels cover 64 and 128)"
+    if D not in (32, 64, 128):
+        reason = f"head dim {D} (the MFMA kernels cover 32, 64 and 128)"
     elif any(t.data_ptr() % 16 or any((st * t.element_size()) % 16 for st in t.stride()[:3])
              for t in tensors):
         reason = "rows not 16-byte aligned (a view with an odd offset or stride)"

@@ -150,7 +150,7 @@ int kat_add_men_bwd(const void* dy, const void* dh, const void* h, const void* w
  * l_strides: 3 int64 = (b, h, t) strides of L. slopes: fp32 [H].
  * Replaces the host wrapper + rational_attention_fwd_kernel[(B,H,T)] launch at
  * forward.py:267-319 (kernel forward.py:49-159). dtype KAT_BF16/KAT_F16 use
- * the MFMA kernels (D in {64, 128}, 16-byte aligned rows); KAT_F32 and other
+ * the MFMA kernels (D in {32, 64, 128}, 16-byte aligned rows); KAT_F32 and other
  * D (<= 256) use the fp32 tiled kernels.
  * ---------------------------------------------------------------------- */
 int kat_attn_fwd(const void* q, const void* k, const void* v, void* out, float* L,

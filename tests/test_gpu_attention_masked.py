@@ -111,7 +111,8 @@ def test_masked_fp32(gpu, B, H, T, D, kind, causal):
 @pytest.mark.parametrize("dtype,B,H,T,D", [(torch.bfloat16, 2, 2, 333, 128),
                                            (torch.float16, 3, 2, 200, 64),
                                            (torch.bfloat16, 2, 1, 1, 64),
-                                           (torch.bfloat16, 1, 2, 700, 64)])
+                                           (torch.bfloat16, 1, 2, 700, 64),
+                                           (torch.float16, 2, 3, 300, 32)])
 def test_masked_lowp(gpu, dtype, B, H, T, D, kind, causal, impl, monkeypatch):
     monkeypatch.setenv("KAT_ATTN_IMPL", impl)
     q, k, v, do = _inputs(5 * T + D, B, H, T, D, dtype)

@@ -1,6 +1,6 @@
 """A seeded random sweep of attention shapes against the oracle: sequence
 lengths that are not multiples of the kernels' tiles, head dims 32 / 64 / 128
-(the MFMA kernels cover 64 and 128, the tiled kernels the rest), 1 to 16
+(bf16 / fp16 on the MFMA kernels, fp32 on the tiled kernels), 1 to 16
 heads, bf16 / fp16 / fp32, causal or with a padding mask or non-causal. The
 draw is fixed (seed below), so a failure names a reproducible case. Bars as
 in test_gpu_attention.py: fp32 <= 1e-5 of max|ref|; bf16 / fp16
