@@ -174,7 +174,9 @@ def bench_attention_variants(torch, F, steps=10, warmup=3, B=4, H=16, T=4096, D=
 def bench_decode(torch, F, reps=50):
     """kat_attn_decode (one query per (b, h) against a bf16 KV cache) at a
     few cache shapes: time per call and HBM GB/s of the K and V bytes it must
-    read (2 B H n D x 2 bytes; q and out are negligible); plus the model's
+    read (2 B H n D x 2 bytes; q and out are negligible), from `reps` calls
+    replayed in a HIP graph (`us`) and issued eagerly from Python
+    (`us_eager_calls`, where the wrapper's host time shows); plus the model's
     generate() with its KV cache against the reference's loop, which re-runs
     the whole prefix for every token (algebraic_model.py:239-265)."""
     dev = torch.device("cuda:0")
@@ -195,10 +197,29 @@ def bench_decode(torch, F, reps=50):
             F.rational_attention_decode(q, k4, v4, slopes, 1 / math.sqrt(D))
         e1.record()
         torch.cuda.synchronize()
+        us_eager = e0.elapsed_time(e1) / reps * 1e3
+        # the same calls replayed from a captured HIP graph, as generate() runs
+        # its decode step: the launch work of the Python wrapper drops out
+        st = torch.cuda.Stream()
+        st.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(st):
+            F.rational_attention_decode(q, k4, v4, slopes, 1 / math.sqrt(D))
+        torch.cuda.current_stream().wait_stream(st)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(reps):
+                F.rational_attention_decode(q, k4, v4, slopes, 1 / math.sqrt(D))
+        graph.replay()
+        torch.cuda.synchronize()
+        e0.record()
+        graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
         us = e0.elapsed_time(e1) / reps * 1e3
+        del graph
         nbytes = 2 * B * H * n * D * 2
-        res[f"B{B}_H{H}_n{n}_D{D}"] = dict(us=round(us, 2), bytes=nbytes,
-                                            GBs=round(nbytes / us / 1e3, 1),
+        res[f"B{B}_H{H}_n{n}_D{D}"] = dict(us=round(us, 2), us_eager_calls=round(us_eager, 2),
+                                            bytes=nbytes, GBs=round(nbytes / us / 1e3, 1),
                                             frac_hbm_peak=round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4))
         del q, kc, vc, k4, v4
     # model generate: config-4 model, batch 8, 512-token prompt, 64 new tokens

@@ -41,6 +41,7 @@ struct DecodeArgs {
 constexpr int kDecThreads = 256;
 constexpr int kDecWaves = kDecThreads / 64;
 constexpr int kDecInFlight = 4;  // rows per lane in flight
+constexpr int kDecCombThreads = 256;  // combine: one thread per column and one for the row sums
 
 template <typename T, int D> struct DecShape {
   static constexpr int EPL = 16 / (int)sizeof(T);  // elements per lane (one 16-byte load)
@@ -126,25 +127,48 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_part_k(DecodeArgs a, 
   }
 }
 
-// o = sum_s acc_s / (sum_s l_s + eps), L = sum_s l_s; one block per (b, h)
+// o = sum_s acc_s / (sum_s l_s + eps), L = sum_s l_s; one block per (b, h).
+// Thread d < D sums column d and thread D the row sums l, all at once: the
+// partials come from work-groups on other XCDs (other L2s), so every load is
+// a round trip to memory, and each thread keeps eight independent loads in
+// flight (eight running sums over the splits s = 8 i + r, added in a fixed
+// order: deterministic).
 template <typename T, int D>
-__global__ __launch_bounds__(256) void attn_decode_combine_k(DecodeArgs a, const float* __restrict__ part) {
+__device__ __forceinline__ float sum_splits(const float* __restrict__ p, int S, int col) {
+  float t[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  int s = 0;
+  for (; s + 8 <= S; s += 8) {
+#pragma unroll
+    for (int r = 0; r < 8; ++r) t[r] += p[(int64_t)(s + r) * (D + 1) + col];
+  }
+#pragma unroll
+  for (int r = 0; r < 7; ++r)
+    if (s + r < S) t[r] += p[(int64_t)(s + r) * (D + 1) + col];
+  return ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(kDecCombThreads) void attn_decode_combine_k(DecodeArgs a, const float* __restrict__ part) {
   __shared__ float sh_inv;
   const int bh = blockIdx.x, b = bh / a.H, h = bh - b * a.H;
   const float* p = part + (int64_t)bh * a.splits * (D + 1);
-  if (threadIdx.x == 0) {
-    float l = 0.f;
-    for (int s = 0; s < a.splits; ++s) l += p[s * (D + 1) + D];
-    if (a.L) a.L[bh] = l;
-    sh_inv = 1.f / (l + a.eps);  // forward.py:150
+  float t[(D + kDecCombThreads) / kDecCombThreads];  // columns threadIdx.x + k * threads
+#pragma unroll
+  for (int k = 0; k < (D + kDecCombThreads) / kDecCombThreads; ++k) {
+    const int col = (int)threadIdx.x + k * kDecCombThreads;
+    t[k] = col <= D ? sum_splits<T, D>(p, a.splits, col) : 0.f;
+    if (col == D) {
+      if (a.L) a.L[bh] = t[k];
+      sh_inv = 1.f / (t[k] + a.eps);  // forward.py:150
+    }
   }
   __syncthreads();
   const float inv = sh_inv;
   T* o = (T*)a.o + b * a.so[0] + h * a.so[1];
-  for (int d = threadIdx.x; d < D; d += blockDim.x) {
-    float t = 0.f;
-    for (int s = 0; s < a.splits; ++s) t += p[s * (D + 1) + d];
-    o[d] = from_acc<T>(t * inv);
+#pragma unroll
+  for (int k = 0; k < (D + kDecCombThreads) / kDecCombThreads; ++k) {
+    const int col = (int)threadIdx.x + k * kDecCombThreads;
+    if (col < D) o[col] = from_acc<T>(t[k] * inv);
   }
 }
 
@@ -178,8 +202,8 @@ template <typename T, int D> static int launch_decode(const DecodeArgs& a, float
   hipLaunchKernelGGL((attn_decode_part_k<T, D>), dim3((unsigned)a.splits, (unsigned)(a.B * a.H)),
                      dim3(kDecThreads), 0, st, a, part);
   if (int rc = check_launch("kat_attn_decode (partials)")) return rc;
-  hipLaunchKernelGGL((attn_decode_combine_k<T, D>), dim3((unsigned)(a.B * a.H)), dim3(std::min(D, 256)),
-                     0, st, a, (const float*)part);
+  hipLaunchKernelGGL((attn_decode_combine_k<T, D>), dim3((unsigned)(a.B * a.H)), dim3(kDecCombThreads), 0, st, a,
+                     (const float*)part);
   return check_launch("kat_attn_decode (combine)");
 }
 
