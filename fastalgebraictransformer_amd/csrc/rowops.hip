@@ -931,13 +931,19 @@ __global__ __launch_bounds__(256) void men_bwd_mp_k(
 // in two interleaved accumulators, then the 64 group sums are added in group
 // order. 16 columns per block give cols / 16 blocks (256 at 4096 columns), so
 // the reduction spreads over the whole chip.
+// 16 fp32 columns are half a 128-byte line: the two blocks that share a line
+// are blocks b and b + 8, which the dispatcher places on the same XCD (blocks
+// go round-robin over the 8 XCDs), so the line crosses HBM once for both
+// (adjacent blocks, on two XCDs with separate L2s, fetched every line twice).
 template <typename A>
 __global__ __launch_bounds__(1024) void colsum_k(const A* __restrict__ partial, int G, int n_cols,
                                                  A* __restrict__ out) {
   __shared__ A red[64][17];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int c = lane & 15, rg = wave * 4 + (lane >> 4);
-  const int col = blockIdx.x * 16 + c;
+  const int b = blockIdx.x, nb16 = (int)gridDim.x & ~15;
+  const int cg = b < nb16 ? (((b >> 4) * 8 + (b & 7)) * 2 + ((b >> 3) & 1)) : b;
+  const int col = cg * 16 + c;
   A s0 = A(0), s1 = A(0);
   if (col < n_cols) {
     int g = rg;
@@ -949,11 +955,11 @@ __global__ __launch_bounds__(1024) void colsum_k(const A* __restrict__ partial, 
   }
   red[rg][c] = s0 + s1;
   __syncthreads();
-  if (threadIdx.x < 16 && blockIdx.x * 16 + (int)threadIdx.x < n_cols) {
+  if (threadIdx.x < 16 && cg * 16 + (int)threadIdx.x < n_cols) {
     A t = A(0);
 #pragma unroll 8
     for (int i = 0; i < 64; ++i) t += red[i][threadIdx.x];
-    out[blockIdx.x * 16 + threadIdx.x] = t;
+    out[cg * 16 + threadIdx.x] = t;
   }
 }
 
