@@ -76,35 +76,43 @@ constexpr int kNW = 4;         // waves per block
 constexpr int kRows = 32;      // rows owned per wave
 constexpr int kBM = kNW * kRows;  // rows owned per block
 constexpr int kBN = 64;        // streamed rows per LDS tile
+// forward: 16-query subtiles per wave. 2: 32 queries per wave, two 4-wave blocks
+// per CU (two waves per SIMD). 4 (64 queries per wave, one wave per SIMD, the O
+// accumulators in AGPRs: 228 VGPRs + 164 AGPRs) halves the LDS and DMA traffic
+// per MFMA but measured 18% slower at config 3 (0.353 vs 0.298 ms): a single
+// wave issues VALU too slowly for the rational map.
+constexpr int kFwdQS = 2;
 // kernel modes: causal (keys j <= i) and a key padding mask; the reference's
 // configuration is kModeCausal alone
 constexpr int kModeCausal = 1;
 constexpr int kModeKeyMask = 2;
 
 // ============================================================================
-// Forward: 128 queries per block, 4 waves x 32 queries, 2 blocks per CU.
+// Forward: 4 waves x 16 QS queries per block.
 //   S^T[key][q]  = K Q^T (+ bias)   A = K  (LDS rows)         B = Q^T (VGPRs)
 //   O^T[d][q]   += V^T P^T          A = V^T (LDS transposed)  B = P^T (from S^T)
 // ============================================================================
-template <typename T, int D, int MODE>
-__global__ __launch_bounds__(256, 2) void attn_fwd_k(AttnArgs a) {
+template <typename T, int D, int MODE, int QS>
+__global__ __launch_bounds__(256, QS == 2 ? 2 : 1) void attn_fwd_k(AttnArgs a) {
   typedef Mfma<T> M;
   constexpr int KK = D / 32;  // k-steps of QK^T
   constexpr int DS = D / 16;  // 16-wide d subtiles of O^T
   constexpr bool kCausal = (MODE & kModeCausal) != 0;
   constexpr bool kKM = (MODE & kModeKeyMask) != 0;
+  constexpr int RW = 16 * QS;    // queries per wave
+  constexpr int BMQ = kNW * RW;  // queries per block
   __shared__ short sk[2][kBN * D];
   __shared__ short sv[2][kBN * D];
 
   const int T_ = a.T, H = a.H;
   int bh, rank;
   block_order((int)blockIdx.x, a.B * H, bh, rank);
-  const int n_qt = (T_ + kBM - 1) / kBM;
-  const int q0 = (n_qt - 1 - rank) * kBM;
+  const int n_qt = (T_ + BMQ - 1) / BMQ;
+  const int q0 = (n_qt - 1 - rank) * BMQ;
   const int b = bh / H, h = bh - b * H;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 4, li = lane & 15;
-  const int qw = q0 + kRows * w;
+  const int qw = q0 + RW * w;
 
   const T* qp = (const T*)a.q + b * a.sq[0] + h * a.sq[1];
   const T* kp = (const T*)a.k + b * a.sk[0] + h * a.sk[1];
@@ -115,11 +123,11 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_k(AttnArgs a) {
   const float scale = a.scale;
 
   // Q^T fragments (B operand): lane (g, li) holds Q[qw + 16 qs + li][32 kk + 8 g .. +7]
-  i16x8 qf[2][KK];
+  i16x8 qf[QS][KK];
   {
     const __amdgpu_buffer_rsrc_t rq = rsrc(qp, row_bytes(T_, sq2, D));
 #pragma unroll
-    for (int qs = 0; qs < 2; ++qs)
+    for (int qs = 0; qs < QS; ++qs)
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk)
         qf[qs][kk] = load16(rq, ((uint32_t)(qw + 16 * qs + li) * sq2 + 32 * kk + 8 * g) * 2);
@@ -139,26 +147,28 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_k(AttnArgs a) {
   int kcur = 0;
   const uint8_t* kmb = kKM ? a.km + (int64_t)b * a.skm : nullptr;
 
-  f32x4 oacc[DS][2];
+  f32x4 oacc[DS][QS];
 #pragma unroll
   for (int ds = 0; ds < DS; ++ds)
 #pragma unroll
-    for (int qs = 0; qs < 2; ++qs) oacc[ds][qs] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float lsum[2] = {0.f, 0.f};
+    for (int qs = 0; qs < QS; ++qs) oacc[ds][qs] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float lsum[QS];
+#pragma unroll
+  for (int qs = 0; qs < QS; ++qs) lsum[qs] = 0.f;
 
   TileDma<D, kNW> dk, dv;
   dk.init(w, lane, sk2);
   dv.init(w, lane, sv2);
 
   // S^T of the 16 keys at tile rows hr .. hr + 15
-  auto m1 = [&](int hr, f32x4 (&s_)[2], const short* ks_) __attribute__((always_inline)) {
+  auto m1 = [&](int hr, f32x4 (&s_)[QS], const short* ks_) __attribute__((always_inline)) {
 #pragma unroll
-    for (int qs = 0; qs < 2; ++qs) s_[qs] = cbx;
+    for (int qs = 0; qs < QS; ++qs) s_[qs] = cbx;
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {
       const i16x8 kf = lds16(ks_ + soff<D>(hr + li, 32 * kk + 8 * g));
 #pragma unroll
-      for (int qs = 0; qs < 2; ++qs) s_[qs] = M::mma(kf, qf[qs][kk], s_[qs]);
+      for (int qs = 0; qs < QS; ++qs) s_[qs] = M::mma(kf, qf[qs][kk], s_[qs]);
     }
   };
   // f' of those scores, packed as P^T; row sums into lsum. MASKED: the
@@ -166,13 +176,13 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_k(AttnArgs a) {
   // keys -- causal: keys past the query get f' = 0; non-causal: scores whose
   // bias form has the wrong sign for |i - j| are corrected; keys outside the
   // validity mask (padding mask, or past T) get f' = 0.
-  auto vh = [&](auto masked_tag, int kh, const f32x4 (&s_)[2], uint32_t (&pk)[2][2]) __attribute__((always_inline)) {
+  auto vh = [&](auto masked_tag, int kh, const f32x4 (&s_)[QS], uint32_t (&pk)[QS][2]) __attribute__((always_inline)) {
     constexpr bool MASKED = decltype(masked_tag)::value;
     constexpr bool kVM = kKM || !kCausal;  // a validity mask exists
     uint32_t nib = 0;
     if constexpr (MASKED && kVM) nib = (uint32_t)(vm >> (kh - kcur + 4 * g));
 #pragma unroll
-    for (int qs = 0; qs < 2; ++qs) {
+    for (int qs = 0; qs < QS; ++qs) {
       const float tterm = (kCausal ? slope : sgn * slope) * (float)(kh - qw - 16 * qs);
       float f[4];
 #pragma unroll
@@ -195,20 +205,20 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_k(AttnArgs a) {
     }
   };
   // O^T += V^T P^T over the 32 keys at tile rows r0 .. r0 + 31
-  auto m2 = [&](int r0, const uint32_t (&pa)[2][2], const uint32_t (&pb)[2][2], const short* vs_) __attribute__((always_inline)) {
-    i16x8 pf[2];
+  auto m2 = [&](int r0, const uint32_t (&pa)[QS][2], const uint32_t (&pb)[QS][2], const short* vs_) __attribute__((always_inline)) {
+    i16x8 pf[QS];
 #pragma unroll
-    for (int qs = 0; qs < 2; ++qs) pf[qs] = pack_frag(pa[qs][0], pa[qs][1], pb[qs][0], pb[qs][1]);
+    for (int qs = 0; qs < QS; ++qs) pf[qs] = pack_frag(pa[qs][0], pa[qs][1], pb[qs][0], pb[qs][1]);
 #pragma unroll
     for (int ds = 0; ds < DS; ++ds) {
       const i16x8 vt = frag_tr<D>(vs_, r0, 16 * ds, g, li);
 #pragma unroll
-      for (int qs = 0; qs < 2; ++qs) oacc[ds][qs] = M::mma(vt, pf[qs], oacc[ds][qs]);
+      for (int qs = 0; qs < QS; ++qs) oacc[ds][qs] = M::mma(vt, pf[qs], oacc[ds][qs]);
     }
   };
   auto tile = [&](auto masked_tag, int k0, const short* ks_, const short* vs_) __attribute__((always_inline)) {
-    f32x4 sA[2], sB[2];
-    uint32_t pa0[2][2], pb0[2][2], pa1[2][2], pb1[2][2];
+    f32x4 sA[QS], sB[QS];
+    uint32_t pa0[QS][2], pb0[QS][2], pa1[QS][2], pb1[QS][2];
     m1(0, sA, ks_);
     m1(16, sB, ks_);
     vh(masked_tag, k0, sA, pa0);
@@ -230,14 +240,14 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_k(AttnArgs a) {
     if constexpr (kCausal && !kKM) {
       if (k0 + kBN - 1 <= qw)
         tile(std::false_type{}, k0, ks_, vs_);
-      else if (k0 <= qw + kRows - 1)
+      else if (k0 <= qw + RW - 1)
         tile(std::true_type{}, k0, ks_, vs_);
     } else {
       bool plain;
       if constexpr (kCausal) {
         plain = k0 + kBN - 1 <= qw;
       } else {
-        const bool above = k0 > qw + kRows - 1;
+        const bool above = k0 > qw + RW - 1;
         if (above && sgn > 0.f) {
           cbx = -cbx;
           sgn = -1.f;
@@ -245,7 +255,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_k(AttnArgs a) {
         plain = above || k0 + kBN - 1 <= qw;
       }
       plain = plain && vm == ~0ull;
-      if (vm == 0ull || (kCausal && k0 > qw + kRows - 1)) {
+      if (vm == 0ull || (kCausal && k0 > qw + RW - 1)) {
       } else if (plain) {
         tile(std::false_type{}, k0, ks_, vs_);
       } else {
@@ -254,7 +264,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_k(AttnArgs a) {
     }
   };
 
-  const int n_kt = kCausal ? (std::min(q0 + kBM, T_) + kBN - 1) / kBN : (T_ + kBN - 1) / kBN;
+  const int n_kt = kCausal ? (std::min(q0 + BMQ, T_) + kBN - 1) / kBN : (T_ + kBN - 1) / kBN;
   // this lane's padding-mask byte of key tile kt (0 past the end)
   auto kmbyte = [&](int kt) __attribute__((always_inline)) {
     const int j = kt * kBN + lane;
@@ -295,7 +305,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_k(AttnArgs a) {
   T* __restrict__ op = (T*)a.o + b * a.so[0] + h * a.so[1];
   float* __restrict__ Lp = a.L + b * a.sl[0] + h * a.sl[1];
 #pragma unroll
-  for (int qs = 0; qs < 2; ++qs) {
+  for (int qs = 0; qs < QS; ++qs) {
     float l = lsum[qs];
     l += __shfl_xor(l, 16, 64);
     l += __shfl_xor(l, 32, 64);
@@ -1148,13 +1158,14 @@ bool offsets_ok(const AttnArgs& a, bool bwd) {
   const int64_t lim = 0x7fffffffLL;
   const int64_t* s2[5] = {&a.sq[2], &a.sk[2], &a.sv[2], &a.sdo[2], &a.so[2]};
   for (int t = 0; t < (bwd ? 5 : 3); ++t)
-    if (*s2[t] < a.D || ((int64_t)a.T + kBM) * *s2[t] * 2 > lim) return false;
+    if (*s2[t] < a.D || ((int64_t)a.T + std::max(kBM, 64 * kFwdQS)) * *s2[t] * 2 > lim) return false;
   return (int64_t)a.T * a.D * 2 < lim && (int64_t)a.T * 8 < lim;
 }
 
 template <typename T, int D, int MODE> int launch_fwd(const AttnArgs& a, hipStream_t st) {
-  const int64_t nb = (int64_t)((a.T + kBM - 1) / kBM) * a.B * a.H;
-  hipLaunchKernelGGL((attn_fwd_k<T, D, MODE>), dim3((unsigned)nb), dim3(256), 0, st, a);
+  constexpr int QS = kFwdQS;
+  const int64_t nb = (int64_t)((a.T + 64 * QS - 1) / (64 * QS)) * a.B * a.H;
+  hipLaunchKernelGGL((attn_fwd_k<T, D, MODE, QS>), dim3((unsigned)nb), dim3(256), 0, st, a);
   return check_launch("kat_attn_fwd (mfma)");
 }
 
