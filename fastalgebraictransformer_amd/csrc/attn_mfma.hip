@@ -110,6 +110,8 @@ __global__ __launch_bounds__(256, QS == 2 ? 2 : 1) void attn_fwd_k(AttnArgs a) {
   const int n_qt = (T_ + BMQ - 1) / BMQ;
   const int q0 = (n_qt - 1 - rank) * BMQ;
   const int b = bh / H, h = bh - b * H;
+  // the wave index stays a per-lane value here: as a scalar (wave_id) the
+  // forward measured 3% slower
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 4, li = lane & 15;
   const int qw = q0 + RW * w;
@@ -575,7 +577,7 @@ __global__ __launch_bounds__(64 * kDqW, 1) void attn_bwd_dq_k(AttnArgs a, const 
   const int qb = n_qb - 1 - rank;
   const int q0 = qb * kDqM;
   const int b = bh / H, h = bh - b * H;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
   const int g = lane >> 4, li = lane & 15;
   const int nt = (T_ + 63) / 64;
   const int qtw = (q0 >> 6) + w;            // this wave's 64-query tile
@@ -733,9 +735,12 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
   const int bh = bh0 + bl;
   const int k0 = rank * kBM;
   const int b = bh / H, h = bh - b * H;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  // the key group (and the tile conditions derived from it) as scalars; the
+  // role test stays a per-lane value: as a scalar branch the two roles' code
+  // no longer fits 256 VGPRs (spills)
+  const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
   const int grp = w % kNW;
-  const bool prole = w < kNW;
+  const bool prole = (tid >> 6) < kNW;
   const int g = lane >> 4, li = lane & 15;
   const int kw = k0 + kRows * grp;
 

@@ -119,6 +119,13 @@ __device__ __forceinline__ int ds_exp(float b) {
   return std::min(100, std::max(-100, 14 - E));
 }
 
+// Index of the calling wave in its block as a wave-uniform (scalar) value.
+// threadIdx.x >> 6 is the same in every lane of a wave, but the compiler
+// cannot prove it, and branches on values derived from it become exec-mask
+// saves and restores around every role and tile condition; read from the first
+// lane they are plain scalar branches.
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
+
 __device__ __forceinline__ i16x8 pack_frag(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
   return __builtin_bit_cast(i16x8, (u32x4{a, b, c, d}));
 }
