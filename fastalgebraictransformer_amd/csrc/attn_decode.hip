@@ -230,8 +230,8 @@ extern "C" size_t kat_attn_decode_workspace_size(int64_t B, int64_t H, int64_t T
 }
 
 // Argument checks and launch shared by kat_attn_decode and
-// kat_attn_decode_noalloc. get_part(need) returns the partials buffer for
-// `need` bytes, or nullptr after recording an error.
+// kat_attn_decode_noalloc. get_part(need, rc) returns the partials buffer for
+// `need` bytes, or nullptr after recording an error and setting rc to its code.
 template <typename GetPart>
 static int decode_impl(const char* nm, const void* q, const void* k, const void* v, void* out, float* L,
                        const float* slopes, const int32_t* lengths, int64_t B, int64_t H, int64_t T,
@@ -273,8 +273,9 @@ static int decode_impl(const char* nm, const void* q, const void* k, const void*
   a.eps = eps;
   decode_split(B, H, std::max<int64_t>(T, 1), decode_rpp((int)D, dtype), a.splits, a.chunk);
   const size_t need = (size_t)(B * H) * (size_t)a.splits * (size_t)(D + 1) * sizeof(float);
-  float* part = get_part(need);
-  if (!part) return KAT_EINVAL;  // get_part recorded the message
+  int rc = KAT_OK;
+  float* part = get_part(need, rc);
+  if (!part) return rc;  // get_part recorded the message
   const hipStream_t st = as_stream(stream);
   switch (dtype) {
     case KAT_F32: return decode_d<float>(a, part, st);
@@ -291,10 +292,10 @@ extern "C" int kat_attn_decode(const void* q, const void* k, const void* v, void
                                void* stream) {
   const char* nm = "kat_attn_decode";
   return decode_impl(nm, q, k, v, out, L, slopes, lengths, B, H, T, D, strides, scale, eps, dtype,
-                     stream, [&](size_t need) -> float* {
+                     stream, [&](size_t need, int& rc) -> float* {
                        if (!workspace || workspace_bytes < need) {
-                         fail(KAT_EINVAL, "%s: workspace %zu bytes < required %zu", nm, workspace_bytes,
-                              need);
+                         rc = fail(KAT_EINVAL, "%s: workspace %zu bytes < required %zu", nm, workspace_bytes,
+                                   need);
                          return nullptr;
                        }
                        return reinterpret_cast<float*>(workspace);
@@ -315,11 +316,12 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 float* g_scratch_ptr[kMaxDevices] = {};
 
-// device address of `scratch` on the current device, or nullptr (error recorded)
-float* device_scratch(const char* nm) {
+// device address of `scratch` on the current device, or nullptr (error
+// recorded, rc set to its code)
+float* device_scratch(const char* nm, int& rc) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
-    fail(KAT_EHIP, "%s: no current HIP device", nm);
+    rc = fail(KAT_EHIP, "%s: no current HIP device", nm);
     return nullptr;
   }
   std::lock_guard<std::mutex> lock(g_scratch_mu);
@@ -327,7 +329,7 @@ float* device_scratch(const char* nm) {
     void* p = nullptr;
     const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess || !p) {
-      fail(KAT_EHIP, "%s: hipGetSymbolAddress(scratch) on device %d: %s", nm, dev, hipGetErrorString(e));
+      rc = fail(KAT_EHIP, "%s: hipGetSymbolAddress(scratch) on device %d: %s", nm, dev, hipGetErrorString(e));
       return nullptr;
     }
     g_scratch_ptr[dev] = static_cast<float*>(p);
@@ -342,14 +344,14 @@ extern "C" int kat_attn_decode_noalloc(const void* q, const void* k, const void*
                                        float eps, int dtype, void* stream) {
   const char* nm = "kat_attn_decode_noalloc";
   return decode_impl(nm, q, k, v, out, L, slopes, lengths, B, H, T, D, strides, scale, eps, dtype,
-                     stream, [&](size_t need) -> float* {
+                     stream, [&](size_t need, int& rc) -> float* {
                        if (need > (size_t)KAT_DECODE_SCRATCH_BYTES) {
-                         fail(KAT_EUNSUPPORTED,
+                         rc = fail(KAT_EUNSUPPORTED,
                               "%s: the partials need %zu bytes, more than the %zu-byte scratch array "
                               "(B*H*splits*(D+1) floats; use kat_attn_decode with a workspace)",
                               nm, need, (size_t)KAT_DECODE_SCRATCH_BYTES);
                          return nullptr;
                        }
-                       return device_scratch(nm);
+                       return device_scratch(nm, rc);
                      });
 }

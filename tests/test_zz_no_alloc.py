@@ -28,7 +28,7 @@ def _case(B, H, T, D, dtype, seed, ragged):
     return q, kc, vc, F.compute_alibi_slopes(H).cuda(), 1.0 / math.sqrt(D), lengths
 
 
-def _call(noalloc, q, kc, vc, slopes, scale, lengths):
+def _call(noalloc, q, kc, vc, slopes, scale, lengths, raw=False):
     lib = _lib.load()
     B, H, D = q.shape
     T = kc.shape[2]
@@ -49,6 +49,8 @@ def _call(noalloc, q, kc, vc, slopes, scale, lengths):
         rc = lib.kat_attn_decode(q.data_ptr(), kc.data_ptr(), vc.data_ptr(), out.data_ptr(),
                                  L.data_ptr(), slopes.data_ptr(), lp, ws.data_ptr(), nbytes, B, H, T,
                                  D, strides, scale, 1e-6, code, st)
+    if raw:
+        return rc
     _lib.check(rc, "decode")
     torch.cuda.synchronize()
     return out, L
@@ -76,6 +78,8 @@ def test_noalloc_decode_rejects_more_than_its_array(gpu):
     B, H, T, D = 128, 128, 16, 128
     q, kc, vc, slopes, scale, _ = _case(B, H, T, D, torch.bfloat16, 7, False)
     assert _lib.load().kat_attn_decode_workspace_size(B, H, T, D, 1) > 8 << 20
+    assert _call(True, q, kc, vc, slopes, scale, None, raw=True) == 2  # KAT_EUNSUPPORTED
+    assert "scratch array" in _lib.load().kat_last_error().decode()
     with pytest.raises(RuntimeError, match="scratch array"):
         _call(True, q, kc, vc, slopes, scale, None)
     # and the workspace entry point still serves it
