@@ -82,6 +82,7 @@ constexpr int kBN = 64;        // streamed rows per LDS tile
 // per MFMA but measured 18% slower at config 3 (0.353 vs 0.298 ms): a single
 // wave issues VALU too slowly for the rational map.
 constexpr int kFwdQS = 2;
+constexpr int kFwdBM = kNW * 16 * kFwdQS;  // queries per forward block
 // kernel modes: causal (keys j <= i) and a key padding mask; the reference's
 // configuration is kModeCausal alone
 constexpr int kModeCausal = 1;
@@ -1163,13 +1164,13 @@ bool offsets_ok(const AttnArgs& a, bool bwd) {
   const int64_t lim = 0x7fffffffLL;
   const int64_t* s2[5] = {&a.sq[2], &a.sk[2], &a.sv[2], &a.sdo[2], &a.so[2]};
   for (int t = 0; t < (bwd ? 5 : 3); ++t)
-    if (*s2[t] < a.D || ((int64_t)a.T + std::max(kBM, 64 * kFwdQS)) * *s2[t] * 2 > lim) return false;
+    if (*s2[t] < a.D || ((int64_t)a.T + std::max(kBM, kFwdBM)) * *s2[t] * 2 > lim) return false;
   return (int64_t)a.T * a.D * 2 < lim && (int64_t)a.T * 8 < lim;
 }
 
 template <typename T, int D, int MODE> int launch_fwd(const AttnArgs& a, hipStream_t st) {
   constexpr int QS = kFwdQS;
-  const int64_t nb = (int64_t)((a.T + 64 * QS - 1) / (64 * QS)) * a.B * a.H;
+  const int64_t nb = (int64_t)((a.T + kFwdBM - 1) / kFwdBM) * a.B * a.H;
   hipLaunchKernelGGL((attn_fwd_k<T, D, MODE, QS>), dim3((unsigned)nb), dim3(256), 0, st, a);
   return check_launch("kat_attn_fwd (mfma)");
 }
@@ -1212,7 +1213,8 @@ int launch_bwd(const AttnArgs& a, void* ws, hipStream_t st) {
   }
 
 template <typename T> int attn_fwd_mfma(const AttnArgs& a, hipStream_t st) {
-  if ((int64_t)((a.T + kBM - 1) / kBM) * a.B * a.H > 0x7fffffffLL || !offsets_ok(a, false)) return KAT_EUNSUPPORTED;
+  if ((int64_t)((a.T + kFwdBM - 1) / kFwdBM) * a.B * a.H > 0x7fffffffLL || !offsets_ok(a, false))
+    return KAT_EUNSUPPORTED;
   if (a.D == 128) KAT_MODE_SWITCH(a, return (launch_fwd<T, 128, MODE>(a, st)));
   if (a.D == 64) KAT_MODE_SWITCH(a, return (launch_fwd<T, 64, MODE>(a, st)));
   if (a.D == 32) KAT_MODE_SWITCH(a, return (launch_fwd<T, 32, MODE>(a, st)));
