@@ -502,15 +502,22 @@ __global__ __launch_bounds__(256) void attn_bwd_stscale_k(BwdWs ws, int T, int c
 // ============================================================================
 // dS^T tiles. The dK / dV kernel stores the fp16 dS it feeds its dK product
 // (2^kh dS, zero where a key is masked or past its query) for every 64-key x
-// 64-query tile (kt, qt) the backward touches: 64 key rows of 64 query columns,
-// row-major, 8 KB. Tiles are grouped by the dQ kernel's blocks of kQB query
-// tiles so that each dQ block streams one contiguous run: a head's runs follow
-// each other by query block qb, and within a run come, key tile by key tile
-// (kt = 0 .. the block's last, causal; every kt otherwise), the block's kQB
-// query tiles side by side (in causal mode the tiles with kt > qt inside a
-// run are not written and not read). Within each 32-query half of a tile the
-// columns follow the dK kernel's MFMA operand order: column 8 g + 4 h + j
-// holds query 16 h + 4 g + j.
+// 64-query tile (kt, qt) the backward touches, 8 KB each. Tiles are grouped by
+// the dQ kernel's blocks of kQB query tiles so that each dQ block streams one
+// contiguous run: a head's runs follow each other by query block qb, and
+// within a run come, key tile by key tile (kt = 0 .. the block's last, causal;
+// every kt otherwise), the block's kQB query tiles side by side (in causal
+// mode the tiles with kt > qt inside a run are not written and not read).
+// Logically a tile is 64 key rows x 64 query columns; within each 32-query
+// half the columns follow the dK kernel's MFMA operand order (column
+// 8 g + 4 h + j holds query 16 h + 4 g + j). It is stored as eight 1 KB
+// blocks, one per (32-key half kh2, 32-query half qh, 16-key group ks), at
+// block (4 kh2 + 2 qh + ks): the 16-byte piece (key row 16 ks + i, columns
+// 8 g .. 8 g + 7 of the query half) at position 16 g + i, i.e. exactly what
+// lane (g, i) of the dK kernel's wave holds, so that each of its stores
+// writes 1 KB contiguously (16 half-lines of 64 bytes took 4% longer over the
+// backward). A 32-key half (one dQ stage) is the tile's first or second
+// contiguous 4 KB, which the dQ kernel's DMA permutes back into row order.
 // ============================================================================
 constexpr int kQB = 8;  // 64-query tiles per dQ block
 
@@ -601,7 +608,15 @@ __global__ __launch_bounds__(64 * kDqW, 1) void attn_bwd_dq_k(AttnArgs a, const 
   KDma dk;
   SDma dd;  // the wave's own dS rows
   dk.init(kw_ ? w : 0, lane, D);
-  dd.init(0, lane, 64);
+  // LDS slot (row, p) of the swizzled [32][64] stage tile takes data chunk
+  // c = p ^ swz(row) of key row `row`, which the stored layout keeps in 1 KB
+  // block 2 (c / 4) + row / 16 at position 16 (c % 4) + row % 16
+#pragma unroll
+  for (int u = 0; u < SDma::SEGS; ++u) {
+    const int row = u * SDma::RPS + lane / SDma::CPR;
+    const int c = (lane % SDma::CPR) ^ swz<64>(row);
+    dd.off[u] = (uint32_t)((((c >> 2) * 2 + (row >> 4)) * 64 + 16 * (c & 3) + (row & 15)) * 16);
+  }
   auto tile_in = [&](int kt) __attribute__((always_inline)) { return wact && (!kCausal || kt <= qtw); };
   // stage st: rows 32 (st & 1) .. of key tile st >> 1
   auto issue = [&](int buf, int st) __attribute__((always_inline)) {
@@ -765,7 +780,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
   const int ktg = kw >> 6;
   const bool dst_ok = ktg < nt;
   f16* const dsh = dst + (int64_t)bl * ds_tiles_per_head(nt, kCausal) * 4096;
-  const uint32_t dso = (uint32_t)((32 * (grp & 1) + li) * 64 + 8 * g);
+  const uint32_t dso = (uint32_t)((grp & 1) * 2048 + lane * 8);  // block 4 (grp & 1), lane's 16 bytes
 
   // B operands: K16^T (P role) or V^T (D role) fragments; lane (g, li) holds row
   // kw + 16 ks + li, columns 32 kk + 8 g .. +7
@@ -1055,19 +1070,19 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
         // dS^T for the dQ kernel: 16 bytes per lane and ks (streaming stores:
         // the dQ kernel reads them back only after this kernel)
         if (dst_ok) {
-          f16* const tb = dsh + ds_tile(ktg, qc >> 6, nt, kCausal) * 4096 + r0;
+          f16* const tb = dsh + ds_tile(ktg, qc >> 6, nt, kCausal) * 4096 + (r0 >> 5) * 1024;
 #pragma unroll
           for (int ks = 0; ks < 2; ++ks)
             __builtin_nontemporal_store(pack_frag(pa[ks][0], pa[ks][1], pb[ks][0], pb[ks][1]),
-                                        reinterpret_cast<i16x8*>(tb + dso + 16 * 64 * ks));
+                                        reinterpret_cast<i16x8*>(tb + dso + 512 * ks));
         }
         m2(std::false_type{}, r0, pa, pb, sm.q[buf]);
       } else if (dst_ok && c < n_ch && (!kCausal || (c >> 1) >= (grp >> 1))) {
         // a skipped chunk inside a kept tile: its dS is zero
-        f16* const tb = dsh + ds_tile(ktg, qc >> 6, nt, kCausal) * 4096 + r0;
+        f16* const tb = dsh + ds_tile(ktg, qc >> 6, nt, kCausal) * 4096 + (r0 >> 5) * 1024;
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks)
-          __builtin_nontemporal_store(i16x8{0, 0, 0, 0, 0, 0, 0, 0}, reinterpret_cast<i16x8*>(tb + dso + 16 * 64 * ks));
+          __builtin_nontemporal_store(i16x8{0, 0, 0, 0, 0, 0, 0, 0}, reinterpret_cast<i16x8*>(tb + dso + 512 * ks));
       }
     }
   };
