@@ -61,6 +61,7 @@
 // whose p <= (r / 2)^4 / L is itself negligible.
 
 #include <algorithm>
+#include <cstddef>
 #include <cstdlib>
 #include <type_traits>
 
@@ -304,9 +305,12 @@ __global__ __launch_bounds__(256, QS == 2 ? 2 : 1) void attn_fwd_k(AttnArgs a) {
     if (kt + 1 < n_kt) step(kt + 1, std::integral_constant<int, 1>{});
   }
 
-  // epilogue: L' across the 4 lane groups, normalise, store
+  // epilogue: L' across the 4 lane groups, normalise; O through the wave's
+  // own RW x D staging tile in the (now idle) K buffers, stored by rows
   T* __restrict__ op = (T*)a.o + b * a.so[0] + h * a.so[1];
   float* __restrict__ Lp = a.L + b * a.sl[0] + h * a.sl[1];
+  static_assert(sizeof(sk) >= kNW * RW * D * 2, "staging tiles fit the K buffers");
+  short* const et = &sk[0][0] + w * RW * D;
 #pragma unroll
   for (int qs = 0; qs < QS; ++qs) {
     float l = lsum[qs];
@@ -314,17 +318,16 @@ __global__ __launch_bounds__(256, QS == 2 ? 2 : 1) void attn_fwd_k(AttnArgs a) {
     l += __shfl_xor(l, 32, 64);
     const int qrow = qw + 16 * qs + li;
     const float inv = 1.f / (l + 16.f * a.eps);
-    if (qrow < T_) {
-      if (g == 0) Lp[(int64_t)qrow * a.sl[2]] = l * 0.0625f;
-      T* orow = op + (int64_t)qrow * a.so[2];
+    if (qrow < T_ && g == 0) Lp[(int64_t)qrow * a.sl[2]] = l * 0.0625f;
 #pragma unroll
-      for (int ds = 0; ds < DS; ++ds) {
-        const f32x4 o = oacc[ds][qs];
-        *reinterpret_cast<u32x2*>(orow + 16 * ds + 4 * g) =
-            u32x2{M::pack2(o[0] * inv, o[1] * inv), M::pack2(o[2] * inv, o[3] * inv)};
-      }
+    for (int ds = 0; ds < DS; ++ds) {
+      const f32x4 o = oacc[ds][qs];
+      epi_put(et, eoff<D>(16 * qs + li, 16 * ds + 4 * g), M::pack2(o[0] * inv, o[1] * inv),
+              M::pack2(o[2] * inv, o[3] * inv));
     }
   }
+  __syncthreads();  // orders the tile's writes before its reads
+  epi_rows_out<T, D, RW>(et, lane, op, a.so[2], qw, T_);
 }
 
 // Everything the backward's MFMA kernels take besides the inputs (the
@@ -686,20 +689,22 @@ __global__ __launch_bounds__(64 * kDqW, 1) void attn_bwd_dq_k(AttnArgs a, const 
 
   T* __restrict__ dqp = (T*)a.dq + b * a.sdq[0] + h * a.sdq[1];
   const float osc = ldexpf(a.scale, -(khead[bh] + ek));
+  // the wave's 64 query rows through its own 64 x D staging tile in the
+  // (now idle) stage buffers
+  static_assert(sizeof(sm) >= kDqW * 64 * D * 2, "staging tiles fit the stage buffers");
+  short* const et = reinterpret_cast<short*>(&sm) + w * 64 * D;
 #pragma unroll
   for (int qc = 0; qc < 4; ++qc) {
     // column 16 qc + li of the tile: half (qc >> 1), column 16 (qc & 1) + li in it
-    const int qrow = 64 * qtw + 32 * (qc >> 1) + ds_col_query(16 * (qc & 1) + li);
-    if (qrow < T_) {
-      T* row = dqp + (int64_t)qrow * a.sdq[2];
+    const int r = 32 * (qc >> 1) + ds_col_query(16 * (qc & 1) + li);
 #pragma unroll
-      for (int ds = 0; ds < DS; ++ds) {
-        const f32x4 o = acc[ds][qc];
-        *reinterpret_cast<u32x2*>(row + 16 * ds + 4 * g) =
-            u32x2{M::pack2(o[0] * osc, o[1] * osc), M::pack2(o[2] * osc, o[3] * osc)};
-      }
+    for (int ds = 0; ds < DS; ++ds) {
+      const f32x4 o = acc[ds][qc];
+      epi_put(et, eoff<D>(r, 16 * ds + 4 * g), M::pack2(o[0] * osc, o[1] * osc), M::pack2(o[2] * osc, o[3] * osc));
     }
   }
+  __syncthreads();  // orders the tile's writes before its reads
+  epi_rows_out<T, D, 64>(et, lane, dqp, a.sdq[2], 64 * qtw, T_);
 }
 
 // ============================================================================
@@ -1100,20 +1105,25 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
   T* __restrict__ outp = prole ? (T*)a.dv + b * a.sdv[0] + h * a.sdv[1] : (T*)a.dk + b * a.sdk[0] + h * a.sdk[1];
   const int64_t ostr = prole ? a.sdv[2] : a.sdk[2];
   const float osc = prole ? 1.f : ldexpf(scale, -(kh + eq));  // dK: dS's 2^kh and Q16's 2^eq undone (exact)
+  // the wave's 32 rows (keys) through its own 32 x D staging tile in the now
+  // idle tile buffers (8 waves x 32 x D x 2 bytes = the Q16 and dO buffers)
+  static_assert(sizeof(sm.q) + sizeof(sm.o) >= 8 * 32 * D * 2 && offsetof(DkvSmem<D>, q) == 0 &&
+                    offsetof(DkvSmem<D>, o) == sizeof(sm.q),
+                "staging tiles fit the tile buffers");
+  short* const et = reinterpret_cast<short*>(&sm) + w * 32 * D;
+  __syncthreads();  // every wave is done with the tile buffers
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
-    const int key = kw + 16 * ks + li;
-    if (key < T_) {
-      T* row = outp + (int64_t)key * ostr;
 #pragma unroll
-      for (int ds = 0; ds < DS; ++ds) {
-        f32x4 v = acc[ds][ks];
-        if (kKM && !kval[ks]) v = f32x4{0.f, 0.f, 0.f, 0.f};
-        *reinterpret_cast<u32x2*>(row + 16 * ds + 4 * g) =
-            u32x2{M::pack2(v[0] * osc, v[1] * osc), M::pack2(v[2] * osc, v[3] * osc)};
-      }
+    for (int ds = 0; ds < DS; ++ds) {
+      f32x4 v = acc[ds][ks];
+      if (kKM && !kval[ks]) v = f32x4{0.f, 0.f, 0.f, 0.f};
+      epi_put(et, eoff<D>(16 * ks + li, 16 * ds + 4 * g), M::pack2(v[0] * osc, v[1] * osc),
+              M::pack2(v[2] * osc, v[3] * osc));
     }
   }
+  __syncthreads();  // orders the tile's writes before its reads
+  epi_rows_out<T, D, 32>(et, lane, outp, ostr, kw, T_);
 }
 
 // ============================================================================

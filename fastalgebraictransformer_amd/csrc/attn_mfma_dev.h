@@ -278,6 +278,35 @@ __device__ __forceinline__ void block_order(int id, int BH, int& bh, int& rank) 
   }
 }
 
+// Epilogue staging: a wave's output rows (R rows of D 16-bit elements) pass
+// through a row-major LDS tile so that the global stores write whole rows (a
+// 16-byte piece per lane, D / 8 lanes per row) instead of the 8-byte pieces of
+// the MFMA C layout, which leave every store instruction 32-byte fragments of
+// 16 rows. The tile's 16-byte chunks are XOR-ed by the row's low bits, so the
+// 8-byte writes of 16 consecutive rows and the 16-byte reads spread over the
+// banks.
+template <int D> __device__ __forceinline__ int eoff(int row, int col) {
+  return row * D + ((((col >> 3) ^ row) & (D / 8 - 1)) << 3) + (col & 7);
+}
+// element (row, col .. col + 3) of the staging tile: 4 values packed as 2 x 2
+__device__ __forceinline__ void epi_put(short* tile, int off, uint32_t lo, uint32_t hi) {
+  *reinterpret_cast<u32x2*>(tile + off) = u32x2{lo, hi};
+}
+// rows 0 .. R - 1 of the tile to base[(row0 + r) * stride], rows with
+// row0 + r >= nrows skipped; the tile must be complete (written by this wave,
+// with a barrier or an LDS wait in between)
+template <typename T, int D, int R>
+__device__ __forceinline__ void epi_rows_out(const short* tile, int lane, T* __restrict__ base, int64_t stride,
+                                             int row0, int nrows) {
+  constexpr int CPR = D / 8, RPI = 64 / CPR;  // chunks per row, rows per instruction
+#pragma unroll
+  for (int i = 0; i < R / RPI; ++i) {
+    const int r = i * RPI + lane / CPR, c = lane % CPR;
+    const i16x8 v = *reinterpret_cast<const i16x8*>(tile + eoff<D>(r, 8 * c));
+    if (row0 + r < nrows) *reinterpret_cast<i16x8*>(base + (int64_t)(row0 + r) * stride + 8 * c) = v;
+  }
+}
+
 // extent in bytes of T rows of D 16-bit elements at a row stride (elements)
 __device__ __forceinline__ uint32_t row_bytes(int T, uint32_t stride, int D) {
   return ((uint32_t)(T - 1) * stride + (uint32_t)D) * 2u;
