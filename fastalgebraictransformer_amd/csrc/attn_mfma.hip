@@ -441,12 +441,14 @@ __global__ __launch_bounds__(256) void attn_bwd_prep_k(AttnArgs a, BwdWs ws) {
   const float fk = ldexpf(1.f, ek), fq = ldexpf(1.f, eq);
   f16* kq = ws.k16 + (int64_t)bh * a.T * D;
   f16* qq = ws.q16 + (int64_t)bh * a.T * D;
+  // non-temporal stores: the copies are read back only by the later kernels
+  // (measured 0.3-0.9% faster over the backward than write-back stores)
 #pragma unroll
   for (int u = 0; u < NP; ++u) {
     const int row = 64 * t + RPP * u + tid / LPR;
     if (row < a.T) {
-      *reinterpret_cast<i16x8*>(kq + (int64_t)row * D + d) = to_f16x8s<T>(kv[u], fk);
-      *reinterpret_cast<i16x8*>(qq + (int64_t)row * D + d) = to_f16x8s<T>(qv[u], fq);
+      __builtin_nontemporal_store(to_f16x8s<T>(kv[u], fk), reinterpret_cast<i16x8*>(kq + (int64_t)row * D + d));
+      __builtin_nontemporal_store(to_f16x8s<T>(qv[u], fq), reinterpret_cast<i16x8*>(qq + (int64_t)row * D + d));
     }
   }
   if (tid == 0) {
