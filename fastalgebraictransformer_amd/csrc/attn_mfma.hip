@@ -2,8 +2,8 @@
 //
 // The attention math runs in three MFMA kernels, beside two streaming passes:
 //   attn_fwd_k         O, L      query-tile blocks; K, V tiles stream through LDS
-//   attn_bwd_prep_k    fp16 copies of Q and K with per-tile exponents, Delta and
-//                                the row stats, the parts of each head's dS bound
+//   attn_bwd_prep_k    fp16 copy of Q with per-tile exponents, Delta and the
+//                                row stats, the parts of each head's dS bound
 //   attn_bwd_stscale_k the head's dS exponent; scales the row stats by it
 //   attn_bwd_dkv_k     dK, dV    key-tile blocks; fp16 Q and dO tiles stream; the
 //                                waves split into a dV role and a dK role; the dK
@@ -40,9 +40,11 @@
 // 65504), and so do the copies of Q and K those products (and the recomputed
 // S) take. Every fp16 operand carries a power-of-two scale chosen from the
 // data, and every scale is undone exactly (binary floating point):
-//   * Q16 and K16: one exponent per 64-row tile (tile_exp of the tile's
-//     max |x|): 0 while max |x| lies in [2^-6, 2^15), else max |x| 2^e lands
-//     in [2^14, 2^15); covered for tile maxima in [2^-46, 2^55]. S comes out
+//   * Q16 and K16: one exponent per 64-row tile of Q and per 32 keys of K
+//     (tile_exp of their max |x|): 0 while max |x| lies in [2^-6, 2^15), else
+//     max |x| 2^e lands in [2^14, 2^15); covered for maxima in [2^-46, 2^55].
+//     Q16 is copied to HBM once (prep); K16 is formed where it is used, with
+//     the same exponent in the dK/dV and dQ kernels. S comes out
 //     of the MFMA scaled by both tiles' factors, which the bias and the scale
 //     applied to it absorb; an accumulator is rescaled when a new tile brings
 //     another exponent.
@@ -334,10 +336,10 @@ __global__ __launch_bounds__(256, QS == 2 ? 2 : 1) void attn_fwd_k(AttnArgs a) {
 // workspace, laid out by bwd_ws below).
 struct BwdWs {
   float2* stats;  // per row (4 cinv, -4 cinv Delta) [B*H][T], then x 2^kh
-  f16* q16;       // fp16 copies [B*H][T][D], scaled per 64-row tile
-  f16* k16;
-  int* kexp;      // per 64-row tile [B*H][nt]: the copies' exponents
-  int* qexp;
+  f16* q16;       // fp16 copy of Q [B*H][T][D], scaled per 64-row tile
+  int* qexp;      // per 64-row tile [B*H][nt]: its exponents
+  int* kexp;      // per 32-key group [B*H][ceil(T / 32)]: the dK/dV kernel's
+                  // fp16 K exponents, which the dQ kernel's K16 takes
   float* vnrm;    // per tile: max_j ||v_j||_2
   float* abnd;    // per tile: max_i c_i ||dO_i||_2    (c_i = min(4.1, 1.125 * 4 cinv_i))
   float* bbnd;    // per tile: max_i c_i |Delta_i|
@@ -348,10 +350,11 @@ struct BwdWs {
 };
 
 // ============================================================================
-// Backward prep, one block per 64-row tile of one (b, h). Streams every input
-// row once:
-//   k16, q16  fp16 copies of K and Q scaled by 2^kexp / 2^qexp, the tile's
-//             tile_exp of max |x| (exact: a power of two);
+// Backward prep, one block per 64-row tile of one (b, h). Streams the rows of
+// Q, V, O and dO once:
+//   q16       fp16 copy of Q scaled by 2^qexp, the tile's tile_exp of max |q|
+//             (exact: a power of two; K is converted where it is used, in the
+//             dK/dV and dQ kernels);
 //   stats     (4 cinv_i, -4 cinv_i Delta_i), Delta_i = <dO_i, O_i>,
 //             4 cinv_i = 1 / (4 (L_i + eps));
 //   vnrm, abnd, bbnd  the tile's parts of the head's bound on |dS|:
@@ -367,34 +370,31 @@ __global__ __launch_bounds__(256) void attn_bwd_prep_k(AttnArgs a, BwdWs ws) {
   constexpr int LPR = D / 8;
   constexpr int RPP = 256 / LPR;
   constexpr int NP = 64 / RPP;
-  __shared__ float red[5][4];
+  __shared__ float red[4][4];
   const int nt = (a.T + 63) / 64;
   const int bh = (int)(blockIdx.x / (unsigned)nt), t = (int)blockIdx.x - bh * nt;
   const int b = bh / a.H, h = bh - b * a.H;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int sub = tid % LPR, d = 8 * sub;
-  const T* kp = (const T*)a.k + b * a.sk[0] + h * a.sk[1];
   const T* vp = (const T*)a.v + b * a.sv[0] + h * a.sv[1];
   const T* qp = (const T*)a.q + b * a.sq[0] + h * a.sq[1];
   const T* op = (const T*)a.o + b * a.so[0] + h * a.so[1];
   const T* dop = (const T*)a.dout + b * a.sdo[0] + h * a.sdo[1];
   const float* Lp = a.L + b * a.sl[0] + h * a.sl[1];
-  i16x8 kv[NP], qv[NP];
-  float km = 0.f, qm = 0.f, vm = 0.f, am = 0.f, bm = 0.f;
+  i16x8 qv[NP];
+  float qm = 0.f, vm = 0.f, am = 0.f, bm = 0.f;
 #pragma unroll
   for (int u = 0; u < NP; ++u) {
     const int row = 64 * t + RPP * u + tid / LPR;
-    kv[u] = qv[u] = i16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    qv[u] = i16x8{0, 0, 0, 0, 0, 0, 0, 0};
     float vs = 0.f, dsum = 0.f, dsq = 0.f;
     if (row < a.T) {
       // every input row is read once here: non-temporal loads (streamed, not
       // kept in L2)
-      kv[u] = ld_nt16(kp + (int64_t)row * a.sk[2] + d);
       qv[u] = ld_nt16(qp + (int64_t)row * a.sq[2] + d);
       const VecT<T, 8> v8 = __builtin_bit_cast(VecT<T, 8>, ld_nt16(vp + (int64_t)row * a.sv[2] + d));
       const VecT<T, 8> o8 = __builtin_bit_cast(VecT<T, 8>, ld_nt16(op + (int64_t)row * a.so[2] + d));
       const VecT<T, 8> g8 = __builtin_bit_cast(VecT<T, 8>, ld_nt16(dop + (int64_t)row * a.sdo[2] + d));
-      km = fmaxf(km, absmax8<T>(kv[u]));
       qm = fmaxf(qm, absmax8<T>(qv[u]));
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -420,43 +420,38 @@ __global__ __launch_bounds__(256) void attn_bwd_prep_k(AttnArgs a, BwdWs ws) {
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
-    km = fmaxf(km, __shfl_xor(km, o, 64));
     qm = fmaxf(qm, __shfl_xor(qm, o, 64));
     vm = fmaxf(vm, __shfl_xor(vm, o, 64));
     am = fmaxf(am, __shfl_xor(am, o, 64));
     bm = fmaxf(bm, __shfl_xor(bm, o, 64));
   }
   if (lane == 0) {
-    red[0][w] = km;
-    red[1][w] = qm;
-    red[2][w] = vm;
-    red[3][w] = am;
-    red[4][w] = bm;
+    red[0][w] = qm;
+    red[1][w] = vm;
+    red[2][w] = am;
+    red[3][w] = bm;
   }
   __syncthreads();
-  float m[5];
+  float m[4];
 #pragma unroll
-  for (int i = 0; i < 5; ++i) m[i] = fmaxf(fmaxf(red[i][0], red[i][1]), fmaxf(red[i][2], red[i][3]));
-  const int ek = tile_exp(m[0]), eq = tile_exp(m[1]);
-  const float fk = ldexpf(1.f, ek), fq = ldexpf(1.f, eq);
-  f16* kq = ws.k16 + (int64_t)bh * a.T * D;
+  for (int i = 0; i < 4; ++i) m[i] = fmaxf(fmaxf(red[i][0], red[i][1]), fmaxf(red[i][2], red[i][3]));
+  const int eq = tile_exp(m[0]);
+  const float fq = ldexpf(1.f, eq);
   f16* qq = ws.q16 + (int64_t)bh * a.T * D;
-  // non-temporal stores: the copies are read back only by the later kernels
+  // non-temporal stores: the copy is read back only by the later kernels
   // (measured 0.3-0.9% faster over the backward than write-back stores)
 #pragma unroll
   for (int u = 0; u < NP; ++u) {
     const int row = 64 * t + RPP * u + tid / LPR;
     if (row < a.T) {
-      __builtin_nontemporal_store(to_f16x8s<T>(kv[u], fk), reinterpret_cast<i16x8*>(kq + (int64_t)row * D + d));
       __builtin_nontemporal_store(to_f16x8s<T>(qv[u], fq), reinterpret_cast<i16x8*>(qq + (int64_t)row * D + d));
     }
   }
   if (tid == 0) {
-    ws.kexp[blockIdx.x] = ek;
     ws.qexp[blockIdx.x] = eq;
-    ws.vnrm[blockIdx.x] = m[2];
-    ws.abnd[blockIdx.x] = m[3];
-    ws.bbnd[blockIdx.x] = m[4];
+    ws.vnrm[blockIdx.x] = m[1];
+    ws.abnd[blockIdx.x] = m[2];
+    ws.bbnd[blockIdx.x] = m[3];
   }
 }
 
@@ -547,29 +542,33 @@ __device__ __forceinline__ int ds_col_query(int c) { return 16 * ((c >> 2) & 1) 
 //                                              B = dS^T  (LDS transposed)
 // A plain GEMM, bound by streaming the stored dS once. Each wave stages its
 // own dS rows (from the block's contiguous run, non-temporal LDS-DMA) and the
-// block shares the K16 rows, 32 keys per stage, four stages deep (three in
-// flight while one is worked); a stage issues the same number of DMA
-// instructions per wave whatever it holds (rows a wave does not need come
-// through an empty resource: zeros, no memory access), so that one vmcnt value
-// waits for the oldest stage. Each K16 fragment read from LDS feeds four
-// MFMAs. Blocks take the forward's order (heads pinned to XCDs, longest
-// blocks first across the XCD's heads). dS carries the head's 2^kh and K16
-// its tile's 2^ek: the accumulators are rescaled when ek changes and the
-// epilogue multiplies by scale 2^-(kh + ek) (exact). Blocks cover the heads
-// bh0 .. bh0 + G - 1 (the dS tiles in the workspace).
+// block shares the K rows, 32 keys per stage, four stages deep (two in flight
+// while one is worked and one is converted); a stage issues the same number
+// of DMA instructions per wave whatever it holds (rows a wave does not need
+// come through an empty resource: zeros, no memory access), so that one vmcnt
+// value waits for the oldest stage. The K rows come in the input dtype and
+// are converted in LDS, one stage ahead, to the fp16 copy K16 = K 2^ek that
+// the dK/dV kernel formed for the same 32 keys (ek: its exponent, read from
+// kexp; the conversion is the same function, so K16 is bit-identical): the
+// backward keeps no fp16 copy of K in HBM, and this kernel's spare VALU does
+// the conversion. Each K16 fragment read from LDS feeds four MFMAs. Blocks
+// take the forward's order (heads pinned to XCDs, longest blocks first across
+// the XCD's heads). dS carries the head's 2^kh and K16 its 32 keys' 2^ek: the
+// accumulators are rescaled when ek changes and the epilogue multiplies by
+// scale 2^-(kh + ek) (exact). Blocks cover the heads bh0 .. bh0 + G - 1 (the
+// dS tiles in the workspace).
 // ============================================================================
 constexpr int kDqW = kQB;           // waves per dQ block, one 64-query tile each
 constexpr int kDqM = kQB * 64;      // queries per dQ block
 constexpr int kDqS = 4;             // stages (32 keys each)
 
 template <int D> struct DqSmem {
-  short k[kDqS][32 * D];          // K16 rows
+  short k[kDqS][32 * D];          // K rows (converted in place to K16)
   short s[kDqS][kDqW][32 * 64];   // each wave's dS^T rows
 };
 
 template <typename T, int D, int MODE>
-__global__ __launch_bounds__(64 * kDqW, 1) void attn_bwd_dq_k(AttnArgs a, const f16* __restrict__ k16,
-                                                              const int* __restrict__ kexp,
+__global__ __launch_bounds__(64 * kDqW, 1) void attn_bwd_dq_k(AttnArgs a, const int* __restrict__ kexp,
                                                               const int* __restrict__ khead,
                                                               const f16* __restrict__ dst, int bh0, int G) {
   typedef Mfma<T> M;
@@ -595,10 +594,12 @@ __global__ __launch_bounds__(64 * kDqW, 1) void attn_bwd_dq_k(AttnArgs a, const 
   const int nt = (T_ + 63) / 64;
   const int qtw = (q0 >> 6) + w;            // this wave's 64-query tile
   const bool wact = qtw < nt;
-  const f16* kp = k16 + (int64_t)bh * T_ * D;
-  const uint32_t kbytes = row_bytes(T_, D, D);
+  const T* kp = (const T*)a.k + b * a.sk[0] + h * a.sk[1];
+  const uint32_t sk2 = (uint32_t)a.sk[2];
+  const uint32_t kbytes = row_bytes(T_, sk2, D);
   const f16* run = dst + ((int64_t)bl * ds_tiles_per_head(nt, kCausal) + ds_run_base(qb, nt, kCausal)) * 4096;
-  const int* kexp_h = kexp + (int64_t)bh * nt;
+  const int ng = (T_ + 31) / 32;  // 32-key groups (exponents)
+  const int* kexp_h = kexp + (int64_t)bh * ng;
   const int n_kt = kCausal ? std::min((q0 >> 6) + kDqW, nt) : nt;
   const int n_st = 2 * n_kt;                // stages: 32-key halves
   const bool kw_ = w < KW;
@@ -612,7 +613,7 @@ __global__ __launch_bounds__(64 * kDqW, 1) void attn_bwd_dq_k(AttnArgs a, const 
 
   KDma dk;
   SDma dd;  // the wave's own dS rows
-  dk.init(kw_ ? w : 0, lane, D);
+  dk.init(kw_ ? w : 0, lane, sk2);
   // LDS slot (row, p) of the swizzled [32][64] stage tile takes data chunk
   // c = p ^ swz(row) of key row `row`, which the stored layout keeps in 1 KB
   // block 2 (c / 4) + row / 16 at position 16 (c % 4) + row % 16
@@ -626,15 +627,15 @@ __global__ __launch_bounds__(64 * kDqW, 1) void attn_bwd_dq_k(AttnArgs a, const 
   // stage st: rows 32 (st & 1) .. of key tile st >> 1
   auto issue = [&](int buf, int st) __attribute__((always_inline)) {
     const int kt = st >> 1;
-    if (kw_) dk.issue(sm.k[buf], kp, kbytes, 32 * st, D, w);
+    if (kw_) dk.issue(sm.k[buf], kp, kbytes, 32 * st, sk2, w);
     const bool have = tile_in(kt);
     dd.template issue<true>(sm.s[buf][w], run + (have ? ((int64_t)kt * kQB + w) * 4096 : 0), have ? 8192u : 0u,
                             32 * (st & 1), 64, 0);
   };
-  // stage st has landed when at most the stages issued after it are in flight
-  // (loads complete in order); the count is an immediate
-  auto wait_for = [&](int st) __attribute__((always_inline)) {
-    const int after = std::min(n_st - 1 - st, kDqS - 2) * ndma;
+  // stage st has landed when at most the stages issued after it (up to `ahead`
+  // of them) are in flight (loads complete in order); the count is an immediate
+  auto wait_for = [&](int st, int ahead) __attribute__((always_inline)) {
+    const int after = std::min(n_st - 1 - st, ahead) * ndma;
     switch (after) {
       case 2 * (KDma::SEGS + SDma::SEGS): __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * (KDma::SEGS + SDma::SEGS))); break;
       case KDma::SEGS + SDma::SEGS: __builtin_amdgcn_s_waitcnt(0x0F70 | (KDma::SEGS + SDma::SEGS)); break;
@@ -643,26 +644,39 @@ __global__ __launch_bounds__(64 * kDqW, 1) void attn_bwd_dq_k(AttnArgs a, const 
       default: dma_wait();
     }
   };
+  // exponent of stage st's 32 keys (a stage past the last key group holds only
+  // zero rows: any exponent serves)
+  auto stage_exp = [&](int st) __attribute__((always_inline)) { return kexp_h[std::min(st, ng - 1)]; };
+  // stage st's K rows to K16 in place: one 16-byte chunk per thread
+  auto convert = [&](short* kt_, int st) __attribute__((always_inline)) {
+    const float f = ldexpf(1.f, stage_exp(st));
+#pragma unroll
+    for (int c = tid; c < 32 * D / 8; c += 64 * kDqW) {
+      i16x8* p = reinterpret_cast<i16x8*>(kt_ + 8 * c);
+      *p = to_f16x8s<T>(*p, f);
+    }
+  };
   int ek = 0;
   for (int st = 0; st < kDqS - 1; ++st)
     if (st < n_st) issue(st, st);
-  wait_for(0);
+  wait_for(std::min(1, n_st - 1), 1);
+  __syncthreads();
+  convert(sm.k[0], 0);
+  if (n_st > 1) convert(sm.k[1], 1);
   __syncthreads();
   // unrolled by four: static buffers
   auto step = [&](int st, auto buf_tag) __attribute__((always_inline)) {
     constexpr int buf = decltype(buf_tag)::value;
     if (st + kDqS - 1 < n_st) issue((buf + kDqS - 1) % kDqS, st + kDqS - 1);
     const int kt = st >> 1;
-    if constexpr ((buf & 1) == 0) {
-      const int ekt = kexp_h[kt];
-      if (ekt != ek) {
-        const float f = ldexpf(1.f, ekt - ek);
+    const int est = stage_exp(st);
+    if (est != ek) {
+      const float f = ldexpf(1.f, est - ek);
 #pragma unroll
-        for (int ds = 0; ds < DS; ++ds)
+      for (int ds = 0; ds < DS; ++ds)
 #pragma unroll
-          for (int qc = 0; qc < 4; ++qc) acc[ds][qc] *= f;
-        ek = ekt;
-      }
+        for (int qc = 0; qc < 4; ++qc) acc[ds][qc] *= f;
+      ek = est;
     }
     if (tile_in(kt)) {
       const short* sd = sm.s[buf][w];
@@ -676,9 +690,12 @@ __global__ __launch_bounds__(64 * kDqW, 1) void attn_bwd_dq_k(AttnArgs a, const 
         for (int qc = 0; qc < 4; ++qc) acc[ds][qc] = mma_f16(at, bq[qc], acc[ds][qc]);
       }
     }
-    // the next stage has landed, and every wave is done with this stage's buffers
-    if (st + 1 < n_st) wait_for(st + 1);
+    // the stage after the next has landed (the next is converted), and every
+    // wave is done with this stage's buffers
+    if (st + 2 < n_st) wait_for(st + 2, 1);
     __syncthreads();
+    // its K rows to K16 (read by step st + 2, after the next barrier)
+    if (st + 2 < n_st) convert(sm.k[(buf + 2) % kDqS], st + 2);
   };
   for (int st = 0; st < n_st; st += 4) {
     step(st, std::integral_constant<int, 0>{});
@@ -744,6 +761,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
                                                          const f16* __restrict__ q16,
                                                          const int* __restrict__ qexp,
                                                          const int* __restrict__ khead,
+                                                         int* __restrict__ kexp,
                                                          f16* __restrict__ dst, int bh0, int G) {
   typedef Mfma<T> M;
   constexpr int KK = D / 32;
@@ -815,6 +833,8 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
 #pragma unroll
       for (int o = 32; o > 0; o >>= 1) km = fmaxf(km, __shfl_xor(km, o, 64));
       ekw = tile_exp(km);
+      // the dQ kernel converts these 32 keys with the same exponent
+      if (lane == 0 && kw < T_) kexp[(int64_t)bh * ((T_ + 31) / 32) + (kw >> 5)] = ekw;
       const float fk = ldexpf(1.f, ekw);
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
@@ -1165,9 +1185,8 @@ static BwdWs bwd_ws(void* base, int64_t B, int64_t H, int64_t T, int64_t D, bool
   auto take = [&](size_t n) { char* q = p + o; o += al(n); return q; };
   w.stats = reinterpret_cast<float2*>(take(rows * sizeof(float2)));
   w.q16 = reinterpret_cast<f16*>(take(rows * (size_t)D * sizeof(f16)));
-  w.k16 = reinterpret_cast<f16*>(take(rows * (size_t)D * sizeof(f16)));
-  w.kexp = reinterpret_cast<int*>(take(tiles * sizeof(int)));
   w.qexp = reinterpret_cast<int*>(take(tiles * sizeof(int)));
+  w.kexp = reinterpret_cast<int*>(take((size_t)BH * (size_t)((T + 31) / 32) * sizeof(int)));
   w.vnrm = reinterpret_cast<float*>(take(tiles * sizeof(float)));
   w.abnd = reinterpret_cast<float*>(take(tiles * sizeof(float)));
   w.bbnd = reinterpret_cast<float*>(take(tiles * sizeof(float)));
@@ -1219,10 +1238,10 @@ int launch_bwd(const AttnArgs& a, void* ws, hipStream_t st) {
   for (int bh0 = 0; bh0 < BH; bh0 += w.group) {
     const int G = std::min(w.group, BH - bh0);
     hipLaunchKernelGGL((attn_bwd_dkv_k<T, D, MODE>), dim3((unsigned)(nb * G)), dim3(512), 0, st, a, w.stats, w.q16,
-                       w.qexp, w.khead, w.dst, bh0, G);
+                       w.qexp, w.khead, w.kexp, w.dst, bh0, G);
     if (int rc = check_launch("kat_attn_bwd (dkv, mfma)")) return rc;
-    hipLaunchKernelGGL((attn_bwd_dq_k<T, D, MODE>), dim3((unsigned)(nbq * G)), dim3(64 * kDqW), 0, st, a, w.k16,
-                       w.kexp, w.khead, w.dst, bh0, G);
+    hipLaunchKernelGGL((attn_bwd_dq_k<T, D, MODE>), dim3((unsigned)(nbq * G)), dim3(64 * kDqW), 0, st, a, w.kexp,
+                       w.khead, w.dst, bh0, G);
     if (int rc = check_launch("kat_attn_bwd (dq, mfma)")) return rc;
   }
   return 0;

@@ -159,7 +159,7 @@ int kat_attn_fwd(const void* q, const void* k, const void* v, void* out, float* 
                  int causal, int dtype, void* stream);
 
 /* Workspace bytes kat_attn_bwd needs. On the MFMA path it holds, besides
- * per-row and per-tile values and fp16 copies of Q and K, the fp16 dS tiles
+ * per-row and per-tile values and an fp16 copy of Q, the fp16 dS tiles
  * of a group of heads (the causal half of each head's T x T, 64 x 64 tiles;
  * at most 4 GiB of them, or one head's; KAT_ATTN_DS_CAP_BYTES in the
  * environment lowers the cap). */
@@ -174,8 +174,8 @@ size_t kat_attn_bwd_workspace_size(int64_t B, int64_t H, int64_t T, int64_t D, i
  * (kernels backward.py:62-158 and 165-266). Deterministic. On the MFMA path
  * dS is computed once (by the dK/dV kernel, which stores it for dQ), and it
  * and the copies of Q and K its products take enter the MFMA in fp16, each
- * with a power-of-two scale chosen from the data (per 64-row tile for Q and
- * K, from a bound on |dS| per head for dS) and undone exactly: the gradients
+ * with a power-of-two scale chosen from the data (per 64-row tile for Q, per
+ * 32 keys for K, from a bound on |dS| per head for dS) and undone exactly: the gradients
  * are exactly equivariant under power-of-two scalings
  * of q, k, v and dout, and per-tile maxima of |q| and |k| in [2^-46, 2^55]
  * are covered. The dS bounds assume (out, L) are the forward's outputs for

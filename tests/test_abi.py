@@ -44,11 +44,13 @@ def test_load_and_version():
 def test_workspace_sizes():
     lib = _lib.load()
     assert lib.kat_attn_bwd_workspace_size(4, 16, 4096, 128, 1) >= 4 * 16 * 4096 * 4
-    # bf16 / fp16 with an MFMA head dim: per-row stats (8 B) plus fp16 copies of
-    # Q and K; fp32 only needs Delta and cinv
+    # bf16 / fp16 with an MFMA head dim: per-row stats (8 B), the fp16 copy of
+    # Q and the fp16 dS tiles (the causal half of T x T per head: 64 x 64
+    # tiles of 8 KB); fp32 only needs Delta and cinv
     rows = 4 * 16 * 4096
-    assert lib.kat_attn_bwd_workspace_size(4, 16, 4096, 128, 1) >= rows * 8 + 2 * rows * 128 * 2
-    assert lib.kat_attn_bwd_workspace_size(4, 16, 4096, 64, 2) >= rows * 8 + 2 * rows * 64 * 2
+    tiles = 64 * 65 // 2
+    assert lib.kat_attn_bwd_workspace_size(4, 16, 4096, 128, 1) >= rows * 8 + rows * 128 * 2 + 64 * tiles * 8192
+    assert lib.kat_attn_bwd_workspace_size(4, 16, 4096, 64, 2) >= rows * 8 + rows * 64 * 2 + 64 * tiles * 8192
     assert lib.kat_attn_bwd_workspace_size(4, 16, 4096, 128, 0) < rows * 16
     assert lib.kat_attn_bwd_workspace_size(0, 16, 4096, 128, 1) == 0
     n = lib.kat_men_bwd_workspace_size(16384, 4096, 1)
