@@ -256,7 +256,7 @@ def test_mfma_backward_is_invariant_to_the_upstream_gradient_scale(gpu, D, maske
 # ------------------------------------------------- input magnitude range ----
 # The MFMA backward rounds dS, and copies of Q and K, to fp16 (range 2^-14 ..
 # 65504). Each copy carries a power-of-two scale chosen from the data (per
-# 64-row tile for Q and K, per row and per head for dS), so inputs far outside
+# 64-row tile for Q, per 32 keys for K, per head for dS), so inputs far outside
 # N(0, 1) must still meet the bar. Outputs scale with the inputs: each check
 # divides got and ref by the known factor of that output and applies the
 # unit-scale bar, 2e-2 + 1/2 ulp.
@@ -294,6 +294,47 @@ def test_mfma_backward_input_range_bf16(gpu, D, case, monkeypatch):
     # s = scale q.k changes only for qk1e-4 (where it shrinks to ~1e-9, the bias alone)
     factors = {"o": fv, "dq": fv * fd * fk, "dk": fv * fd * fq, "dv": fd}
     _scaled_check(q, k, v, do, slopes, scale, factors)
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_mfma_backward_key_groups_of_different_magnitude(gpu, D, dtype, monkeypatch):
+    # K's fp16 form carries one exponent per 32 keys, chosen by the dK/dV
+    # kernel and reused by the dQ kernel, which rescales its accumulators
+    # whenever the next 32 keys bring another exponent. Keys whose magnitude
+    # cycles 2^s, 1, 2^-s from one 32-key group to the next give every group
+    # a different exponent (also inside each 64-key tile): a wrong exponent
+    # for any group would move that group's share of dq or dk by 2^s.
+    _pin_mfma(monkeypatch, D)
+    B, H, T = 1, 2, 300
+    q, k, v, do = (t.float() for t in _inputs(47 + D, B, H, T, D, torch.float32))
+    sh = 12 if dtype == torch.float16 else 20
+    gsc = torch.tensor([2.0 ** (sh * (1 - (j // 32) % 3)) for j in range(T)])
+    k = k * gsc.view(1, 1, T, 1).to(k.device)
+    q, k, v, do = (t.to(dtype) for t in (q, k, v, do))
+    slopes = F.compute_alibi_slopes(H)
+    scale = 1.0 / math.sqrt(D)
+    o, L, dq, dk, dv = _run(q, k, v, do, slopes.to(dev), scale)
+    ro, rL = O.attention_fwd(q, k, v, slopes, scale, dtype=torch.float32)
+    rq, rk, rv = O.attention_bwd(q, k, v, o, L, do, slopes, scale, dtype=torch.float32)
+    assert _rel_max(L, rL) <= 1e-2
+    for name, got, ref in (("o", o, ro), ("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
+        got = got.detach().to("cpu", torch.float64)
+        ref = ref.detach().to("cpu", torch.float64)
+        assert bool(torch.isfinite(got).all()), name
+        rel = float((got - ref).norm() / ref.norm())
+        print(f"{name}: max err / max |ref| {_rel_max(got, ref):.3e}, relL2 {rel:.3e}")
+        assert _rel_max(got, ref) <= 2e-2 and rel <= 1e-2, (name, _rel_max(got, ref), rel)
+        if name == "dv":
+            # each group's rows against that group's own scale (dv = P^T dO
+            # takes P from the S recomputed on the groups' fp16 keys; dk is
+            # checked over the whole tensor only: the dS of the 2^s groups
+            # lies so far below the head's largest that fp16 holds it in its
+            # subnormal range, the documented limit of the one dS exponent
+            # per head)
+            for j0 in range(0, T, 32):
+                gg, gr = got[:, :, j0:j0 + 32], ref[:, :, j0:j0 + 32]
+                assert _rel_max(gg, gr) <= 2e-2, (name, j0, _rel_max(gg, gr))
 
 
 @pytest.mark.parametrize("D", [32, 64, 128])
