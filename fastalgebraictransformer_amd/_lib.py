@@ -49,6 +49,7 @@ _SIGNATURES = {
                       _I64P, _I64P, _F, _F, _INT, _INT, _P], _INT),
     "kat_attn_fwd_masked": ([_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64P,
                              _I64P, _F, _F, _INT, _INT, _P], _INT),
+    "kat_attn_bwd_masked_workspace_size": ([_I64, _I64, _I64, _I64, _INT, _INT], _SZ),
     "kat_attn_bwd_masked": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _P, _SZ, _I64,
                              _I64, _I64, _I64, _I64P, _I64P, _F, _F, _INT, _INT, _P], _INT),
     "kat_attn_decode_workspace_size": ([_I64, _I64, _I64, _I64, _INT], _SZ),

@@ -34,7 +34,10 @@ def _attn_bwd_into(q, k, v, output, L, grad_output, dq, dk, dv, alibi_slopes, sc
     _warn_if_tiled((q, k, v, output, grad_output, dq, dk, dv), D, q.dtype)
     slopes = alibi_slopes.to(device=q.device, dtype=torch.float32).contiguous()
     code = _lib.dtype_code(q)
-    ws_bytes = lib.kat_attn_bwd_workspace_size(B, H, T, D, code)
+    if extended:
+        ws_bytes = lib.kat_attn_bwd_masked_workspace_size(B, H, T, D, code, int(bool(causal)))
+    else:
+        ws_bytes = lib.kat_attn_bwd_workspace_size(B, H, T, D, code)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
     strides = _lib.i64_array(
         _bht_strides(q) + _bht_strides(k) + _bht_strides(v) + _bht_strides(output) +

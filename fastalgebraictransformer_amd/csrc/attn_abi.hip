@@ -59,16 +59,17 @@ template <typename T> bool rows16(const void* p, const int64_t* s) {
 }
 
 // workspace of the tiled path: Delta [B*H*T] fp32, then cinv [B*H*T] fp32 (each
-// 256-byte aligned); the MFMA path lays out its own (attn_mfma_workspace). One
-// buffer of the larger size serves whichever path a call takes.
+// 256-byte aligned); the MFMA path lays out its own (attn_mfma_workspace), sized
+// for the call's mode (causal or not). One buffer of the larger size serves
+// whichever path a call takes.
 size_t stat_bytes(int64_t B, int64_t H, int64_t T) {
   return (((size_t)(B * H * T) * sizeof(float)) + 255) & ~(size_t)255;
 }
 size_t delta_bytes(int64_t B, int64_t H, int64_t T) { return 2 * stat_bytes(B, H, T); }
-size_t bwd_workspace(int64_t B, int64_t H, int64_t T, int64_t D, int dtype) {
+size_t bwd_workspace(int64_t B, int64_t H, int64_t T, int64_t D, int dtype, bool causal) {
   size_t n = delta_bytes(B, H, T);
   if ((dtype == KAT_BF16 || dtype == KAT_F16) && attn_mfma_supported((int)D))
-    n = std::max(n, attn_mfma_workspace(B, H, T, D));
+    n = std::max(n, attn_mfma_workspace(B, H, T, D, causal));
   return n;
 }
 
@@ -153,7 +154,13 @@ extern "C" int kat_attn_fwd_masked(const void* q, const void* k, const void* v, 
 extern "C" size_t kat_attn_bwd_workspace_size(int64_t B, int64_t H, int64_t T, int64_t D,
                                               int dtype) {
   if (B <= 0 || H <= 0 || T <= 0 || D < 0) return 0;
-  return bwd_workspace(B, H, T, D, dtype);
+  return bwd_workspace(B, H, T, D, dtype, true);
+}
+
+extern "C" size_t kat_attn_bwd_masked_workspace_size(int64_t B, int64_t H, int64_t T, int64_t D,
+                                                     int dtype, int causal) {
+  if (B <= 0 || H <= 0 || T <= 0 || D < 0) return 0;
+  return bwd_workspace(B, H, T, D, dtype, causal != 0);
 }
 
 static int attn_bwd_impl(const char* nm, const void* q, const void* k, const void* v,
@@ -171,7 +178,7 @@ static int attn_bwd_impl(const char* nm, const void* q, const void* k, const voi
   if (key_mask && mask_stride_b < T && B > 1)
     return fail(KAT_EINVAL, "%s: key-mask batch stride %lld < T %lld", nm, (long long)mask_stride_b,
                 (long long)T);
-  const size_t need = bwd_workspace(B, H, T, D, dtype);
+  const size_t need = bwd_workspace(B, H, T, D, dtype, causal != 0);
   if (!workspace || workspace_bytes < need)
     return fail(KAT_EINVAL, "%s: workspace %zu bytes < required %zu", nm, workspace_bytes, need);
   a.q = q;

@@ -40,13 +40,15 @@ template <typename T> int attn_delta(const AttnArgs& a, float* delta, float* cin
 template <typename T> int attn_bwd_generic(const AttnArgs& a, const float* delta, hipStream_t st);
 
 // bf16 / fp16 MFMA kernels; return KAT_EUNSUPPORTED when the shape is not covered.
-// The backward runs its own prep pass; ws holds attn_mfma_workspace() bytes:
-// per-row stats (float2), fp16 copies of Q and K ([B*H][T][D] each), per-tile
-// exponents and dS-bound parts, per-head dS exponents, and the fp16 dS tiles
-// of a group of heads (at most 4 GiB of them, or one head's).
+// The backward runs its own prep pass; ws holds attn_mfma_workspace() bytes for
+// the call's mode: per-row stats (float2), an fp16 copy of Q ([B*H][T][D]),
+// per-tile exponents and dS-bound parts, per-32-key K exponents, the fp16 dS
+// tiles of a group of heads or of one band of a head's keys (at most 4 GiB of
+// them, or one band of 512 keys), and for banded calls one head's fp32 dQ
+// partial sums.
 template <typename T> int attn_fwd_mfma(const AttnArgs& a, hipStream_t st);
 template <typename T> int attn_bwd_mfma(const AttnArgs& a, void* ws, hipStream_t st);
 bool attn_mfma_supported(int D);
-size_t attn_mfma_workspace(int64_t B, int64_t H, int64_t T, int64_t D);
+size_t attn_mfma_workspace(int64_t B, int64_t H, int64_t T, int64_t D, bool causal);
 
 }  // namespace kat

@@ -3,8 +3,9 @@
 // The attention math runs in three MFMA kernels, beside two streaming passes:
 //   attn_fwd_k         O, L      query-tile blocks; K, V tiles stream through LDS
 //   attn_bwd_prep_k    fp16 copy of Q with per-tile exponents, Delta and the
-//                                row stats, the parts of each head's dS bound
-//   attn_bwd_stscale_k the head's dS exponent; scales the row stats by it
+//                                row stats, the parts of the dS bounds
+//   attn_bwd_stscale_k the dS exponent of each query tile; scales the row
+//                                stats by it
 //   attn_bwd_dkv_k     dK, dV    key-tile blocks; fp16 Q and dO tiles stream; the
 //                                waves split into a dV role and a dK role; the dK
 //                                role also stores the fp16 dS it computes
@@ -48,12 +49,14 @@
 //     of the MFMA scaled by both tiles' factors, which the bias and the scale
 //     applied to it absorb; an accumulator is rescaled when a new tile brings
 //     another exponent.
-//   * dS (one copy, which both dK and dQ take): per head, 2^kh with kh from
+//   * dS (one copy, which both dK and dQ take): per 64-query tile, 2^kq from
 //     the bound 4 cinv_i w |dP_ij - Delta_i| <= min(4.1, 1.125 4 cinv_i)
 //     (||dO_i||_2 ||v_j||_2 + |Delta_i|) (w = t^3 r^2 <= 1.11, and
 //     4 cinv_i w = p g <= 4 when L is the forward's row sum), maximised over
-//     the head, so that every scaled dS stays below 2^14 and reaches fp16's
-//     subnormal range only 27 binades below the head's largest.
+//     the tile's rows and the head's keys, so that every scaled dS stays
+//     below 2^14; kq is the head's exponent unless the tile's bound lies
+//     2^8 or more below the head's (then in steps of 2^8), so a dS reaches
+//     fp16's subnormal range only 19 binades or more below its tile's bound.
 // So the gradients are exactly equivariant under power-of-two scalings of q,
 // k, v and dO, and dO's scale (a training step's is ~1e-5 .. 1e-7 per element)
 // does not move dS into fp16's subnormal range.
@@ -335,7 +338,7 @@ __global__ __launch_bounds__(256, QS == 2 ? 2 : 1) void attn_fwd_k(AttnArgs a) {
 // Everything the backward's MFMA kernels take besides the inputs (the
 // workspace, laid out by bwd_ws below).
 struct BwdWs {
-  float2* stats;  // per row (4 cinv, -4 cinv Delta) [B*H][T], then x 2^kh
+  float2* stats;  // per row (4 cinv, -4 cinv Delta) [B*H][T], then x 2^kq (the row's tile)
   f16* q16;       // fp16 copy of Q [B*H][T][D], scaled per 64-row tile
   int* qexp;      // per 64-row tile [B*H][nt]: its exponents
   int* kexp;      // per 32-key group [B*H][ceil(T / 32)]: the dK/dV kernel's
@@ -343,9 +346,11 @@ struct BwdWs {
   float* vnrm;    // per tile: max_j ||v_j||_2
   float* abnd;    // per tile: max_i c_i ||dO_i||_2    (c_i = min(4.1, 1.125 * 4 cinv_i))
   float* bbnd;    // per tile: max_i c_i |Delta_i|
-  int* khead;     // per head [B*H]: dS exponent kh
-  f16* dst;       // dS^T tiles of a group of heads (layout at attn_bwd_dkv_k)
+  int* ktile;     // per 64-query tile [B*H][nt]: dS exponent kq
+  f16* dst;       // dS^T tiles of a group of heads, or of one band of one head
+  float* dqacc;   // banded calls: fp32 dQ partial sums of one head [nt][64][D]
   int group;      // heads per dK / dV + dQ launch pair (the dS^T tiles' capacity)
+  int band;       // key tiles per band (nt: one band)
   size_t bytes;
 };
 
@@ -361,7 +366,8 @@ struct BwdWs {
 //             |dS_ij| = 4 cinv_i w |dP_ij - Delta_i| with w = t^3 r^2 <= 1.11 and
 //             4 cinv_i w = p g <= 4 (p <= 1 when L is the forward's row sum), and
 //             |dP_ij - Delta_i| <= ||dO_i||_2 ||v_j||_2 + |Delta_i|, so
-//             |dS_ij| <= abnd_max vnrm_max + bbnd_max over the head.
+//             |dS_ij| <= abnd_t vnrm_max + bbnd_t for the rows i of tile t
+//             (vnrm_max: over the head).
 // A row's LPR = D / 8 lanes are consecutive lanes of one wave; the block covers
 // its 64 rows in NP passes of 256 / LPR rows.
 // ============================================================================
@@ -455,12 +461,21 @@ __global__ __launch_bounds__(256) void attn_bwd_prep_k(AttnArgs a, BwdWs ws) {
   }
 }
 
-// The head's dS exponent kh = ds_exp(abnd_max vnrm_max + bbnd_max) (maxima over
-// the head's tiles), so that every 2^kh dS of the head lies below 2^14; the
-// per-row stats are multiplied by 2^kh in place (exact), so that
+// dS exponents, one per 64-query tile t. kh = ds_exp(abnd_max vnrm_max +
+// bbnd_max) is the exponent of the head's bound and e_t = ds_exp(abnd_t
+// vnrm_max + bbnd_t) >= kh that of the tile's, so that every 2^e_t dS of the
+// tile's rows lies below 2^14. A tile takes kq_t = kh + 8 floor((e_t - kh) / 8),
+// capped at kh + kTileExpSpan: kh while its bound lies within 2^8 of the
+// head's (its dS then reach fp16's subnormal range only 19 binades below their
+// own bound), so that the dK accumulators, rescaled whenever the exponent
+// changes from one query tile to the next, are rescaled only between tiles of
+// very different magnitude; the cap bounds the factor of such a rescale. The
+// per-row stats are multiplied by 2^kq_t in place (exact), so that
 // dS = w (stats.x dP + stats.y) comes out scaled. Blocks of 256 rows of one
 // head; each reduces the head's tile values itself (no atomics, no ordering
-// between blocks) and the head's first block records kh.
+// between blocks) and records the exponents of its own tiles.
+constexpr int kTileExpSpan = 40;  // a multiple of 8
+
 __global__ __launch_bounds__(256) void attn_bwd_stscale_k(BwdWs ws, int T, int cpb) {
   __shared__ float red[3][4];
   const int nt = (T + 63) / 64;
@@ -489,10 +504,12 @@ __global__ __launch_bounds__(256) void attn_bwd_stscale_k(BwdWs ws, int T, int c
   am = fmaxf(fmaxf(red[1][0], red[1][1]), fmaxf(red[1][2], red[1][3]));
   bm = fmaxf(fmaxf(red[2][0], red[2][1]), fmaxf(red[2][2], red[2][3]));
   const int kh = ds_exp(fmaf(am, vm, bm));
-  if (ch == 0 && tid == 0) ws.khead[bh] = kh;
   const int r = 256 * ch + tid;
   if (r < T) {
-    const float f = ldexpf(1.f, kh);
+    const int64_t t = (int64_t)bh * nt + (r >> 6);
+    const int kq = kh + std::min((ds_exp(fmaf(ws.abnd[t], vm, ws.bbnd[t])) - kh) & ~7, kTileExpSpan);
+    if ((r & 63) == 0) ws.ktile[t] = kq;
+    const float f = ldexpf(1.f, kq);
     const int64_t x = (int64_t)bh * T + r;
     const float2 s = ws.stats[x];
     ws.stats[x] = make_float2(s.x * f, s.y * f);
@@ -501,13 +518,18 @@ __global__ __launch_bounds__(256) void attn_bwd_stscale_k(BwdWs ws, int T, int c
 
 // ============================================================================
 // dS^T tiles. The dK / dV kernel stores the fp16 dS it feeds its dK product
-// (2^kh dS, zero where a key is masked or past its query) for every 64-key x
+// (2^kq dS, zero where a key is masked or past its query) for every 64-key x
 // 64-query tile (kt, qt) the backward touches, 8 KB each. Tiles are grouped by
 // the dQ kernel's blocks of kQB query tiles so that each dQ block streams one
 // contiguous run: a head's runs follow each other by query block qb, and
 // within a run come, key tile by key tile (kt = 0 .. the block's last, causal;
 // every kt otherwise), the block's kQB query tiles side by side (in causal
 // mode the tiles with kt > qt inside a run are not written and not read).
+// Long sequences whose tiles exceed the workspace's cap run in bands of key
+// tiles [kb0, kb0 + nk) (kb0 and nk multiples of kQB, the last band shorter):
+// a band keeps the same layout restricted to its key tiles, with runs for the
+// query blocks that hold any of them (causal: qb >= kb0 / kQB). The whole head
+// is the band kb0 = 0, nk = nt.
 // Logically a tile is 64 key rows x 64 query columns; within each 32-query
 // half the columns follow the dK kernel's MFMA operand order (column
 // 8 g + 4 h + j holds query 16 h + 4 g + j). It is stored as eight 1 KB
@@ -521,15 +543,20 @@ __global__ __launch_bounds__(256) void attn_bwd_stscale_k(BwdWs ws, int T, int c
 // ============================================================================
 constexpr int kQB = 8;  // 64-query tiles per dQ block
 
-__host__ __device__ inline int64_t ds_run_base(int qb, int nt, bool causal) {
-  return causal ? (int64_t)kQB * kQB * qb * (qb + 1) / 2 : (int64_t)qb * kQB * nt;
+// first tile of query block qb's run in the band [kb0, kb0 + nk): causal runs
+// hold min(nk, kQB (qb + 1) - kb0) key tiles (the last run: nk), the others nk
+__host__ __device__ inline int64_t ds_run_base(int qb, bool causal, int kb0, int nk) {
+  if (!causal) return (int64_t)qb * kQB * nk;
+  const int64_t m = qb - kb0 / kQB, f = nk / kQB;
+  const int64_t s = m <= f ? kQB * m * (m + 1) / 2 : kQB * f * (f + 1) / 2 + (m - f) * nk;
+  return kQB * s;
 }
-__host__ __device__ inline int64_t ds_tiles_per_head(int nt, bool causal) {
+__host__ __device__ inline int64_t ds_tiles_per_band(int nt, bool causal, int kb0, int nk) {
   const int nqb = (nt + kQB - 1) / kQB;
-  return ds_run_base(nqb - 1, nt, causal) + (int64_t)kQB * nt;
+  return ds_run_base(nqb - 1, causal, kb0, nk) + (int64_t)kQB * nk;
 }
-__device__ __forceinline__ int64_t ds_tile(int kt, int qt, int nt, bool causal) {
-  return ds_run_base(qt / kQB, nt, causal) + (int64_t)kt * kQB + qt % kQB;
+__device__ __forceinline__ int64_t ds_tile(int kt, int qt, bool causal, int kb0, int nk) {
+  return ds_run_base(qt / kQB, causal, kb0, nk) + (int64_t)(kt - kb0) * kQB + qt % kQB;
 }
 // query (0..31, within its half-tile) of column c of the half-tile
 __device__ __forceinline__ int ds_col_query(int c) { return 16 * ((c >> 2) & 1) + 4 * (c >> 3) + (c & 3); }
@@ -553,10 +580,14 @@ __device__ __forceinline__ int ds_col_query(int c) { return 16 * ((c >> 2) & 1) 
 // backward keeps no fp16 copy of K in HBM, and this kernel's spare VALU does
 // the conversion. Each K16 fragment read from LDS feeds four MFMAs. Blocks
 // take the forward's order (heads pinned to XCDs, longest blocks first across
-// the XCD's heads). dS carries the head's 2^kh and K16 its 32 keys' 2^ek: the
-// accumulators are rescaled when ek changes and the epilogue multiplies by
-// scale 2^-(kh + ek) (exact). Blocks cover the heads bh0 .. bh0 + G - 1 (the
-// dS tiles in the workspace).
+// the XCD's heads). dS carries its query tile's 2^kq and K16 its 32 keys'
+// 2^ek: the accumulators are rescaled when ek changes and the epilogue
+// multiplies by scale 2^-(kq + ek) (exact). Blocks cover the heads
+// bh0 .. bh0 + G - 1 (the dS tiles in the workspace) and the key tiles of the
+// band [kb0, kb0 + nk): a wave whose queries see keys before the band starts
+// from its fp32 partial sums in dqacc, and one whose queries see keys after it
+// leaves its partial sums there (divided by 2^ek, exact) instead of writing
+// dQ; the bands run in order, so the sums are added in a fixed order.
 // ============================================================================
 constexpr int kDqW = kQB;           // waves per dQ block, one 64-query tile each
 constexpr int kDqM = kQB * 64;      // queries per dQ block
@@ -569,8 +600,9 @@ template <int D> struct DqSmem {
 
 template <typename T, int D, int MODE>
 __global__ __launch_bounds__(64 * kDqW, 1) void attn_bwd_dq_k(AttnArgs a, const int* __restrict__ kexp,
-                                                              const int* __restrict__ khead,
-                                                              const f16* __restrict__ dst, int bh0, int G) {
+                                                              const int* __restrict__ ktile,
+                                                              const f16* __restrict__ dst, int bh0, int G,
+                                                              int kb0, int nk, float* __restrict__ dqacc) {
   typedef Mfma<T> M;
   constexpr int DS = D / 16;
   constexpr bool kCausal = (MODE & kModeCausal) != 0;
@@ -597,11 +629,14 @@ __global__ __launch_bounds__(64 * kDqW, 1) void attn_bwd_dq_k(AttnArgs a, const 
   const T* kp = (const T*)a.k + b * a.sk[0] + h * a.sk[1];
   const uint32_t sk2 = (uint32_t)a.sk[2];
   const uint32_t kbytes = row_bytes(T_, sk2, D);
-  const f16* run = dst + ((int64_t)bl * ds_tiles_per_head(nt, kCausal) + ds_run_base(qb, nt, kCausal)) * 4096;
+  const f16* run =
+      dst + ((int64_t)bl * ds_tiles_per_band(nt, kCausal, kb0, nk) + ds_run_base(qb, kCausal, kb0, nk)) * 4096;
   const int ng = (T_ + 31) / 32;  // 32-key groups (exponents)
   const int* kexp_h = kexp + (int64_t)bh * ng;
-  const int n_kt = kCausal ? std::min((q0 >> 6) + kDqW, nt) : nt;
-  const int n_st = 2 * n_kt;                // stages: 32-key halves
+  const int kt_all = kCausal ? std::min((q0 >> 6) + kDqW, nt) : nt;  // the block's key tiles: 0 .. kt_all - 1
+  const int kt_end = std::min(kb0 + nk, kt_all);
+  const int n_st = 2 * (kt_end - kb0);      // stages: 32-key halves of the band's key tiles
+  float* const part = dqacc + ((int64_t)bl * nt + qtw) * 64 * D;  // this wave's partial sums
   const bool kw_ = w < KW;
   const int ndma = (kw_ ? KDma::SEGS : 0) + SDma::SEGS;  // this wave's DMA per stage
 
@@ -624,12 +659,12 @@ __global__ __launch_bounds__(64 * kDqW, 1) void attn_bwd_dq_k(AttnArgs a, const 
     dd.off[u] = (uint32_t)((((c >> 2) * 2 + (row >> 4)) * 64 + 16 * (c & 3) + (row & 15)) * 16);
   }
   auto tile_in = [&](int kt) __attribute__((always_inline)) { return wact && (!kCausal || kt <= qtw); };
-  // stage st: rows 32 (st & 1) .. of key tile st >> 1
+  // stage st: rows 32 (st & 1) .. of key tile kb0 + (st >> 1)
   auto issue = [&](int buf, int st) __attribute__((always_inline)) {
-    const int kt = st >> 1;
-    if (kw_) dk.issue(sm.k[buf], kp, kbytes, 32 * st, sk2, w);
-    const bool have = tile_in(kt);
-    dd.template issue<true>(sm.s[buf][w], run + (have ? ((int64_t)kt * kQB + w) * 4096 : 0), have ? 8192u : 0u,
+    const int kl = st >> 1;
+    if (kw_) dk.issue(sm.k[buf], kp, kbytes, 32 * (2 * kb0 + st), sk2, w);
+    const bool have = tile_in(kb0 + kl);
+    dd.template issue<true>(sm.s[buf][w], run + (have ? ((int64_t)kl * kQB + w) * 4096 : 0), have ? 8192u : 0u,
                             32 * (st & 1), 64, 0);
   };
   // stage st has landed when at most the stages issued after it (up to `ahead`
@@ -646,7 +681,7 @@ __global__ __launch_bounds__(64 * kDqW, 1) void attn_bwd_dq_k(AttnArgs a, const 
   };
   // exponent of stage st's 32 keys (a stage past the last key group holds only
   // zero rows: any exponent serves)
-  auto stage_exp = [&](int st) __attribute__((always_inline)) { return kexp_h[std::min(st, ng - 1)]; };
+  auto stage_exp = [&](int st) __attribute__((always_inline)) { return kexp_h[std::min(2 * kb0 + st, ng - 1)]; };
   // stage st's K rows to K16 in place: one 16-byte chunk per thread
   auto convert = [&](short* kt_, int st) __attribute__((always_inline)) {
     const float f = ldexpf(1.f, stage_exp(st));
@@ -657,6 +692,17 @@ __global__ __launch_bounds__(64 * kDqW, 1) void attn_bwd_dq_k(AttnArgs a, const 
     }
   };
   int ek = 0;
+  if (kb0 > 0 && wact) {
+    // the partial sums of the earlier bands (lane order, as stored below),
+    // complete before the first DMA is issued: with these loads pending at
+    // the loop, the compiler's own waits there would also wait for the DMA
+    // issued ahead (measured: the kernel 40% slower)
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds)
+#pragma unroll
+      for (int qc = 0; qc < 4; ++qc) acc[ds][qc] = *reinterpret_cast<const f32x4*>(part + ((ds * 4 + qc) * 64 + lane) * 4);
+    dma_wait();
+  }
   for (int st = 0; st < kDqS - 1; ++st)
     if (st < n_st) issue(st, st);
   wait_for(std::min(1, n_st - 1), 1);
@@ -668,7 +714,7 @@ __global__ __launch_bounds__(64 * kDqW, 1) void attn_bwd_dq_k(AttnArgs a, const 
   auto step = [&](int st, auto buf_tag) __attribute__((always_inline)) {
     constexpr int buf = decltype(buf_tag)::value;
     if (st + kDqS - 1 < n_st) issue((buf + kDqS - 1) % kDqS, st + kDqS - 1);
-    const int kt = st >> 1;
+    const int kt = kb0 + (st >> 1);
     const int est = stage_exp(st);
     if (est != ek) {
       const float f = ldexpf(1.f, est - ek);
@@ -706,8 +752,19 @@ __global__ __launch_bounds__(64 * kDqW, 1) void attn_bwd_dq_k(AttnArgs a, const 
     }
   }
 
+  if (kt_end < kt_all) {
+    // keys after the band remain: keep the partial sums, with ek taken out
+    if (wact) {
+      const float f = ldexpf(1.f, -ek);
+#pragma unroll
+      for (int ds = 0; ds < DS; ++ds)
+#pragma unroll
+        for (int qc = 0; qc < 4; ++qc) *reinterpret_cast<f32x4*>(part + ((ds * 4 + qc) * 64 + lane) * 4) = acc[ds][qc] * f;
+    }
+    return;
+  }
   T* __restrict__ dqp = (T*)a.dq + b * a.sdq[0] + h * a.sdq[1];
-  const float osc = ldexpf(a.scale, -(khead[bh] + ek));
+  const float osc = ldexpf(a.scale, -((wact ? ktile[(int64_t)bh * nt + qtw] : 0) + ek));
   // the wave's 64 query rows through its own 64 x D staging tile in the
   // (now idle) stage buffers
   static_assert(sizeof(sm) >= kDqW * 64 * D * 2, "staging tiles fit the stage buffers");
@@ -760,9 +817,10 @@ template <typename T, int D, int MODE>
 __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float2* __restrict__ stats,
                                                          const f16* __restrict__ q16,
                                                          const int* __restrict__ qexp,
-                                                         const int* __restrict__ khead,
+                                                         const int* __restrict__ ktile,
                                                          int* __restrict__ kexp,
-                                                         f16* __restrict__ dst, int bh0, int G) {
+                                                         f16* __restrict__ dst, int bh0, int G, int kb0,
+                                                         int nk) {
   typedef Mfma<T> M;
   constexpr int KK = D / 32;
   constexpr int DS = D / 16;
@@ -774,7 +832,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
   int bl, rank;
   block_order((int)blockIdx.x, G, bl, rank);  // rank 0: the first keys (most queries)
   const int bh = bh0 + bl;
-  const int k0 = rank * kBM;
+  const int k0 = kb0 * 64 + rank * kBM;  // blocks cover the band's keys
   const int b = bh / H, h = bh - b * H;
   // the key group (and the tile conditions derived from it) as scalars; the
   // role test stays a per-lane value: as a scalar branch the two roles' code
@@ -795,17 +853,19 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
   const uint32_t stbytes = (uint32_t)T_ * 8u;
   const float slope = a.slopes[h];
   const float scale = a.scale;
-  // the stats carry dS's 2^kh (stats.x = 2^kh 4 cinv); P takes 4 cinv / 16 = cinv / 4
-  const int kh = khead[bh];
-  const float p4 = ldexpf(0.25f, -kh);
+  // the stats carry their tile's dS exponent (stats.x = 2^kq 4 cinv); P takes
+  // 4 cinv / 16 = cinv / 4, i.e. stats.x p4 with p4 = 2^-kq / 4 (set per tile)
+  float p4 = 0.25f;
   const int nt = (T_ + 63) / 64;
   const int* qexp_h = qexp + (int64_t)bh * nt;
+  const int* ktile_h = ktile + (int64_t)bh * nt;
   // D role: where this wave's dS^T goes (lane (g, li) of half-tile row
   // 16 ks + li, columns 8 g .. 8 g + 7); tiles past the head's last are not kept
   const int ktg = kw >> 6;
   const bool dst_ok = ktg < nt;
-  f16* const dsh = dst + (int64_t)bl * ds_tiles_per_head(nt, kCausal) * 4096;
+  f16* const dsh = dst + (int64_t)bl * ds_tiles_per_band(nt, kCausal, kb0, nk) * 4096;
   const uint32_t dso = (uint32_t)((grp & 1) * 2048 + lane * 8);  // block 4 (grp & 1), lane's 16 bytes
+  f16* dtile = dsh;  // the current query tile's dS^T tile
 
   // B operands: K16^T (P role) or V^T (D role) fragments; lane (g, li) holds row
   // kw + 16 ks + li, columns 32 kk + 8 g .. +7
@@ -849,8 +909,9 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
   // bias in use (negated for query chunks wholly below this wave's keys in
   // non-causal mode). S comes out of the MFMA scaled by 2^(eq + ekw) (eq: the
   // Q16 tile's exponent): cbx carries that factor and sc = scale 2^-(eq + ekw)
-  // removes it; the dK accumulators hold 2^eq times the sum.
-  int eq = 0;
+  // removes it; the dK accumulators hold 2^(eq + kq) times the sum (kq: the
+  // query tile's dS exponent), rescaled when a tile brings other exponents.
+  int eq = 0, kq = 0;
   float sfac = ldexpf(1.f, ekw);  // 2^(eq + ekw)
   f32x4 cbx = cb * sfac;
   float sc = ldexpf(scale, -ekw);
@@ -1011,21 +1072,26 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
     f32x4 (*xw)[64] = sm.x[CM & 1][grp];
     uint32_t pa[2][2], pb[2][2];
     if constexpr ((CM & 1) == 0) {
-      // a new Q16 tile: its exponent (both roles track it)
-      const int eqt = qexp_h[(qbase >> 6) + it];
+      // a new query tile: its Q16 and dS exponents (both roles track them)
+      const int eqt = qexp_h[(qbase >> 6) + it], kqt = ktile_h[(qbase >> 6) + it];
       if (eqt != eq) {
         const float f = ldexpf(1.f, eqt - eq);
         sfac *= f;
         sc = ldexpf(sc, eq - eqt);
         if constexpr (kCausal) cbx *= f;
-        if (!prole) {
-#pragma unroll
-          for (int ds = 0; ds < DS; ++ds)
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) acc[ds][ks] *= f;
-        }
-        eq = eqt;
       }
+      p4 = ldexpf(0.25f, -kqt);
+      // D role: this query tile's dS^T tile (both of its chunks)
+      dtile = dsh + ds_tile(ktg, (qbase >> 6) + it, kCausal, kb0, nk) * 4096;
+      if (!prole && eqt + kqt != eq + kq) {
+        const float f = ldexpf(1.f, (eqt + kqt) - (eq + kq));
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds)
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks) acc[ds][ks] *= f;
+      }
+      eq = eqt;
+      kq = kqt;
     }
     if constexpr (!kCausal) {
       const bool above = kw > qc + 31;
@@ -1097,7 +1163,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
         // dS^T for the dQ kernel: 16 bytes per lane and ks (streaming stores:
         // the dQ kernel reads them back only after this kernel)
         if (dst_ok) {
-          f16* const tb = dsh + ds_tile(ktg, qc >> 6, nt, kCausal) * 4096 + (r0 >> 5) * 1024;
+          f16* const tb = dtile + (r0 >> 5) * 1024;
 #pragma unroll
           for (int ks = 0; ks < 2; ++ks)
             __builtin_nontemporal_store(pack_frag(pa[ks][0], pa[ks][1], pb[ks][0], pb[ks][1]),
@@ -1106,7 +1172,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
         m2(std::false_type{}, r0, pa, pb, sm.q[buf]);
       } else if (dst_ok && c < n_ch && (!kCausal || (c >> 1) >= (grp >> 1))) {
         // a skipped chunk inside a kept tile: its dS is zero
-        f16* const tb = dsh + ds_tile(ktg, qc >> 6, nt, kCausal) * 4096 + (r0 >> 5) * 1024;
+        f16* const tb = dtile + (r0 >> 5) * 1024;
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks)
           __builtin_nontemporal_store(i16x8{0, 0, 0, 0, 0, 0, 0, 0}, reinterpret_cast<i16x8*>(tb + dso + 512 * ks));
@@ -1126,7 +1192,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
 
   T* __restrict__ outp = prole ? (T*)a.dv + b * a.sdv[0] + h * a.sdv[1] : (T*)a.dk + b * a.sdk[0] + h * a.sdk[1];
   const int64_t ostr = prole ? a.sdv[2] : a.sdk[2];
-  const float osc = prole ? 1.f : ldexpf(scale, -(kh + eq));  // dK: dS's 2^kh and Q16's 2^eq undone (exact)
+  const float osc = prole ? 1.f : ldexpf(scale, -(kq + eq));  // dK: dS's 2^kq and Q16's 2^eq undone (exact)
   // the wave's 32 rows (keys) through its own 32 x D staging tile in the now
   // idle tile buffers (8 waves x 32 x D x 2 bytes = the Q16 and dO buffers)
   static_assert(sizeof(sm.q) + sizeof(sm.o) >= 8 * 32 * D * 2 && offsetof(DkvSmem<D>, q) == 0 &&
@@ -1154,14 +1220,20 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
 bool attn_mfma_supported(int D) { return D == 32 || D == 64 || D == 128; }
 
 // Backward workspace (each part 256-byte aligned): per-row stats (float2), the
-// fp16 copies of Q and K ([B*H][T][D] each), the per-tile exponents and bound
-// parts ([B*H][nt] each, nt = ceil(T / 64)), the per-head dS exponents, and the
-// dS^T tiles of `group` heads. The group is as many heads as fit ds_cap() bytes
-// of causal tiles (at least one, a multiple of 8 when there are 8 or more, so
-// that heads keep their XCD); a non-causal call, which keeps every tile, takes
-// as many heads as fit the same space (at least one head's full tile set).
-// KAT_ATTN_DS_CAP_BYTES overrides the 4 GiB default (tests use it to run
-// several groups at small sizes).
+// fp16 copy of Q ([B*H][T][D]), per-tile Q exponents and dS-bound parts and
+// dS exponents ([B*H][nt] each, nt = ceil(T / 64)), per-32-key K exponents,
+// the dS^T tiles, and (banded calls only) one head's fp32 dQ partial sums.
+// The dS^T region holds ds_cap() bytes of the call's mode's tiles (causal: the
+// lower triangle of each head's 64 x 64 tiles, ~T^2 bytes per head; non-causal:
+// all, ~2 T^2 bytes): as many heads as fit (a multiple of 8 when there are 8 or
+// more, so that heads keep their XCD), and dK/dV + dQ run per group of heads.
+// When one head's tiles exceed the cap, the head's key tiles split into bands
+// of kQB-tile multiples (the widest whose first band fits the cap, at least
+// kQB tiles = 512 keys) and dK/dV + dQ run per band of each head, dQ
+// accumulating in fp32 in band order: the workspace stays within the cap plus
+// O(B*H*T*D) bytes at every T (beyond T ~ 2^23 / cap-GiB^-1 the minimum band
+// of 512 keys itself exceeds the cap). KAT_ATTN_DS_CAP_BYTES overrides the
+// 4 GiB default (tests use it to run several groups or bands at small sizes).
 static size_t ds_cap() {
   const char* e = getenv("KAT_ATTN_DS_CAP_BYTES");
   const long long v = e ? atoll(e) : 0;
@@ -1173,12 +1245,30 @@ static BwdWs bwd_ws(void* base, int64_t B, int64_t H, int64_t T, int64_t D, bool
   const int64_t BH = B * H;
   const int nt = (int)((T + 63) / 64);
   const size_t rows = (size_t)(BH * T), tiles = (size_t)BH * (size_t)nt;
-  const size_t tri = (size_t)ds_tiles_per_head(nt, true) * 8192u, sq = (size_t)ds_tiles_per_head(nt, false) * 8192u;
-  int64_t gc = std::max<int64_t>(1, std::min<int64_t>(BH, (int64_t)(ds_cap() / tri)));
-  if (gc >= 8) gc &= ~(int64_t)7;
-  const size_t ds_bytes = std::max(gc * tri, sq);
-  int64_t gn = std::max<int64_t>(1, std::min<int64_t>(BH, (int64_t)(ds_bytes / sq)));
-  if (gn >= 8) gn &= ~(int64_t)7;
+  const size_t cap = ds_cap();
+  const size_t head = (size_t)ds_tiles_per_band(nt, causal, 0, nt) * 8192u;
+  int64_t group = 1;
+  int band = nt;
+  size_t ds_bytes, acc_bytes = 0;
+  if (head <= cap) {
+    group = std::max<int64_t>(1, std::min<int64_t>(BH, (int64_t)(cap / head)));
+    if (group >= 8) group &= ~(int64_t)7;
+    ds_bytes = (size_t)group * head;
+  } else {
+    // the widest band (a multiple of kQB key tiles) whose tiles fit the cap;
+    // the first band of a head is its largest
+    int lo = 1, hi = (nt - 1) / kQB;  // in units of kQB tiles; hi * kQB < nt
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) / 2;
+      if ((size_t)ds_tiles_per_band(nt, causal, 0, mid * kQB) * 8192u <= cap)
+        lo = mid;
+      else
+        hi = mid - 1;
+    }
+    band = std::max(1, lo) * kQB;
+    ds_bytes = (size_t)ds_tiles_per_band(nt, causal, 0, band) * 8192u;
+    acc_bytes = (size_t)nt * 64 * (size_t)D * sizeof(float);
+  }
   char* p = reinterpret_cast<char*>(base);
   BwdWs w;
   size_t o = 0;
@@ -1190,15 +1280,17 @@ static BwdWs bwd_ws(void* base, int64_t B, int64_t H, int64_t T, int64_t D, bool
   w.vnrm = reinterpret_cast<float*>(take(tiles * sizeof(float)));
   w.abnd = reinterpret_cast<float*>(take(tiles * sizeof(float)));
   w.bbnd = reinterpret_cast<float*>(take(tiles * sizeof(float)));
-  w.khead = reinterpret_cast<int*>(take((size_t)BH * sizeof(int)));
+  w.ktile = reinterpret_cast<int*>(take(tiles * sizeof(int)));
   w.dst = reinterpret_cast<f16*>(take(ds_bytes));
-  w.group = (int)(causal ? gc : gn);
+  w.dqacc = acc_bytes ? reinterpret_cast<float*>(take(acc_bytes)) : nullptr;
+  w.group = (int)group;
+  w.band = band;
   w.bytes = o;
   return w;
 }
 
-size_t attn_mfma_workspace(int64_t B, int64_t H, int64_t T, int64_t D) {
-  return bwd_ws(nullptr, B, H, T, D, true).bytes;
+size_t attn_mfma_workspace(int64_t B, int64_t H, int64_t T, int64_t D, bool causal) {
+  return bwd_ws(nullptr, B, H, T, D, causal).bytes;
 }
 
 namespace {
@@ -1233,16 +1325,22 @@ int launch_bwd(const AttnArgs& a, void* ws, hipStream_t st) {
   const int cpb = (a.T + 255) / 256;
   hipLaunchKernelGGL(attn_bwd_stscale_k, dim3((unsigned)((int64_t)BH * cpb)), dim3(256), 0, st, w, a.T, cpb);
   if (int rc = check_launch("kat_attn_bwd (stats scale)")) return rc;
-  // per group of heads: dK, dV (and the dS^T tiles), then dQ from those tiles
-  const int64_t nb = (a.T + kBM - 1) / kBM, nbq = (a.T + kDqM - 1) / kDqM;
+  // per group of heads (and per band of key tiles): dK, dV (and the dS^T
+  // tiles), then dQ from those tiles
+  const int nt = (a.T + 63) / 64, nqb = (a.T + kDqM - 1) / kDqM;
   for (int bh0 = 0; bh0 < BH; bh0 += w.group) {
     const int G = std::min(w.group, BH - bh0);
-    hipLaunchKernelGGL((attn_bwd_dkv_k<T, D, MODE>), dim3((unsigned)(nb * G)), dim3(512), 0, st, a, w.stats, w.q16,
-                       w.qexp, w.khead, w.kexp, w.dst, bh0, G);
-    if (int rc = check_launch("kat_attn_bwd (dkv, mfma)")) return rc;
-    hipLaunchKernelGGL((attn_bwd_dq_k<T, D, MODE>), dim3((unsigned)(nbq * G)), dim3(64 * kDqW), 0, st, a, w.kexp,
-                       w.khead, w.dst, bh0, G);
-    if (int rc = check_launch("kat_attn_bwd (dq, mfma)")) return rc;
+    for (int kb0 = 0; kb0 < nt; kb0 += w.band) {
+      const int nk = std::min(w.band, nt - kb0);
+      const int64_t nb = (std::min<int64_t>((int64_t)(kb0 + nk) * 64, a.T) - (int64_t)kb0 * 64 + kBM - 1) / kBM;
+      const int64_t nbq = nqb - (kCausal ? kb0 / kQB : 0);
+      hipLaunchKernelGGL((attn_bwd_dkv_k<T, D, MODE>), dim3((unsigned)(nb * G)), dim3(512), 0, st, a, w.stats,
+                         w.q16, w.qexp, w.ktile, w.kexp, w.dst, bh0, G, kb0, nk);
+      if (int rc = check_launch("kat_attn_bwd (dkv, mfma)")) return rc;
+      hipLaunchKernelGGL((attn_bwd_dq_k<T, D, MODE>), dim3((unsigned)(nbq * G)), dim3(64 * kDqW), 0, st, a,
+                         w.kexp, w.ktile, w.dst, bh0, G, kb0, nk, w.dqacc);
+      if (int rc = check_launch("kat_attn_bwd (dq, mfma)")) return rc;
+    }
   }
   return 0;
 }

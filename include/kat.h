@@ -158,11 +158,17 @@ int kat_attn_fwd(const void* q, const void* k, const void* v, void* out, float* 
                  const int64_t* strides, const int64_t* l_strides, float scale, float eps,
                  int causal, int dtype, void* stream);
 
-/* Workspace bytes kat_attn_bwd needs. On the MFMA path it holds, besides
- * per-row and per-tile values and an fp16 copy of Q, the fp16 dS tiles
- * of a group of heads (the causal half of each head's T x T, 64 x 64 tiles;
- * at most 4 GiB of them, or one head's; KAT_ATTN_DS_CAP_BYTES in the
- * environment lowers the cap). */
+/* Workspace bytes kat_attn_bwd needs (causal, as every kat_attn_bwd call).
+ * On the MFMA path it holds, besides per-row and per-tile values and an fp16
+ * copy of Q (O(B*H*T*D) bytes), the fp16 dS tiles of the causal half of each
+ * head's T x T scores in 64 x 64 tiles, ~T^2 bytes per head: at most a cap of
+ * 4 GiB of them (KAT_ATTN_DS_CAP_BYTES in the environment sets another cap)
+ * for as many heads as fit. A head whose tiles exceed the cap runs in bands
+ * of its keys (multiples of 512 keys, each band's tiles within the cap, dQ
+ * summed in fp32 over the bands in a fixed order; results are bit-identical
+ * to one band), plus T*D*4 bytes for those sums, so the workspace stays
+ * within cap + O(B*H*T*D) bytes at every T up to the T at which one band of
+ * 512 keys alone exceeds the cap (T ~ 2^23 at 4 GiB). */
 size_t kat_attn_bwd_workspace_size(int64_t B, int64_t H, int64_t T, int64_t D, int dtype);
 
 /* Gradients of kat_attn_fwd:
@@ -175,8 +181,8 @@ size_t kat_attn_bwd_workspace_size(int64_t B, int64_t H, int64_t T, int64_t D, i
  * dS is computed once (by the dK/dV kernel, which stores it for dQ), and it
  * and the copies of Q and K its products take enter the MFMA in fp16, each
  * with a power-of-two scale chosen from the data (per 64-row tile for Q, per
- * 32 keys for K, from a bound on |dS| per head for dS) and undone exactly: the gradients
- * are exactly equivariant under power-of-two scalings
+ * 32 keys for K, per 64-query tile from a bound on |dS| for dS) and undone
+ * exactly: the gradients are exactly equivariant under power-of-two scalings
  * of q, k, v and dout, and per-tile maxima of |q| and |k| in [2^-46, 2^55]
  * are covered. The dS bounds assume (out, L) are the forward's outputs for
  * (q, k, v), as the reference's derivation does. */
@@ -198,12 +204,20 @@ int kat_attn_bwd(const void* q, const void* k, const void* v, const void* out,
  * A dropped key contributes nothing (the CPU path's -1e4 fill leaves
  * sigma(-1e4)^4 ~ 6e-18 per key); a query with no visible key gets L = 0,
  * o = 0, dq = 0, and dropped keys get dk = dv = 0. Other arguments, layouts
- * and workspace as kat_attn_fwd / kat_attn_bwd. */
+ * as kat_attn_fwd / kat_attn_bwd; the backward's workspace size comes from
+ * kat_attn_bwd_masked_workspace_size. */
 int kat_attn_fwd_masked(const void* q, const void* k, const void* v, void* out, float* L,
                         const float* slopes, const uint8_t* key_mask, int64_t mask_stride_b,
                         int64_t B, int64_t H, int64_t T, int64_t D, const int64_t* strides,
                         const int64_t* l_strides, float scale, float eps, int causal, int dtype,
                         void* stream);
+/* Workspace bytes kat_attn_bwd_masked needs for the given mode: as
+ * kat_attn_bwd_workspace_size for causal != 0; for causal == 0 the dS tiles
+ * cover all of each head's T x T scores (~2 T^2 bytes per head), under the
+ * same cap and banding. No counterpart in the reference (its kernels have no
+ * non-causal mode). */
+size_t kat_attn_bwd_masked_workspace_size(int64_t B, int64_t H, int64_t T, int64_t D, int dtype,
+                                          int causal);
 int kat_attn_bwd_masked(const void* q, const void* k, const void* v, const void* out,
                         const float* L, const void* dout, void* dq, void* dk, void* dv,
                         const float* slopes, const uint8_t* key_mask, int64_t mask_stride_b,

@@ -58,6 +58,36 @@ def test_workspace_sizes():
     assert lib.kat_men_bwd_workspace_size(8, 96, 3) % (96 * 8) == 0
 
 
+def test_backward_workspace_is_bounded_by_the_cap(monkeypatch):
+    # the dS tiles are sized by the call's mode (causal: the lower triangle of
+    # each head's tiles) and capped: a head whose tiles exceed the cap runs in
+    # bands of its keys, so the workspace stays within the cap plus O(T D)
+    # (stats, the fp16 copy of Q, per-tile values, fp32 dQ partial sums)
+    lib = _lib.load()
+    monkeypatch.delenv("KAT_ATTN_DS_CAP_BYTES", raising=False)
+    causal = lib.kat_attn_bwd_workspace_size(4, 16, 4096, 128, 1)
+    assert causal == lib.kat_attn_bwd_masked_workspace_size(4, 16, 4096, 128, 1, 1)
+    # 64 heads x 2304 tiles of 8 KB (the causal runs of 8 dQ blocks)
+    rows, tri = 4 * 16 * 4096, 64 * 2304 * 8192
+    assert causal < rows * (8 + 256) + tri + (1 << 20)
+    assert lib.kat_attn_bwd_masked_workspace_size(4, 16, 4096, 128, 1, 0) > causal + tri // 2
+    T, D = 65536, 128
+    linear = T * (8 + 2 * D) + T * D * 4 + (1 << 20)
+    # 4.3 GB of causal tiles per head: banded under the default 4 GiB cap
+    assert lib.kat_attn_bwd_workspace_size(1, 1, T, D, 1) <= (4 << 30) + linear
+    for cap in (1 << 30, 256 << 20):
+        monkeypatch.setenv("KAT_ATTN_DS_CAP_BYTES", str(cap))
+        for c in (1, 0):
+            n = lib.kat_attn_bwd_masked_workspace_size(1, 1, T, D, 1, c)
+            assert cap // 4 < n <= cap + linear, (cap, c, n)
+    # a cap below one band of 512 keys still sizes that band: at T = 4096 its
+    # causal runs hold 8 + 7 x 8 key tiles x 8 query tiles (4 MiB), plus the
+    # fp32 dQ partial sums
+    monkeypatch.setenv("KAT_ATTN_DS_CAP_BYTES", "1")
+    n = lib.kat_attn_bwd_workspace_size(1, 1, 4096, 128, 1)
+    assert 512 * 8192 < n < 4096 * (8 + 256 + 512) + 512 * 8192 + (1 << 20)
+
+
 def _msg(lib):
     return lib.kat_last_error().decode()
 

@@ -18,6 +18,7 @@ import pytest
 import torch
 
 import fastalgebraictransformer_amd as F
+from fastalgebraictransformer_amd import _lib
 import oracle as O
 from _util import check_lowp, golden, lowp_ulp, max_abs
 
@@ -218,7 +219,7 @@ def test_backward_is_deterministic(gpu, monkeypatch):
 def test_mfma_backward_is_invariant_to_the_upstream_gradient_scale(gpu, D, masked, monkeypatch):
     # dQ, dK, dV are linear in dO. A training step's dO is ~1e-5 .. 1e-7 per
     # element, where an unscaled fp16 dS would lose its significant bits; the
-    # kernels scale dS per head by a power of two, so dO * 2^-e must give
+    # kernels scale dS per query tile by a power of two, so dO * 2^-e must give
     # exactly 2^-e times the gradients of dO (bit for bit: every scaling is a
     # power of two and the outputs stay within bf16's exponent range)
     monkeypatch.setenv("KAT_ATTN_IMPL", "mfma")
@@ -256,7 +257,7 @@ def test_mfma_backward_is_invariant_to_the_upstream_gradient_scale(gpu, D, maske
 # ------------------------------------------------- input magnitude range ----
 # The MFMA backward rounds dS, and copies of Q and K, to fp16 (range 2^-14 ..
 # 65504). Each copy carries a power-of-two scale chosen from the data (per
-# 64-row tile for Q, per 32 keys for K, per head for dS), so inputs far outside
+# 64-row tile for Q, per 32 keys for K, per 64-query tile for dS), so inputs far outside
 # N(0, 1) must still meet the bar. Outputs scale with the inputs: each check
 # divides got and ref by the known factor of that output and applies the
 # unit-scale bar, 2e-2 + 1/2 ulp.
@@ -329,9 +330,9 @@ def test_mfma_backward_key_groups_of_different_magnitude(gpu, D, dtype, monkeypa
             # each group's rows against that group's own scale (dv = P^T dO
             # takes P from the S recomputed on the groups' fp16 keys; dk is
             # checked over the whole tensor only: the dS of the 2^s groups
-            # lies so far below the head's largest that fp16 holds it in its
-            # subnormal range, the documented limit of the one dS exponent
-            # per head)
+            # lies so far below its query tile's largest that fp16 holds it in
+            # its subnormal range -- dS has one exponent per query tile, none
+            # per key, the documented limit)
             for j0 in range(0, T, 32):
                 gg, gr = got[:, :, j0:j0 + 32], ref[:, :, j0:j0 + 32]
                 assert _rel_max(gg, gr) <= 2e-2, (name, j0, _rel_max(gg, gr))
@@ -428,6 +429,134 @@ def test_mfma_backward_head_groups_are_bit_identical(gpu, mode, dtype, D, monkey
     for name, a, b in zip(("dq", "dk", "dv"), *runs):
         assert bool(torch.isfinite(a).all()), name
         assert torch.equal(a, b), name
+
+
+@pytest.mark.parametrize("mode", ["plain", "masked", "noncausal"])
+@pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 128), (torch.float16, 64)])
+def test_mfma_backward_key_bands_are_bit_identical(gpu, mode, dtype, D, monkeypatch):
+    # when one head's dS^T tiles exceed the cap, the backward runs dK/dV + dQ
+    # per band of key tiles (multiples of 8 tiles = 512 keys), dQ keeping fp32
+    # partial sums between the bands. The MFMA accumulation order is the one
+    # of the single-band run and the partial sums are stored and reloaded
+    # exactly, so the gradients must be equal bit for bit.
+    from fastalgebraictransformer_amd.backward import _attn_bwd_into
+    from fastalgebraictransformer_amd.forward import _attn_fwd_into, _key_mask_arg
+    _pin_mfma(monkeypatch, D)
+    B, H, T = 2, 3, 1300  # 21 key tiles: bands of 8, 8 and 5 tiles
+    q, k, v, do = _inputs(131 + D, B, H, T, D, dtype)
+    slopes = F.compute_alibi_slopes(H).to(dev)
+    scale = 1.0 / math.sqrt(D)
+    km, causal, ext = None, True, False
+    if mode != "plain":
+        ext, causal = True, mode == "masked"
+        m = torch.ones(B, T, dtype=torch.int32)
+        m[0, :300] = 0
+        m[1, 7::5] = 0
+        m[1, 600:1100] = 0  # whole key tiles (and a whole band's worth) dropped
+        km = _key_mask_arg(m, B, T, dev)
+    o = torch.empty_like(q)
+    L = torch.empty(B, H, T, dtype=torch.float32, device=dev)
+    _attn_fwd_into(q, k, v, o, L, slopes, scale, causal, 1e-6, km, extended=ext)
+    lib = _lib.load()
+    code = _lib.dtype_code(q)
+    runs = []
+    # 192 tiles of 8 KB: an 8-tile band of this T in every mode, not 16 tiles
+    for cap in (None, 192 * 8192):
+        if cap is None:
+            monkeypatch.delenv("KAT_ATTN_DS_CAP_BYTES", raising=False)
+        else:
+            monkeypatch.setenv("KAT_ATTN_DS_CAP_BYTES", str(cap))
+        ws = lib.kat_attn_bwd_masked_workspace_size(B, H, T, D, code, int(causal))
+        g = [torch.full_like(q, float("nan")) for _ in range(3)]
+        _attn_bwd_into(q, k, v, o, L, do, *g, slopes, scale, causal, 1e-6, km, extended=ext)
+        torch.cuda.synchronize()
+        runs.append((g, ws))
+    (g0, ws0), (g1, ws1) = runs
+    assert ws1 < ws0
+    for name, a, b in zip(("dq", "dk", "dv"), g0, g1):
+        assert bool(torch.isfinite(a).all()), name
+        assert torch.equal(a, b), name
+    # and the banded result against the oracle at the bf16 / fp16 bar, on two
+    # heads (batch 1's mask drops a band's worth of keys)
+    for bs, hs in ((slice(0, 1), slice(0, 1)), (slice(1, 2), slice(2, 3))):
+        kmb = None if km is None else km[bs].cpu()
+        args = [t[bs, hs] for t in (q, k, v)]
+        rq, rk, rv = O.attention_bwd(*args, o[bs, hs], L[bs, hs], do[bs, hs], slopes[hs].cpu(), scale,
+                                     dtype=torch.float32, key_mask=kmb, causal=causal)
+        for name, got, ref in (("dq", g1[0], rq), ("dk", g1[1], rk), ("dv", g1[2], rv)):
+            assert_lowp(got[bs, hs], ref, dtype, name)
+
+
+def test_mfma_backward_at_65536_in_bands_matches_fp32_tiled(gpu, monkeypatch):
+    # T = 65536: one causal head's dS tiles (~4.3 GB) exceed the default 4 GiB
+    # cap, so the default call already runs in two bands; a 512 MiB cap runs
+    # ~12 bands and must give the same bits, with a workspace within the cap
+    # plus O(T D). Against the fp32 tiled kernels (an independent
+    # implementation, O(T) memory) on the same bf16-rounded inputs at the bf16
+    # bar.
+    B, H, T, D = 1, 1, 65536, 128
+    q, k, v, do = _inputs(167, B, H, T, D, torch.bfloat16)
+    slopes = F.compute_alibi_slopes(8)[5:6].to(dev)  # a mid-range slope, 2^-3
+    scale = 1.0 / math.sqrt(D)
+    _pin_mfma(monkeypatch, D)
+    lib = _lib.load()
+    ws_default = lib.kat_attn_bwd_workspace_size(B, H, T, D, 1)
+    assert ws_default <= (4 << 30) + T * D * 16
+    o_m, L_m = F.rational_attention_forward(q, k, v, slopes, scale)
+    g_m = F.rational_attention_backward(q, k, v, o_m, L_m, do, slopes, scale)
+    cap = 512 << 20
+    monkeypatch.setenv("KAT_ATTN_DS_CAP_BYTES", str(cap))
+    assert lib.kat_attn_bwd_workspace_size(B, H, T, D, 1) <= cap + T * D * 16
+    g_c = F.rational_attention_backward(q, k, v, o_m, L_m, do, slopes, scale)
+    monkeypatch.delenv("KAT_ATTN_DS_CAP_BYTES")
+    for a, b, n in zip(g_m, g_c, ("dq", "dk", "dv")):
+        assert torch.equal(a, b), n
+    monkeypatch.setenv("KAT_ATTN_IMPL", "tiled")
+    f32 = [t.float() for t in (q, k, v, do)]
+    o_t, L_t = F.rational_attention_forward(f32[0], f32[1], f32[2], slopes, scale)
+    g_t = F.rational_attention_backward(f32[0], f32[1], f32[2], o_m.float(), L_m, f32[3], slopes, scale)
+    torch.cuda.synchronize()
+    assert _rel_max(L_m, L_t) <= 1e-3
+    errs = {"o": assert_lowp(o_m, o_t, torch.bfloat16, "o")}
+    for n, x, y in zip(("dq", "dk", "dv"), g_m, g_t):
+        errs[n] = assert_lowp(x, y, torch.bfloat16, n)
+    print("T = 65536 in bands vs fp32 tiled: " + ", ".join(f"{n} {e:.3e} / {r:.3e}" for n, (e, r) in errs.items()))
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_mfma_backward_query_tiles_of_different_magnitude(gpu, D, dtype, monkeypatch):
+    # dS enters the fp16 products with one exponent per 64-query tile, chosen
+    # from that tile's bound. Upstream gradients whose magnitude differs by
+    # 2^30 (bf16; 2^12 in fp16, whose own range is narrower) from one 64-query
+    # tile to the next give the small tiles' dS its own exponent: their dq
+    # must hold to the bar relative to their own size. (With one exponent per
+    # head their dS lay 2^30 below the head's largest, in fp16's subnormal
+    # range.) dk and dv are sums over all queries, dominated by the large
+    # tiles; they are checked over the whole tensor.
+    _pin_mfma(monkeypatch, D)
+    B, H, T = 1, 2, 512
+    q, k, v, do = (t.float() for t in _inputs(59 + D, B, H, T, D, torch.float32))
+    sh = 12 if dtype == torch.float16 else 30
+    tsc = torch.tensor([2.0 ** (-sh * ((i // 64) % 2)) for i in range(T)])
+    do = do * tsc.view(1, 1, T, 1).to(do.device)
+    q, k, v, do = (t.to(dtype) for t in (q, k, v, do))
+    slopes = F.compute_alibi_slopes(H)
+    scale = 1.0 / math.sqrt(D)
+    o, L, dq, dk, dv = _run(q, k, v, do, slopes.to(dev), scale)
+    rq, rk, rv = O.attention_bwd(q, k, v, o, L, do, slopes, scale, dtype=torch.float32)
+    for name, got, ref in (("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
+        got = got.detach().to("cpu", torch.float64)
+        ref = ref.detach().to("cpu", torch.float64)
+        assert bool(torch.isfinite(got).all()), name
+        rel = float((got - ref).norm() / ref.norm())
+        assert _rel_max(got, ref) <= 2e-2 and rel <= 1e-2, (name, _rel_max(got, ref), rel)
+        if name == "dq":
+            for i0 in range(0, T, 64):
+                gg, gr = got[:, :, i0:i0 + 64], ref[:, :, i0:i0 + 64]
+                rel_t = float((gg - gr).norm() / gr.norm())
+                print(f"dq tile {i0 // 64}: max err / max |ref| {_rel_max(gg, gr):.3e}, relL2 {rel_t:.3e}")
+                assert _rel_max(gg, gr) <= 2e-2 and rel_t <= 1e-2, (name, i0, _rel_max(gg, gr), rel_t)
 
 
 def test_mfma_long_sequence_matches_fp32_tiled(gpu, monkeypatch):
