@@ -31,7 +31,8 @@ def _attn_bwd_into(q, k, v, output, L, grad_output, dq, dk, dv, alibi_slopes, sc
     allocator. ``extended``: kat_attn_bwd_masked (see _attn_fwd_into)."""
     lib = _lib.load()
     B, H, T, D = q.shape
-    _warn_if_tiled((q, k, v, output, grad_output, dq, dk, dv), D, q.dtype)
+    _warn_if_tiled((q, k, v, output, grad_output, dq, dk, dv), D, q.dtype,
+                   mfma_inputs=(q, k, v, output, grad_output))
     slopes = alibi_slopes.to(device=q.device, dtype=torch.float32).contiguous()
     code = _lib.dtype_code(q)
     if extended:

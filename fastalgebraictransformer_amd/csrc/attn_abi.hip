@@ -2,7 +2,8 @@
 //
 // Kernel choice: bf16 / fp16 tensors with a head dim the MFMA kernels cover
 // (and 16-byte aligned rows) go to the MFMA kernels; everything else (fp32,
-// other head dims up to 256, unaligned views) to the fp32 tiled kernels.
+// fp64, other head dims up to 1024, unaligned views) to the tiled kernels
+// (fp32 arithmetic; fp64 for fp64 tensors).
 // KAT_ATTN_IMPL in the environment overrides the choice: "tiled" forces the
 // tiled kernels, "mfma" makes a bf16 / fp16 call that cannot take the MFMA
 // kernels fail with KAT_EUNSUPPORTED instead of falling back (both used by the
@@ -35,7 +36,7 @@ int fill_args(const char* nm, AttnArgs& a, int64_t B, int64_t H, int64_t T, int6
   if (B < 0 || H < 0 || T < 0 || D < 0) return fail(KAT_EINVAL, "%s: negative size", nm);
   if (B * H > 0x7fffffffLL || T > 0x7fffffffLL)
     return fail(KAT_EUNSUPPORTED, "%s: B*H or T too large", nm);
-  if (D > 256) return fail(KAT_EUNSUPPORTED, "%s: head dim %lld > 256", nm, (long long)D);
+  if (D > 1024) return fail(KAT_EUNSUPPORTED, "%s: head dim %lld > 1024", nm, (long long)D);
   if (!strides || !l_strides) return fail(KAT_EINVAL, "%s: null stride array", nm);
   a.B = (int)B;
   a.H = (int)H;
@@ -58,16 +59,17 @@ template <typename T> bool rows16(const void* p, const int64_t* s) {
          (s[1] * (int64_t)sizeof(T)) % 16 == 0 && (s[2] * (int64_t)sizeof(T)) % 16 == 0;
 }
 
-// workspace of the tiled path: Delta [B*H*T] fp32, then cinv [B*H*T] fp32 (each
-// 256-byte aligned); the MFMA path lays out its own (attn_mfma_workspace), sized
-// for the call's mode (causal or not). One buffer of the larger size serves
-// whichever path a call takes.
-size_t stat_bytes(int64_t B, int64_t H, int64_t T) {
-  return (((size_t)(B * H * T) * sizeof(float)) + 255) & ~(size_t)255;
+// workspace of the tiled path: Delta [B*H*T], then cinv [B*H*T] (each 256-byte
+// aligned; fp32, fp64 for fp64 tensors); the MFMA path lays out its own
+// (attn_mfma_workspace), sized for the call's mode (causal or not). One buffer
+// of the larger size serves whichever path a call takes.
+size_t stat_bytes(int64_t B, int64_t H, int64_t T, int dtype) {
+  const size_t e = dtype == KAT_F64 ? sizeof(double) : sizeof(float);
+  return (((size_t)(B * H * T) * e) + 255) & ~(size_t)255;
 }
-size_t delta_bytes(int64_t B, int64_t H, int64_t T) { return 2 * stat_bytes(B, H, T); }
+size_t delta_bytes(int64_t B, int64_t H, int64_t T, int dtype) { return 2 * stat_bytes(B, H, T, dtype); }
 size_t bwd_workspace(int64_t B, int64_t H, int64_t T, int64_t D, int dtype, bool causal) {
-  size_t n = delta_bytes(B, H, T);
+  size_t n = delta_bytes(B, H, T, dtype);
   if ((dtype == KAT_BF16 || dtype == KAT_F16) && attn_mfma_supported((int)D))
     n = std::max(n, attn_mfma_workspace(B, H, T, D, causal));
   return n;
@@ -85,6 +87,18 @@ template <typename T> static int attn_fwd_t(const AttnArgs& a, hipStream_t st) {
   return attn_fwd_generic<T>(a, st);
 }
 
+// Delta and cinv (accumulation type) at the start of the workspace, then the
+// tiled backward kernels
+template <typename T>
+static int attn_bwd_tiled(const AttnArgs& a, void* ws, hipStream_t st) {
+  typedef typename AccT<T>::type A;
+  const int dt = sizeof(A) == 8 ? KAT_F64 : KAT_F32;
+  A* delta = reinterpret_cast<A*>(ws);
+  A* cinv = reinterpret_cast<A*>(reinterpret_cast<char*>(ws) + stat_bytes(a.B, a.H, a.T, dt));
+  if (int rc = attn_delta<T>(a, delta, cinv, st)) return rc;
+  return attn_bwd_generic<T>(a, delta, st);
+}
+
 template <typename T>
 static int attn_bwd_t(const AttnArgs& a, void* ws, hipStream_t st) {
   if (!force_tiled() && attn_mfma_supported(a.D) && rows16<T>(a.q, a.sq) &&
@@ -95,10 +109,7 @@ static int attn_bwd_t(const AttnArgs& a, void* ws, hipStream_t st) {
     if (rc != KAT_EUNSUPPORTED) return rc;
   }
   if (require_mfma()) return fail(KAT_EUNSUPPORTED, "kat_attn_bwd: shape / layout not covered by the MFMA kernels");
-  float* delta = reinterpret_cast<float*>(ws);
-  float* cinv = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + stat_bytes(a.B, a.H, a.T));
-  if (int rc = attn_delta<T>(a, delta, cinv, st)) return rc;
-  return attn_bwd_generic<T>(a, delta, st);
+  return attn_bwd_tiled<T>(a, ws, st);
 }
 
 static int attn_fwd_impl(const char* nm, const void* q, const void* k, const void* v, void* out,
@@ -127,6 +138,7 @@ static int attn_fwd_impl(const char* nm, const void* q, const void* k, const voi
   const hipStream_t st = as_stream(stream);
   switch (dtype) {
     case KAT_F32: return attn_fwd_generic<float>(a, st);
+    case KAT_F64: return attn_fwd_generic<double>(a, st);
     case KAT_BF16: return attn_fwd_t<bf16>(a, st);
     case KAT_F16: return attn_fwd_t<f16>(a, st);
     default: return fail(KAT_EUNSUPPORTED, "%s: unsupported dtype %d", nm, dtype);
@@ -196,13 +208,10 @@ static int attn_bwd_impl(const char* nm, const void* q, const void* k, const voi
   a.km = key_mask;
   a.skm = mask_stride_b;
   a.causal = causal ? 1 : 0;
-  float* delta = reinterpret_cast<float*>(workspace);
-  float* cinv = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + stat_bytes(B, H, T));
   const hipStream_t st = as_stream(stream);
   switch (dtype) {
-    case KAT_F32:
-      if (int rc = attn_delta<float>(a, delta, cinv, st)) return rc;
-      return attn_bwd_generic<float>(a, delta, st);
+    case KAT_F32: return attn_bwd_tiled<float>(a, workspace, st);
+    case KAT_F64: return attn_bwd_tiled<double>(a, workspace, st);
     case KAT_BF16: return attn_bwd_t<bf16>(a, workspace, st);
     case KAT_F16: return attn_bwd_t<f16>(a, workspace, st);
     default: return fail(KAT_EUNSUPPORTED, "%s: unsupported dtype %d", nm, dtype);

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "kat_common.h"
+
 namespace kat {
 
 // Layout [B, H, T, D]: element (b, h, t, d) of tensor X sits at
@@ -34,10 +36,14 @@ __device__ __forceinline__ bool key_ok(const AttnArgs& a, int b, int j) {
   return a.km == nullptr || a.km[(int64_t)b * a.skm + j] != 0;
 }
 
+// Tiled kernels (any D <= 1024; fp32 arithmetic, fp64 for double tensors).
 template <typename T> int attn_fwd_generic(const AttnArgs& a, hipStream_t st);
-// Delta_i = <dO_i, O_i> and cinv_i = 1 / (16 (L_i + eps)), both [B*H*T] fp32.
-template <typename T> int attn_delta(const AttnArgs& a, float* delta, float* cinv, hipStream_t st);
-template <typename T> int attn_bwd_generic(const AttnArgs& a, const float* delta, hipStream_t st);
+// Delta_i = <dO_i, O_i> and cinv_i = 1 / (16 (L_i + eps)), both [B*H*T] in the
+// accumulation type (fp32, fp64 for double tensors).
+template <typename T>
+int attn_delta(const AttnArgs& a, typename AccT<T>::type* delta, typename AccT<T>::type* cinv, hipStream_t st);
+template <typename T>
+int attn_bwd_generic(const AttnArgs& a, const typename AccT<T>::type* delta, hipStream_t st);
 
 // bf16 / fp16 MFMA kernels; return KAT_EUNSUPPORTED when the shape is not covered.
 // The backward runs its own prep pass; ws holds attn_mfma_workspace() bytes for

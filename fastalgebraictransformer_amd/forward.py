@@ -4,7 +4,8 @@ Same Python API as the reference ``kernels.forward``
 (SkyeGunasekaran/fastAlgebraicTransformer forward.py:21-42
 ``compute_alibi_slopes`` and forward.py:267-319 ``rational_attention_forward``).
 The launch goes to ``kat_attn_fwd`` in libkat.so: a bf16/fp16 MFMA kernel for
-head dims it covers, an fp32 tiled kernel otherwise.
+head dims it covers, a tiled kernel otherwise (fp32 arithmetic; fp64 for fp64
+tensors; any head dim up to 1024).
 """
 
 import math
@@ -44,24 +45,54 @@ def _unit_d(t):
 
 _WARNED = set()
 
+# per-(b, h) slice byte offsets the MFMA kernels address with 31-bit buffer
+# offsets: a row stride s (elements) must satisfy (T + 128) * s * 2 < 2^31
+# (csrc/attn_mfma.hip offsets_ok)
+_MFMA_OFFSET_LIMIT = 0x7FFFFFFF
+_MFMA_ROW_PAD = 128
 
-def _warn_if_tiled(tensors, D, dtype):
+
+def _tiled_reason(shapes_strides_ptrs, D, T, elem):
+    """Why a bf16 / fp16 attention call would leave the MFMA kernels for the
+    tiled ones (None if it takes them), from each operand's (b, h, t) strides
+    and data pointer: the head dim, 16-byte row alignment, and the 31-bit byte
+    offsets the MFMA kernels use within one (b, h) slice."""
+    if D not in (32, 64, 128):
+        return f"head dim {D} (the MFMA kernels cover 32, 64 and 128)"
+    for strides, ptr in shapes_strides_ptrs:
+        if ptr % 16 or any((st * elem) % 16 for st in strides):
+            return "rows not 16-byte aligned (a view with an odd offset or stride)"
+    for strides, _ in shapes_strides_ptrs:
+        st = strides[2]
+        if st < D or (T + _MFMA_ROW_PAD) * st * elem > _MFMA_OFFSET_LIMIT:
+            return (f"row stride {st} at T = {T}: a (b, h) slice spans 2^31 bytes or more "
+                    "(the MFMA kernels address a slice with 31-bit offsets)")
+    if T * D * 2 >= _MFMA_OFFSET_LIMIT or T * 8 >= _MFMA_OFFSET_LIMIT:
+        return f"T = {T}: per-head workspace rows exceed 31-bit offsets"
+    return None
+
+
+def _warn_if_tiled(tensors, D, dtype, mfma_inputs=None):
     """bf16 / fp16 attention runs on the MFMA kernels when the head dim is 32,
-    64 or 128 and every [B, H, T, D] operand has 16-byte aligned rows; otherwise
-    libkat falls back to the fp32 tiled kernels, which are correct but about
-    an order of magnitude slower. Warn once per reason, so a model with
-    another head dim (or a misaligned view) does not lose that silently."""
+    64 or 128, every [B, H, T, D] operand has 16-byte aligned rows and the
+    inputs the kernels address by 31-bit offsets (q, k, v; and O, dO in the
+    backward: ``mfma_inputs``) keep each (b, h) slice below 2^31 bytes;
+    otherwise libkat falls back to the tiled kernels, which are correct but
+    about an order of magnitude slower. Warn once per dtype and reason, so a model with
+    another head dim, a misaligned view or a very long packed sequence does
+    not lose that silently."""
     if dtype not in (torch.bfloat16, torch.float16) or os.environ.get("KAT_ATTN_IMPL") == "tiled":
         return
-    if D not in (32, 64, 128):
-        reason = f"head dim {D} (the MFMA kernels cover 32, 64 and 128)"
-    elif any(t.data_ptr() % 16 or any((st * t.element_size()) % 16 for st in t.stride()[:3])
-             for t in tensors):
-        reason = "rows not 16-byte aligned (a view with an odd offset or stride)"
-    else:
+    T = tensors[0].shape[2]
+    elem = tensors[0].element_size()
+    align = [(t.stride()[:3], t.data_ptr()) for t in tensors]
+    reason = _tiled_reason(align, D, T, elem)
+    if reason is None and mfma_inputs is not None:
+        reason = _tiled_reason([(t.stride()[:3], 0) for t in mfma_inputs], D, T, elem)
+    if reason is None:
         return
-    if reason not in _WARNED:
-        _WARNED.add(reason)
+    if (dtype, reason) not in _WARNED:
+        _WARNED.add((dtype, reason))
         warnings.warn(f"rational attention in {dtype}: {reason}; running the fp32 tiled "
                       "kernels, about 10x slower than the MFMA path", RuntimeWarning, stacklevel=3)
 
@@ -82,7 +113,7 @@ def _attn_fwd_into(q, k, v, out, L, alibi_slopes, scale, causal, eps, key_mask=N
     honours ``causal``; otherwise kat_attn_fwd, always causal as the reference."""
     lib = _lib.load()
     B, H, T, D = q.shape
-    _warn_if_tiled((q, k, v, out), D, q.dtype)
+    _warn_if_tiled((q, k, v, out), D, q.dtype, mfma_inputs=(q, k, v))
     slopes = alibi_slopes.to(device=q.device, dtype=torch.float32).contiguous()
     assert slopes.numel() == H, "alibi_slopes must have n_heads entries"
     strides = _lib.i64_array(_bht_strides(q) + _bht_strides(k) + _bht_strides(v) +

@@ -150,8 +150,11 @@ int kat_add_men_bwd(const void* dy, const void* dh, const void* h, const void* w
  * l_strides: 3 int64 = (b, h, t) strides of L. slopes: fp32 [H].
  * Replaces the host wrapper + rational_attention_fwd_kernel[(B,H,T)] launch at
  * forward.py:267-319 (kernel forward.py:49-159). dtype KAT_BF16/KAT_F16 use
- * the MFMA kernels (D in {32, 64, 128}, 16-byte aligned rows); KAT_F32 and other
- * D (<= 256) use the fp32 tiled kernels.
+ * the MFMA kernels (D in {32, 64, 128}, 16-byte aligned rows); KAT_F32,
+ * KAT_F64 and other D (<= 1024; larger D returns KAT_EUNSUPPORTED) use the
+ * tiled kernels, in fp32 arithmetic (fp64 for KAT_F64; the reference computes
+ * in fp32 for every dtype, forward.py:103, and stores in the input dtype,
+ * :155). L is fp32 for every dtype.
  * ---------------------------------------------------------------------- */
 int kat_attn_fwd(const void* q, const void* k, const void* v, void* out, float* L,
                  const float* slopes, int64_t B, int64_t H, int64_t T, int64_t D,
@@ -168,7 +171,8 @@ int kat_attn_fwd(const void* q, const void* k, const void* v, void* out, float* 
  * summed in fp32 over the bands in a fixed order; results are bit-identical
  * to one band), plus T*D*4 bytes for those sums, so the workspace stays
  * within cap + O(B*H*T*D) bytes at every T up to the T at which one band of
- * 512 keys alone exceeds the cap (T ~ 2^23 at 4 GiB). */
+ * 512 keys alone exceeds the cap (T ~ 2^23 at 4 GiB). The tiled path (fp32,
+ * fp64, other head dims) needs 2 B*H*T values of the accumulation type. */
 size_t kat_attn_bwd_workspace_size(int64_t B, int64_t H, int64_t T, int64_t D, int dtype);
 
 /* Gradients of kat_attn_fwd:

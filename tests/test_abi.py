@@ -104,9 +104,9 @@ def test_argument_errors_are_reported_without_launching():
     assert lib.kat_rswiglu_fwd(None, None, None, 0, 8, 8, 8, 8, 1, None) == 0
     strides = _lib.i64_array([0] * 12)
     lstr = _lib.i64_array([0] * 3)
-    rc = lib.kat_attn_fwd(None, None, None, None, None, None, 1, 1, 8, 512, strides, lstr, 1.0,
+    rc = lib.kat_attn_fwd(None, None, None, None, None, None, 1, 1, 8, 1040, strides, lstr, 1.0,
                           1e-6, 1, 1, None)
-    assert rc == 2 and "head dim" in _msg(lib)
+    assert rc == 2 and "head dim 1040 > 1024" in _msg(lib)
     rc = lib.kat_attn_fwd(None, None, None, None, None, None, 1, 1, 8, 64, strides, lstr, 1.0,
                           1e-6, 1, 1, None)
     assert rc == 1 and "null" in _msg(lib)

@@ -1,0 +1,166 @@
+"""GPU parity of the tiled attention kernels beyond the MFMA path: fp64
+tensors and head dims above 256 (up to 1024).
+
+The reference takes any float dtype -- its kernels load with
+``.to(tl.float32)`` and store in the input dtype (forward.py:103,155) -- and
+any head dim (BLOCK_D = next_pow2(D), forward.py:297-301). Here fp64 tensors
+keep fp64 arithmetic (as the row ops do), so fp64 gradient checks hold; L is
+fp32 as in the reference (forward.py:294).
+
+Tolerances (written beside each check):
+  * fp64: <= 1e-10 of max|ref| against the fp64 oracle on the same inputs,
+    with the kernel's own (fp32) L passed to the oracle's backward. The C ABI
+    takes scale and eps as fp32 (the reference hands them to its kernels as
+    fp32 scalars too), so the oracle takes the same fp32-rounded scale;
+  * fp32: <= 1e-5 of max|ref|, the fp32 bar of test_gpu_attention.py;
+  * bf16: the low-precision bar (check_lowp: 2e-2 + 1/2 ulp elementwise,
+    relative L2 <= 5e-3).
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import fastalgebraictransformer_amd as F
+import oracle as O
+from _util import check_lowp, max_abs
+
+pytestmark = pytest.mark.gpu
+dev = "cuda"
+
+
+def _inputs(seed, B, H, T, D, dtype):
+    g = torch.Generator().manual_seed(seed)
+    return [torch.randn(B, H, T, D, generator=g, dtype=torch.float64).to(dtype).to(dev)
+            for _ in range(4)]
+
+
+def _scale32(D):
+    # 1 / sqrt(D) as the fp32 scalar the kernels receive
+    return float(np.float32(1.0 / math.sqrt(D)))
+
+
+def _rel(got, ref):
+    return max_abs(got, ref) / max(1e-300, float(ref.detach().abs().max()))
+
+
+def _run(q, k, v, do, slopes, scale, key_mask=None, causal=True):
+    q, k, v = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+    if key_mask is None and causal:
+        out = F.rational_attention(q, k, v, slopes, scale)
+        o, L = F.rational_attention_forward(q.detach(), k.detach(), v.detach(), slopes, scale)
+        assert torch.equal(out.detach(), o)
+    else:
+        out = F.rational_attention_masked(q, k, v, slopes, scale, key_mask=key_mask,
+                                          causal=causal)
+        o, L = None, None
+    out.backward(do)
+    torch.cuda.synchronize()
+    return out.detach(), L, q.grad, k.grad, v.grad
+
+
+@pytest.mark.parametrize("B,H,T,D", [(2, 3, 97, 64), (1, 2, 130, 128), (1, 2, 70, 256)])
+def test_fp64_matches_oracle(gpu, B, H, T, D):
+    q, k, v, do = _inputs(7 + D, B, H, T, D, torch.float64)
+    slopes = F.compute_alibi_slopes(H)
+    scale = _scale32(D)
+    o, L, dq, dk, dv = _run(q, k, v, do, slopes.to(dev), scale)
+    assert o.dtype == torch.float64 and dq.dtype == torch.float64 and L.dtype == torch.float32
+    ro, rL = O.attention_fwd(q, k, v, slopes, scale, dtype=torch.float64)
+    assert _rel(o, ro) <= 1e-10, _rel(o, ro)
+    assert _rel(L, rL) <= 1e-7  # L is stored in fp32
+    # the backward takes L as stored (fp32), as the reference's does
+    rq, rk, rv = O.attention_bwd(q, k, v, o, L, do, slopes, scale, dtype=torch.float64)
+    for name, got, ref in (("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
+        assert got.dtype == torch.float64
+        assert _rel(got, ref) <= 1e-10, (name, _rel(got, ref))
+
+
+def test_fp64_masked_noncausal_matches_oracle(gpu):
+    B, H, T, D = 2, 2, 90, 48
+    q, k, v, do = _inputs(31, B, H, T, D, torch.float64)
+    slopes = F.compute_alibi_slopes(H)
+    scale = _scale32(D)
+    km = torch.ones(B, T, dtype=torch.int32)
+    km[0, :17] = 0
+    km[1, 3::4] = 0
+    for causal in (True, False):
+        o, _, dq, dk, dv = _run(q, k, v, do, slopes.to(dev), scale, key_mask=km, causal=causal)
+        ro, rL = O.attention_fwd(q, k, v, slopes, scale, dtype=torch.float64, causal=causal,
+                                 key_mask=km)
+        assert _rel(o, ro) <= 1e-10, (causal, _rel(o, ro))
+        # the oracle's backward on its own fp64 L: the kernel's L (fp32) moves
+        # p by ~6e-8 relative, so this comparison takes 1e-6
+        rq, rk, rv = O.attention_bwd(q, k, v, ro, rL, do, slopes, scale, dtype=torch.float64,
+                                     causal=causal, key_mask=km)
+        for name, got, ref in (("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
+            assert _rel(got, ref) <= 1e-6, (causal, name, _rel(got, ref))
+
+
+def test_fp64_gradcheck(gpu):
+    # finite differences of the fp64 forward against the analytic backward
+    # (gradcheck's default tolerances; the fp32 L perturbs p by ~6e-8)
+    B, H, T, D = 1, 2, 12, 8
+    q, k, v, _ = _inputs(3, B, H, T, D, torch.float64)
+    q, k, v = (t.requires_grad_(True) for t in (q, k, v))
+    slopes = F.compute_alibi_slopes(H).to(dev)
+    scale = _scale32(D)
+    assert torch.autograd.gradcheck(lambda a, b, c: F.rational_attention(a, b, c, slopes, scale),
+                                    (q, k, v), eps=1e-6, atol=1e-6, rtol=1e-4)
+
+
+@pytest.mark.parametrize("D", [257, 320, 512, 640, 1024])
+def test_wide_head_dims_fp32(gpu, D):
+    B, H, T = 1, 2, 75
+    q, k, v, do = _inputs(D, B, H, T, D, torch.float32)
+    slopes = F.compute_alibi_slopes(H)
+    scale = 1.0 / math.sqrt(D)
+    o, L, dq, dk, dv = _run(q, k, v, do, slopes.to(dev), scale)
+    ro, rL = O.attention_fwd(q, k, v, slopes, scale, dtype=torch.float64)
+    assert _rel(o, ro) <= 1e-5 and _rel(L, rL) <= 1e-5, (_rel(o, ro), _rel(L, rL))
+    rq, rk, rv = O.attention_bwd(q, k, v, o, L, do, slopes, scale, dtype=torch.float64)
+    for name, got, ref in (("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
+        assert _rel(got, ref) <= 1e-5, (D, name, _rel(got, ref))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_wide_head_dim_lowp(gpu, dtype):
+    B, H, T, D = 1, 3, 140, 512
+    q, k, v, do = _inputs(11, B, H, T, D, dtype)
+    slopes = F.compute_alibi_slopes(H)
+    scale = 1.0 / math.sqrt(D)
+    with pytest.warns(RuntimeWarning, match="head dim 512"):
+        o, L, dq, dk, dv = _run(q, k, v, do, slopes.to(dev), scale)
+    assert o.dtype == dtype and dq.dtype == dtype
+    ro, rL = O.attention_fwd(q, k, v, slopes, scale, dtype=torch.float32)
+    check_lowp(o, ro, dtype, "o")
+    rq, rk, rv = O.attention_bwd(q, k, v, o, L, do, slopes, scale, dtype=torch.float32)
+    for name, got, ref in (("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
+        check_lowp(got, ref, dtype, name)
+
+
+def test_wide_head_dim_masked_noncausal_fp32(gpu):
+    B, H, T, D = 2, 2, 100, 384
+    q, k, v, do = _inputs(5, B, H, T, D, torch.float32)
+    slopes = F.compute_alibi_slopes(H)
+    scale = 1.0 / math.sqrt(D)
+    km = torch.ones(B, T, dtype=torch.int32)
+    km[0, 60:] = 0
+    km[1, ::3] = 0
+    for causal in (True, False):
+        o, _, dq, dk, dv = _run(q, k, v, do, slopes.to(dev), scale, key_mask=km, causal=causal)
+        ro, rL = O.attention_fwd(q, k, v, slopes, scale, dtype=torch.float64, causal=causal,
+                                 key_mask=km)
+        assert _rel(o, ro) <= 1e-5, (causal, _rel(o, ro))
+        rq, rk, rv = O.attention_bwd(q, k, v, ro, rL, do, slopes, scale, dtype=torch.float64,
+                                     causal=causal, key_mask=km)
+        for name, got, ref in (("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
+            assert _rel(got, ref) <= 1e-5, (causal, name, _rel(got, ref))
+
+
+def test_head_dim_above_1024_is_rejected(gpu):
+    q = torch.zeros(1, 1, 4, 1040, device=dev)
+    with pytest.raises(RuntimeError, match="head dim 1040 > 1024"):
+        F.rational_attention_forward(q, q, q, torch.ones(1, device=dev), 1.0)

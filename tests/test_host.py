@@ -210,3 +210,25 @@ def test_generate_cpu_follows_reference_loop():
             logits[logits < v[:, [-1]]] = float("-inf")
             idx = torch.cat((idx, torch.multinomial(torch.softmax(logits, -1), 1)), dim=1)
     assert torch.equal(out, idx)
+
+
+def test_tiled_fallback_reasons_mirror_the_mfma_limits():
+    # the wrapper's warning predicts every fallback of a bf16 / fp16 call to
+    # the tiled kernels: head dim, 16-byte rows, and 31-bit byte offsets
+    # within a (b, h) slice (csrc/attn_mfma.hip offsets_ok: (T + 128) * row
+    # stride * 2 bytes must stay below 2^31)
+    from fastalgebraictransformer_amd.forward import _tiled_reason
+    T, D = 4096, 128
+    contiguous = [((16 * T * D, T * D, D), 0)]
+    assert _tiled_reason(contiguous, D, T, 2) is None
+    assert "head dim 96" in _tiled_reason(contiguous, 96, T, 2)
+    assert "16-byte" in _tiled_reason([((T * D, T * D, D), 8)], D, T, 2)
+    assert "16-byte" in _tiled_reason([((T * D, T * D, D + 1), 0)], D, T, 2)
+    # the model's packed qkv [B, T, 3, H, D] (H = 16, D = 128): row stride 6144
+    st = 3 * 16 * 128
+    packed = [((T * st, D, st), 0)]
+    last_ok = (0x7FFFFFFF // (st * 2)) - 128
+    assert _tiled_reason(packed, D, last_ok, 2) is None
+    assert "31-bit" in _tiled_reason(packed, D, last_ok + 1, 2)
+    # a row stride below D (overlapping rows) also leaves the MFMA kernels
+    assert _tiled_reason([((T * D, T * D, 64), 0)], D, T, 2) is not None
