@@ -55,6 +55,7 @@ sys.path.insert(0, ROOT)
 METRIC = "attn fwd+bwd TFLOP/s (% MFMA peak) at S=4096; fused-op HBM GB/s (% peak)"
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+PEAK_FP32_TFLOPS = 157.3   # MI355X fp32 (vector and dense matrix)
 
 # HBM bytes per call at the benchmark shape come from the committed rocprofv3
 # summary profiles/attention_bench_hbm_traffic.md: FETCH_SIZE and WRITE_SIZE
@@ -65,12 +66,17 @@ TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "attention_bench_hbm_traffic.md
 
 
 def measured_traffic():
+    """{call: bytes} from the summary's "traffic <call> <bytes>" lines, plus
+    "commit" -> the commit its line "commit <sha>" names (the build that was
+    profiled)."""
     out = {}
     try:
         for line in open(TRAFFIC_SUMMARY):
             parts = line.split()
             if len(parts) == 3 and parts[0] == "traffic":
                 out[parts[1]] = int(parts[2])
+            elif len(parts) == 2 and parts[0] == "commit":
+                out["commit"] = parts[1]
     except OSError:
         pass
     return out
@@ -122,6 +128,48 @@ def bench_attention(torch, F, steps, warmup, B=4, H=16, T=4096, D=128):
     return dict(ms=ms, wall_ms=wall * 1e3 / steps, fwd_ms=sum(fwd) / steps, bwd_ms=sum(bwd) / steps,
                 fwd_median_ms=fwd[steps // 2], bwd_median_ms=bwd[steps // 2],
                 flops_step=7 * unit, flops_fwd=2 * unit, flops_bwd=5 * unit)
+
+
+def bench_config1(torch, F, steps=50, warmup=10, B=2, H=12, T=512, D=64):
+    """the fp32 causal forward (B=2, H=12, S=512, D=64,
+    slopes 2^(-8(i+1)/12), scale 1/8) the reference benchmarks against its
+    PyTorch CPU path; the fp32 tiled kernels run it. Also the fwd+bwd step.
+    TFLOP/s count the same causal units as the headline (forward 2, fwd+bwd 7
+    x B*H*S^2*D flop)."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(1)
+    q, k, v, do = (torch.randn(B, H, T, D, generator=g).to(dev) for _ in range(4))
+    slopes = torch.tensor([2.0 ** (-8.0 * (i + 1) / H) for i in range(H)], dtype=torch.float32,
+                          device=dev)
+    scale = 1.0 / math.sqrt(D)
+    unit = B * H * T * T * D
+
+    def timed(fn):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps
+
+    fwd_ms = timed(lambda: F.rational_attention_forward(q, k, v, slopes, scale))
+    qg, kg, vg = (t.clone().requires_grad_(True) for t in (q, k, v))
+
+    def step():
+        for t in (qg, kg, vg):
+            t.grad = None
+        F.rational_attention(qg, kg, vg, slopes, scale).backward(do)
+    step_ms = timed(step)
+    return {"shape": {"B": B, "H": H, "S": T, "D": D}, "dtype": "fp32", "steps": steps,
+            "kernels": "fp32 tiled (VALU)",
+            "fwd_ms": round(fwd_ms, 4), "fwd_TFLOPs": round(2 * unit / (fwd_ms * 1e-3) / 1e12, 3),
+            "fwd_bwd_ms": round(step_ms, 4),
+            "fwd_bwd_TFLOPs": round(7 * unit / (step_ms * 1e-3) / 1e12, 3),
+            "frac_fp32_vector_peak_fwd": round(2 * unit / (fwd_ms * 1e-3) / 1e12 / PEAK_FP32_TFLOPS, 4)}
 
 
 def bench_attention_variants(torch, F, steps=10, warmup=3, B=4, H=16, T=4096, D=128):
@@ -628,6 +676,8 @@ def main():
     ap.add_argument("--no-config5", action="store_true",
                     help="skip the attention fwd+bwd at the 1.3B model's shape (B=2, H=16, S=8192)")
     ap.add_argument("--no-device", action="store_true", help="skip the MFMA / copy probes")
+    ap.add_argument("--no-config1", action="store_true",
+                    help="skip the config-1 fp32 attention timing (B=2, H=12, S=512, D=64)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain device-to-device copy of 1 GiB (3 times): the "
                          "reference for scaling the FETCH_SIZE / WRITE_SIZE counters")
@@ -680,7 +730,9 @@ def main():
         "roofline": {"bound": "mfma", "call": dom, "achieved": round(ach, 2),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(ach / PEAK_BF16_TFLOPS, 4),
-                     "traffic": measured_traffic().get(dom)},
+                     "traffic": measured_traffic().get(dom),
+                     "traffic_source": {"profile": os.path.relpath(TRAFFIC_SUMMARY, ROOT),
+                                        "commit": measured_traffic().get("commit")}},
         "kernels": {"kat_attn_fwd": {"ms": round(att["fwd_ms"], 4), "median_ms": round(att["fwd_median_ms"], 4),
                                      "TFLOPs": round(fwd_tf, 2), "algorithmic_flops": att["flops_fwd"]},
                     "kat_attn_bwd": {"ms": round(att["bwd_ms"], 4), "median_ms": round(att["bwd_median_ms"], 4),
@@ -695,6 +747,8 @@ def main():
             "ms_per_step": round(a5["ms"], 4), "TFLOPs": round(t5, 2),
             "frac_mfma_peak": round(t5 / PEAK_BF16_TFLOPS, 4),
             "fwd_ms": round(a5["fwd_ms"], 4), "bwd_ms": round(a5["bwd_ms"], 4)}
+    if not args.no_config1:
+        line["config1_fp32"] = bench_config1(torch, F)
     if not args.no_variants:
         line["attention_variants"] = bench_attention_variants(torch, F)
     if not args.no_decode:
