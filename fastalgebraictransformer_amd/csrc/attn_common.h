@@ -47,7 +47,8 @@ int attn_bwd_generic(const AttnArgs& a, const typename AccT<T>::type* delta, hip
 
 // bf16 / fp16 MFMA kernels; return KAT_EUNSUPPORTED when the shape is not covered.
 // The backward runs its own prep pass; ws holds attn_mfma_workspace() bytes for
-// the call's mode: per-row stats (float2), an fp16 copy of Q ([B*H][T][D]),
+// the call's mode: per-row stats (per 64-row tile: 4 cinv, then -4 cinv Delta),
+// an fp16 copy of Q ([B*H][T][D]),
 // per-tile exponents and dS-bound parts, per-32-key K exponents, the fp16 dS
 // tiles of a group of heads or of one band of a head's keys (at most 4 GiB of
 // them, or one band of 512 keys), and for banded calls one head's fp32 dQ

@@ -338,7 +338,8 @@ __global__ __launch_bounds__(256, QS == 2 ? 2 : 1) void attn_fwd_k(AttnArgs a) {
 // Everything the backward's MFMA kernels take besides the inputs (the
 // workspace, laid out by bwd_ws below).
 struct BwdWs {
-  float2* stats;  // per row (4 cinv, -4 cinv Delta) [B*H][T], then x 2^kq (the row's tile)
+  float* stats;   // per 64-row tile [B*H][nt]: 4 cinv of its 64 rows, then -4 cinv Delta
+                  // of them (two float[64]), then x 2^kq (the tile's dS exponent)
   f16* q16;       // fp16 copy of Q [B*H][T][D], scaled per 64-row tile
   int* qexp;      // per 64-row tile [B*H][nt]: its exponents
   int* kexp;      // per 32-key group [B*H][ceil(T / 32)]: the dK/dV kernel's
@@ -416,12 +417,21 @@ __global__ __launch_bounds__(256) void attn_bwd_prep_k(AttnArgs a, BwdWs ws) {
       dsq += __shfl_xor(dsq, o, 64);
     }
     vm = fmaxf(vm, sqrtf(vs));
+    // the tile's stats: rows past T get zeros (the dK/dV kernel DMAs whole
+    // 512-byte tiles, and a zero factor keeps its padding rows finite)
+    float* st = ws.stats + ((int64_t)bh * nt + t) * 128 + (row & 63);
     if (row < a.T) {
       const float c4u = 1.f / (4.f * (Lp[(int64_t)row * a.sl[2]] + a.eps));
-      if (sub == 0) ws.stats[(int64_t)bh * a.T + row] = make_float2(c4u, -c4u * dsum);
+      if (sub == 0) {
+        st[0] = c4u;
+        st[64] = -c4u * dsum;
+      }
       const float cw = fminf(4.1f, 1.125f * c4u);
       am = fmaxf(am, cw * sqrtf(dsq));
       bm = fmaxf(bm, cw * fabsf(dsum));
+    } else if (sub == 0) {
+      st[0] = 0.f;
+      st[64] = 0.f;
     }
   }
 #pragma unroll
@@ -510,9 +520,9 @@ __global__ __launch_bounds__(256) void attn_bwd_stscale_k(BwdWs ws, int T, int c
     const int kq = kh + std::min((ds_exp(fmaf(ws.abnd[t], vm, ws.bbnd[t])) - kh) & ~7, kTileExpSpan);
     if ((r & 63) == 0) ws.ktile[t] = kq;
     const float f = ldexpf(1.f, kq);
-    const int64_t x = (int64_t)bh * T + r;
-    const float2 s = ws.stats[x];
-    ws.stats[x] = make_float2(s.x * f, s.y * f);
+    float* st = ws.stats + t * 128 + (r & 63);
+    st[0] *= f;
+    st[64] *= f;
   }
 }
 
@@ -809,12 +819,12 @@ template <int D>
 struct DkvSmem {
   short q[2][kBN * D];      // Q16 tiles
   short o[2][kBN * D];      // dO tiles
-  float2 st[2][kBN];        // (4 cinv, -4 cinv Delta) of the tile's queries
+  float st[2][2 * kBN];     // the tile's stats: 4 cinv of its queries, then -4 cinv Delta
   f32x4 x[2][kNW][4][64];   // w: [chunk parity][key group][16-query half x ks][lane]
 };
 
 template <typename T, int D, int MODE>
-__global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float2* __restrict__ stats,
+__global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float* __restrict__ stats,
                                                          const f16* __restrict__ q16,
                                                          const int* __restrict__ qexp,
                                                          const int* __restrict__ ktile,
@@ -847,10 +857,10 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
   const T* kp = (const T*)a.k + b * a.sk[0] + h * a.sk[1];
   const T* vp = (const T*)a.v + b * a.sv[0] + h * a.sv[1];
   const T* dop = (const T*)a.dout + b * a.sdo[0] + h * a.sdo[1];
-  const float2* stp = stats + (int64_t)bh * T_;
+  const float* stp = stats + (int64_t)bh * ((T_ + 63) / 64) * 128;
   const uint32_t sk2 = (uint32_t)a.sk[2], sv2 = (uint32_t)a.sv[2], sdo2 = (uint32_t)a.sdo[2];
   const uint32_t qbytes = row_bytes(T_, D, D), obytes = row_bytes(T_, sdo2, D);
-  const uint32_t stbytes = (uint32_t)T_ * 8u;
+  const uint32_t stbytes = (uint32_t)((T_ + 63) / 64) * 512u;
   const float slope = a.slopes[h];
   const float scale = a.scale;
   // the stats carry their tile's dS exponent (stats.x = 2^kq 4 cinv); P takes
@@ -951,7 +961,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
       do_.issue(sm.o[buf], dop, obytes, qrow0, sdo2, w);
     }
     if (w == 0 && lane < 32) {
-      const uint32_t skip = (uint32_t)qrow0 * 8u;
+      const uint32_t skip = (uint32_t)qrow0 * 8u;  // qrow0 is a multiple of 64: 512 bytes per tile
       dma16(rsrc_words((const char*)stp + skip, stbytes > skip ? stbytes - skip : 0u), lds_addr(sm.st[buf]),
             st_off);
     }
@@ -975,12 +985,10 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
   // P role: P (input dtype) of a 16-query half, and w into the exchange buffer.
   // DIAG: a chunk that straddles the diagonal (causal: keys past the query get
   // P = w = 0; non-causal: their bias becomes -slope (key - q)).
-  auto vp_ = [&](auto diag_tag, int qh, int hr, const f32x4 (&s_)[2], const float2* st_, f32x4 (*xw)[64],
+  auto vp_ = [&](auto diag_tag, int qh, int hr, const f32x4 (&s_)[2], const float* st_, f32x4 (*xw)[64],
                  int xg, uint32_t (&pp)[2][2]) __attribute__((always_inline)) {
     constexpr bool DIAG = decltype(diag_tag)::value;
-    const f32x4 s01 = *reinterpret_cast<const f32x4*>(st_ + hr + 4 * g);
-    const f32x4 s23 = *reinterpret_cast<const f32x4*>(st_ + hr + 4 * g + 2);
-    const float c4v[4] = {s01[0], s01[2], s23[0], s23[2]};
+    const f32x4 c4v = *reinterpret_cast<const f32x4*>(st_ + hr + 4 * g);  // 4 cinv of queries hr + 4 g + j
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       const float tterm = slx * (float)(kw + 16 * ks - qh);
@@ -1137,10 +1145,8 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
       if (need) {
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
-          const f32x4 s01 = *reinterpret_cast<const f32x4*>(sm.st[buf] + r0 + 16 * hh + 4 * g);
-          const f32x4 s23 = *reinterpret_cast<const f32x4*>(sm.st[buf] + r0 + 16 * hh + 4 * g + 2);
-          const float c4v[4] = {s01[0], s01[2], s23[0], s23[2]};
-          const float ndv[4] = {s01[1], s01[3], s23[1], s23[3]};
+          const f32x4 c4v = *reinterpret_cast<const f32x4*>(sm.st[buf] + r0 + 16 * hh + 4 * g);
+          const f32x4 ndv = *reinterpret_cast<const f32x4*>(sm.st[buf] + kBN + r0 + 16 * hh + 4 * g);
           uint32_t (&dp)[2][2] = hh ? pb : pa;
 #pragma unroll
           for (int ks = 0; ks < 2; ++ks) {
@@ -1219,7 +1225,8 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
 // ============================================================================
 bool attn_mfma_supported(int D) { return D == 32 || D == 64 || D == 128; }
 
-// Backward workspace (each part 256-byte aligned): per-row stats (float2), the
+// Backward workspace (each part 256-byte aligned): per-row stats (per 64-row
+// tile two float[64]: 4 cinv, then -4 cinv Delta), the
 // fp16 copy of Q ([B*H][T][D]), per-tile Q exponents and dS-bound parts and
 // dS exponents ([B*H][nt] each, nt = ceil(T / 64)), per-32-key K exponents,
 // the dS^T tiles, and (banded calls only) one head's fp32 dQ partial sums.
@@ -1273,7 +1280,7 @@ static BwdWs bwd_ws(void* base, int64_t B, int64_t H, int64_t T, int64_t D, bool
   BwdWs w;
   size_t o = 0;
   auto take = [&](size_t n) { char* q = p + o; o += al(n); return q; };
-  w.stats = reinterpret_cast<float2*>(take(rows * sizeof(float2)));
+  w.stats = reinterpret_cast<float*>(take(tiles * 128 * sizeof(float)));
   w.q16 = reinterpret_cast<f16*>(take(rows * (size_t)D * sizeof(f16)));
   w.qexp = reinterpret_cast<int*>(take(tiles * sizeof(int)));
   w.kexp = reinterpret_cast<int*>(take((size_t)BH * (size_t)((T + 31) / 32) * sizeof(int)));
