@@ -78,7 +78,7 @@ size_t bwd_workspace(int64_t B, int64_t H, int64_t T, int64_t D, int dtype, bool
 }  // namespace
 
 template <typename T> static int attn_fwd_t(const AttnArgs& a, hipStream_t st) {
-  if (!force_tiled() && attn_mfma_supported(a.D) && rows16<T>(a.q, a.sq) &&
+  if (!force_tiled() && attn_mfma_fwd_supported(a.D) && rows16<T>(a.q, a.sq) &&
       rows16<T>(a.k, a.sk) && rows16<T>(a.v, a.sv) && rows16<T>(a.o, a.so)) {
     const int rc = attn_fwd_mfma<T>(a, st);
     if (rc != KAT_EUNSUPPORTED) return rc;

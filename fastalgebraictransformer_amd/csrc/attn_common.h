@@ -55,7 +55,8 @@ int attn_bwd_generic(const AttnArgs& a, const typename AccT<T>::type* delta, hip
 // partial sums.
 template <typename T> int attn_fwd_mfma(const AttnArgs& a, hipStream_t st);
 template <typename T> int attn_bwd_mfma(const AttnArgs& a, void* ws, hipStream_t st);
-bool attn_mfma_supported(int D);
+bool attn_mfma_supported(int D);      // head dims of the MFMA backward (and forward)
+bool attn_mfma_fwd_supported(int D);  // head dims of the MFMA forward
 size_t attn_mfma_workspace(int64_t B, int64_t H, int64_t T, int64_t D, bool causal);
 
 }  // namespace kat

@@ -95,19 +95,22 @@ constexpr int kModeCausal = 1;
 constexpr int kModeKeyMask = 2;
 
 // ============================================================================
-// Forward: 4 waves x 16 QS queries per block.
+// Forward: NW waves x 16 QS queries per block.
 //   S^T[key][q]  = K Q^T (+ bias)   A = K  (LDS rows)         B = Q^T (VGPRs)
 //   O^T[d][q]   += V^T P^T          A = V^T (LDS transposed)  B = P^T (from S^T)
+// D <= 128: 4-wave blocks, two per CU. D = 256: the K and V tiles take 128 KB
+// of LDS, so one block per CU of 8 waves (two per SIMD), 16 queries per wave
+// (the Q fragments and O accumulators of 16 queries take 96 VGPRs).
 // ============================================================================
-template <typename T, int D, int MODE, int QS>
-__global__ __launch_bounds__(256, QS == 2 ? 2 : 1) void attn_fwd_k(AttnArgs a) {
+template <typename T, int D, int MODE, int QS, int NW = kNW>
+__global__ __launch_bounds__(64 * NW, NW == 4 && QS == 2 ? 2 : 1) void attn_fwd_k(AttnArgs a) {
   typedef Mfma<T> M;
   constexpr int KK = D / 32;  // k-steps of QK^T
   constexpr int DS = D / 16;  // 16-wide d subtiles of O^T
   constexpr bool kCausal = (MODE & kModeCausal) != 0;
   constexpr bool kKM = (MODE & kModeKeyMask) != 0;
   constexpr int RW = 16 * QS;    // queries per wave
-  constexpr int BMQ = kNW * RW;  // queries per block
+  constexpr int BMQ = NW * RW;  // queries per block
   __shared__ short sk[2][kBN * D];
   __shared__ short sv[2][kBN * D];
 
@@ -165,7 +168,7 @@ __global__ __launch_bounds__(256, QS == 2 ? 2 : 1) void attn_fwd_k(AttnArgs a) {
 #pragma unroll
   for (int qs = 0; qs < QS; ++qs) lsum[qs] = 0.f;
 
-  TileDma<D, kNW> dk, dv;
+  TileDma<D, NW> dk, dv;
   dk.init(w, lane, sk2);
   dv.init(w, lane, sv2);
 
@@ -314,7 +317,7 @@ __global__ __launch_bounds__(256, QS == 2 ? 2 : 1) void attn_fwd_k(AttnArgs a) {
   // own RW x D staging tile in the (now idle) K buffers, stored by rows
   T* __restrict__ op = (T*)a.o + b * a.so[0] + h * a.so[1];
   float* __restrict__ Lp = a.L + b * a.sl[0] + h * a.sl[1];
-  static_assert(sizeof(sk) >= kNW * RW * D * 2, "staging tiles fit the K buffers");
+  static_assert(sizeof(sk) >= NW * RW * D * 2, "staging tiles fit the K buffers");
   short* const et = &sk[0][0] + w * RW * D;
 #pragma unroll
   for (int qs = 0; qs < QS; ++qs) {
@@ -1224,6 +1227,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
 // Launchers
 // ============================================================================
 bool attn_mfma_supported(int D) { return D == 32 || D == 64 || D == 128; }
+bool attn_mfma_fwd_supported(int D) { return attn_mfma_supported(D) || D == 256; }
 
 // Backward workspace (each part 256-byte aligned): per-row stats (per 64-row
 // tile two float[64]: 4 cinv, then -4 cinv Delta), the
@@ -1314,9 +1318,9 @@ bool offsets_ok(const AttnArgs& a, bool bwd) {
 }
 
 template <typename T, int D, int MODE> int launch_fwd(const AttnArgs& a, hipStream_t st) {
-  constexpr int QS = kFwdQS;
-  const int64_t nb = (int64_t)((a.T + kFwdBM - 1) / kFwdBM) * a.B * a.H;
-  hipLaunchKernelGGL((attn_fwd_k<T, D, MODE, QS>), dim3((unsigned)nb), dim3(256), 0, st, a);
+  constexpr int QS = D == 256 ? 1 : kFwdQS, NW = D == 256 ? 8 : kNW, BMQ = NW * 16 * QS;
+  const int64_t nb = (int64_t)((a.T + BMQ - 1) / BMQ) * a.B * a.H;
+  hipLaunchKernelGGL((attn_fwd_k<T, D, MODE, QS, NW>), dim3((unsigned)nb), dim3(64 * NW), 0, st, a);
   return check_launch("kat_attn_fwd (mfma)");
 }
 
@@ -1366,6 +1370,7 @@ int launch_bwd(const AttnArgs& a, void* ws, hipStream_t st) {
 template <typename T> int attn_fwd_mfma(const AttnArgs& a, hipStream_t st) {
   if ((int64_t)((a.T + kFwdBM - 1) / kFwdBM) * a.B * a.H > 0x7fffffffLL || !offsets_ok(a, false))
     return KAT_EUNSUPPORTED;
+  if (a.D == 256) KAT_MODE_SWITCH(a, return (launch_fwd<T, 256, MODE>(a, st)));
   if (a.D == 128) KAT_MODE_SWITCH(a, return (launch_fwd<T, 128, MODE>(a, st)));
   if (a.D == 64) KAT_MODE_SWITCH(a, return (launch_fwd<T, 64, MODE>(a, st)));
   if (a.D == 32) KAT_MODE_SWITCH(a, return (launch_fwd<T, 32, MODE>(a, st)));

@@ -150,7 +150,7 @@ int kat_add_men_bwd(const void* dy, const void* dh, const void* h, const void* w
  * l_strides: 3 int64 = (b, h, t) strides of L. slopes: fp32 [H].
  * Replaces the host wrapper + rational_attention_fwd_kernel[(B,H,T)] launch at
  * forward.py:267-319 (kernel forward.py:49-159). dtype KAT_BF16/KAT_F16 use
- * the MFMA kernels (D in {32, 64, 128}, 16-byte aligned rows); KAT_F32,
+ * the MFMA kernels (D in {32, 64, 128, 256}, 16-byte aligned rows); KAT_F32,
  * KAT_F64 and other D (<= 1024; larger D returns KAT_EUNSUPPORTED) use the
  * tiled kernels, in fp32 arithmetic (fp64 for KAT_F64; the reference computes
  * in fp32 for every dtype, forward.py:103, and stores in the input dtype,

@@ -164,3 +164,74 @@ def test_head_dim_above_1024_is_rejected(gpu):
     q = torch.zeros(1, 1, 4, 1040, device=dev)
     with pytest.raises(RuntimeError, match="head dim 1040 > 1024"):
         F.rational_attention_forward(q, q, q, torch.ones(1, device=dev), 1.0)
+
+
+# ------------------------------------------------ MFMA forward at D = 256 ----
+# The MFMA forward also covers D = 256 (8-wave blocks of 16-query waves); the
+# backward at D = 256 runs the tiled kernels. Bar: check_lowp on o (the
+# north-star 2e-2 max-abs + 1/2 ulp, relative L2 <= 5e-3), L within 1e-2.
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("T", [1, 77, 300, 1025])
+def test_mfma_forward_d256(gpu, dtype, T, monkeypatch):
+    monkeypatch.setenv("KAT_ATTN_IMPL", "mfma")  # fail instead of falling back
+    B, H, D = 2, 3, 256
+    q, k, v, _ = _inputs(17 + T, B, H, T, D, dtype)
+    slopes = F.compute_alibi_slopes(H)
+    scale = 1.0 / math.sqrt(D)
+    o, L = F.rational_attention_forward(q, k, v, slopes.to(dev), scale)
+    torch.cuda.synchronize()
+    ro, rL = O.attention_fwd(q, k, v, slopes, scale, dtype=torch.float32)
+    check_lowp(o, ro, dtype, "o")
+    assert _rel(L, rL) <= 1e-2, _rel(L, rL)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_mfma_forward_d256_masked(gpu, causal, monkeypatch):
+    monkeypatch.setenv("KAT_ATTN_IMPL", "mfma")
+    B, H, T, D = 2, 2, 333, 256
+    q, k, v, _ = _inputs(23, B, H, T, D, torch.bfloat16)
+    slopes = F.compute_alibi_slopes(H)
+    scale = 1.0 / math.sqrt(D)
+    km = torch.ones(B, T, dtype=torch.int32)
+    km[0, 200:] = 0
+    km[1, 5::7] = 0
+    km[1, 64:128] = 0  # a whole key tile dropped
+    with torch.no_grad():
+        o = F.rational_attention_masked(q, k, v, slopes.to(dev), scale, key_mask=km, causal=causal)
+    torch.cuda.synchronize()
+    ro, _ = O.attention_fwd(q, k, v, slopes, scale, dtype=torch.float32, causal=causal, key_mask=km)
+    check_lowp(o, ro, torch.bfloat16, "o")
+
+
+def test_mfma_forward_d256_long_matches_tiled(gpu, monkeypatch):
+    # T = 4096 (the config-3 length): MFMA forward against the fp32 tiled
+    # kernels on the same bf16 inputs
+    B, H, T, D = 1, 2, 4096, 256
+    q, k, v, _ = _inputs(29, B, H, T, D, torch.bfloat16)
+    slopes = F.compute_alibi_slopes(8)[4:6].to(dev)
+    scale = 1.0 / math.sqrt(D)
+    monkeypatch.setenv("KAT_ATTN_IMPL", "mfma")
+    o_m, L_m = F.rational_attention_forward(q, k, v, slopes, scale)
+    monkeypatch.setenv("KAT_ATTN_IMPL", "tiled")
+    o_t, L_t = F.rational_attention_forward(q.float(), k.float(), v.float(), slopes, scale)
+    torch.cuda.synchronize()
+    check_lowp(o_m, o_t, torch.bfloat16, "o")
+    assert _rel(L_m, L_t) <= 1e-3
+
+
+def test_d256_training_step_mfma_forward_tiled_backward(gpu):
+    # fwd + bwd through autograd at D = 256: the forward on the MFMA kernel,
+    # the backward on the tiled kernels (which warns once); gradients against
+    # the oracle at the bf16 bar
+    B, H, T, D = 1, 2, 200, 256
+    q, k, v, do = _inputs(37, B, H, T, D, torch.bfloat16)
+    slopes = F.compute_alibi_slopes(H)
+    scale = 1.0 / math.sqrt(D)
+    with pytest.warns(RuntimeWarning, match="head dim 256"):
+        o, _, dq, dk, dv = _run(q, k, v, do, slopes.to(dev), scale)
+    ro, rL = O.attention_fwd(q, k, v, slopes, scale, dtype=torch.float32)
+    check_lowp(o, ro, torch.bfloat16, "o")
+    rq, rk, rv = O.attention_bwd(q, k, v, o, rL, do, slopes, scale, dtype=torch.float32)
+    for name, got, ref in (("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
+        check_lowp(got, ref, torch.bfloat16, name)
