@@ -20,6 +20,8 @@ throughput 7*B*H*S^2*D / step time in TFLOP/s. The same JSON line carries:
                  2-row batch slice plus embed / head / loss, extrapolated);
   * config5_attention -- fwd+bwd of the 1.3 B model's attention shape
                  (B=2, H=16, S=8192, D=128, bf16);
+  * head_dims  -- fwd+bwd at D = 32, 64 and 256 (bf16, S=4096, the headline's
+                 B*H*D, so the same flops), all on the MFMA kernels;
   * attention_variants -- fwd+bwd of the padding-mask / non-causal attention
                  extension at the same shape (right-padded batch, non-causal,
                  both), TFLOP/s over the (query, key) pairs each attends;
@@ -37,7 +39,7 @@ throughput 7*B*H*S^2*D / step time in TFLOP/s. The same JSON line carries:
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-fused]
                        [--no-variants] [--no-decode] [--no-model] [--no-model-large]
-                       [--no-config5]
+                       [--no-config5] [--no-head-dims]
        python bench.py --copy-calibration   (one plain 1 GiB device copy, for
                                              scaling HBM byte counters)
 """
@@ -675,6 +677,8 @@ def main():
                     help="skip the ~1.3B model step (batch 2 x 8192, ~47 GB; reported only)")
     ap.add_argument("--no-config5", action="store_true",
                     help="skip the attention fwd+bwd at the 1.3B model's shape (B=2, H=16, S=8192)")
+    ap.add_argument("--no-head-dims", action="store_true",
+                    help="skip the attention fwd+bwd at D = 32, 64 and 256")
     ap.add_argument("--no-device", action="store_true", help="skip the MFMA / copy probes")
     ap.add_argument("--no-config1", action="store_true",
                     help="skip the config-1 fp32 attention timing (B=2, H=12, S=512, D=64)")
@@ -747,6 +751,15 @@ def main():
             "ms_per_step": round(a5["ms"], 4), "TFLOPs": round(t5, 2),
             "frac_mfma_peak": round(t5 / PEAK_BF16_TFLOPS, 4),
             "fwd_ms": round(a5["fwd_ms"], 4), "bwd_ms": round(a5["bwd_ms"], 4)}
+    if not args.no_head_dims:
+        hd = {}
+        for Dh, Hh in ((32, 64), (64, 32), (256, 8)):
+            ah = bench_attention(torch, F, 10, 3, B=4, H=Hh, T=4096, D=Dh)
+            th = ah["flops_step"] / (ah["ms"] * 1e-3) / 1e12
+            hd[f"D{Dh}"] = {"shape": {"B": 4, "H": Hh, "S": 4096, "D": Dh}, "ms_per_step": round(ah["ms"], 4),
+                            "TFLOPs": round(th, 2), "frac_mfma_peak": round(th / PEAK_BF16_TFLOPS, 4),
+                            "fwd_ms": round(ah["fwd_ms"], 4), "bwd_ms": round(ah["bwd_ms"], 4)}
+        line["head_dims"] = hd
     if not args.no_config1:
         line["config1_fp32"] = bench_config1(torch, F)
     if not args.no_variants:

@@ -602,13 +602,17 @@ __device__ __forceinline__ int ds_col_query(int c) { return 16 * ((c >> 2) & 1) 
 // leaves its partial sums there (divided by 2^ek, exact) instead of writing
 // dQ; the bands run in order, so the sums are added in a fixed order.
 // ============================================================================
-constexpr int kDqW = kQB;           // waves per dQ block, one 64-query tile each
-constexpr int kDqM = kQB * 64;      // queries per dQ block
+constexpr int kDqW = kQB;           // waves per dQ block
 constexpr int kDqS = 4;             // stages (32 keys each)
+// queries per dQ wave: a 64-query tile, or at D = 256 (whose accumulators for
+// 64 queries would take all 256 VGPRs) a 32-query half of one; a block covers
+// kDqW waves' queries, i.e. a whole dS run (kQB tiles) or half of one
+template <int D> constexpr int dq_qw() { return D == 256 ? 32 : 64; }
+template <int D> constexpr int dq_block_queries() { return kDqW * dq_qw<D>(); }
 
 template <int D> struct DqSmem {
-  short k[kDqS][32 * D];          // K rows (converted in place to K16)
-  short s[kDqS][kDqW][32 * 64];   // each wave's dS^T rows
+  short k[kDqS][32 * D];                   // K rows (converted in place to K16)
+  short s[kDqS][kDqW][32 * dq_qw<D>()];    // each wave's dS^T rows
 };
 
 template <typename T, int D, int MODE>
@@ -618,57 +622,63 @@ __global__ __launch_bounds__(64 * kDqW, 1) void attn_bwd_dq_k(AttnArgs a, const 
                                                               int kb0, int nk, float* __restrict__ dqacc) {
   typedef Mfma<T> M;
   constexpr int DS = D / 16;
+  constexpr int QW = dq_qw<D>(), QC = QW / 16;  // queries per wave, 16-query column groups
+  constexpr int BQ = dq_block_queries<D>();      // queries per block
+  constexpr int WPT = 64 / QW;                   // waves per 64-query tile
   constexpr bool kCausal = (MODE & kModeCausal) != 0;
   // K16 rows: 1 KB DMA segments over the first KW waves (all 8 at D = 128,
   // 4 at D = 64); dS rows: each wave its own
   constexpr int KW = std::min(kDqW, 32 * D / 512);
   typedef TileDma<D, KW, 32> KDma;
-  typedef TileDma<64, 1, 32> SDma;
+  typedef TileDma<QW, 1, 32> SDma;
   __shared__ DqSmem<D> sm;
 
   const int T_ = a.T, H = a.H;
-  const int n_qb = (T_ + kDqM - 1) / kDqM;
+  const int n_qb = (T_ + BQ - 1) / BQ;
   int bl, rank;
   block_order((int)blockIdx.x, G, bl, rank);
   const int bh = bh0 + bl;
   const int qb = n_qb - 1 - rank;
-  const int q0 = qb * kDqM;
+  const int q0 = qb * BQ;
   const int b = bh / H, h = bh - b * H;
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
   const int g = lane >> 4, li = lane & 15;
   const int nt = (T_ + 63) / 64;
-  const int qtw = (q0 >> 6) + w;            // this wave's 64-query tile
+  const int qtw = (q0 >> 6) + w / WPT;      // this wave's 64-query tile
+  const int qh = WPT == 1 ? 0 : w % WPT;    // and its 32-query half (QW = 32)
+  const int tir = qtw % kQB;                // the tile's place in its dS run
   const bool wact = qtw < nt;
   const T* kp = (const T*)a.k + b * a.sk[0] + h * a.sk[1];
   const uint32_t sk2 = (uint32_t)a.sk[2];
   const uint32_t kbytes = row_bytes(T_, sk2, D);
-  const f16* run =
-      dst + ((int64_t)bl * ds_tiles_per_band(nt, kCausal, kb0, nk) + ds_run_base(qb, kCausal, kb0, nk)) * 4096;
+  const f16* run = dst + ((int64_t)bl * ds_tiles_per_band(nt, kCausal, kb0, nk) +
+                           ds_run_base(q0 / (kQB * 64), kCausal, kb0, nk)) * 4096;
   const int ng = (T_ + 31) / 32;  // 32-key groups (exponents)
   const int* kexp_h = kexp + (int64_t)bh * ng;
-  const int kt_all = kCausal ? std::min((q0 >> 6) + kDqW, nt) : nt;  // the block's key tiles: 0 .. kt_all - 1
+  const int kt_all = kCausal ? std::min((q0 >> 6) + BQ / 64, nt) : nt;  // the block's key tiles: 0 .. kt_all - 1
   const int kt_end = std::min(kb0 + nk, kt_all);
   const int n_st = 2 * (kt_end - kb0);      // stages: 32-key halves of the band's key tiles
-  float* const part = dqacc + ((int64_t)bl * nt + qtw) * 64 * D;  // this wave's partial sums
+  float* const part = dqacc + (((int64_t)bl * nt + qtw) * 64 + qh * QW) * D;  // this wave's partial sums
   const bool kw_ = w < KW;
   const int ndma = (kw_ ? KDma::SEGS : 0) + SDma::SEGS;  // this wave's DMA per stage
 
-  f32x4 acc[DS][4];  // [d subtile][16-query column group]
+  f32x4 acc[DS][QC];  // [d subtile][16-query column group]
 #pragma unroll
   for (int ds = 0; ds < DS; ++ds)
 #pragma unroll
-    for (int qc = 0; qc < 4; ++qc) acc[ds][qc] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int qc = 0; qc < QC; ++qc) acc[ds][qc] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   KDma dk;
   SDma dd;  // the wave's own dS rows
   dk.init(kw_ ? w : 0, lane, sk2);
-  // LDS slot (row, p) of the swizzled [32][64] stage tile takes data chunk
+  // LDS slot (row, p) of the swizzled [32][QW] stage tile takes data chunk
   // c = p ^ swz(row) of key row `row`, which the stored layout keeps in 1 KB
-  // block 2 (c / 4) + row / 16 at position 16 (c % 4) + row % 16
+  // block 2 (c / 4) + row / 16 at position 16 (c % 4) + row % 16 (QW = 32:
+  // the 32-query half's two blocks, qh's 2 KB of the stage)
 #pragma unroll
   for (int u = 0; u < SDma::SEGS; ++u) {
     const int row = u * SDma::RPS + lane / SDma::CPR;
-    const int c = (lane % SDma::CPR) ^ swz<64>(row);
+    const int c = (lane % SDma::CPR) ^ swz<QW>(row);
     dd.off[u] = (uint32_t)((((c >> 2) * 2 + (row >> 4)) * 64 + 16 * (c & 3) + (row & 15)) * 16);
   }
   auto tile_in = [&](int kt) __attribute__((always_inline)) { return wact && (!kCausal || kt <= qtw); };
@@ -677,20 +687,19 @@ __global__ __launch_bounds__(64 * kDqW, 1) void attn_bwd_dq_k(AttnArgs a, const 
     const int kl = st >> 1;
     if (kw_) dk.issue(sm.k[buf], kp, kbytes, 32 * (2 * kb0 + st), sk2, w);
     const bool have = tile_in(kb0 + kl);
-    dd.template issue<true>(sm.s[buf][w], run + (have ? ((int64_t)kl * kQB + w) * 4096 : 0), have ? 8192u : 0u,
-                            32 * (st & 1), 64, 0);
+    dd.template issue<true>(sm.s[buf][w], run + (have ? ((int64_t)kl * kQB + tir) * 4096 + qh * 1024 : 0),
+                            have ? 8192u - 2048u * qh : 0u, 32 * (st & 1), 64, 0);
   };
   // stage st has landed when at most the stages issued after it (up to `ahead`
   // of them) are in flight (loads complete in order); the count is an immediate
+  constexpr int kA = KDma::SEGS + SDma::SEGS, kB = SDma::SEGS;
   auto wait_for = [&](int st, int ahead) __attribute__((always_inline)) {
     const int after = std::min(n_st - 1 - st, ahead) * ndma;
-    switch (after) {
-      case 2 * (KDma::SEGS + SDma::SEGS): __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * (KDma::SEGS + SDma::SEGS))); break;
-      case KDma::SEGS + SDma::SEGS: __builtin_amdgcn_s_waitcnt(0x0F70 | (KDma::SEGS + SDma::SEGS)); break;
-      case 2 * SDma::SEGS: __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * SDma::SEGS)); break;
-      case SDma::SEGS: __builtin_amdgcn_s_waitcnt(0x0F70 | SDma::SEGS); break;
-      default: dma_wait();
-    }
+    if (after == 2 * kA) __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * kA));
+    else if (after == kA) __builtin_amdgcn_s_waitcnt(0x0F70 | kA);
+    else if (after == 2 * kB) __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * kB));
+    else if (after == kB) __builtin_amdgcn_s_waitcnt(0x0F70 | kB);
+    else dma_wait();
   };
   // exponent of stage st's 32 keys (a stage past the last key group holds only
   // zero rows: any exponent serves)
@@ -713,7 +722,7 @@ __global__ __launch_bounds__(64 * kDqW, 1) void attn_bwd_dq_k(AttnArgs a, const 
 #pragma unroll
     for (int ds = 0; ds < DS; ++ds)
 #pragma unroll
-      for (int qc = 0; qc < 4; ++qc) acc[ds][qc] = *reinterpret_cast<const f32x4*>(part + ((ds * 4 + qc) * 64 + lane) * 4);
+      for (int qc = 0; qc < QC; ++qc) acc[ds][qc] = *reinterpret_cast<const f32x4*>(part + ((ds * QC + qc) * 64 + lane) * 4);
     dma_wait();
   }
   for (int st = 0; st < kDqS - 1; ++st)
@@ -734,19 +743,19 @@ __global__ __launch_bounds__(64 * kDqW, 1) void attn_bwd_dq_k(AttnArgs a, const 
 #pragma unroll
       for (int ds = 0; ds < DS; ++ds)
 #pragma unroll
-        for (int qc = 0; qc < 4; ++qc) acc[ds][qc] *= f;
+        for (int qc = 0; qc < QC; ++qc) acc[ds][qc] *= f;
       ek = est;
     }
     if (tile_in(kt)) {
       const short* sd = sm.s[buf][w];
-      i16x8 bq[4];
+      i16x8 bq[QC];
 #pragma unroll
-      for (int qc = 0; qc < 4; ++qc) bq[qc] = frag_tr<64>(sd, 0, 16 * qc, g, li);
+      for (int qc = 0; qc < QC; ++qc) bq[qc] = frag_tr<QW>(sd, 0, 16 * qc, g, li);
 #pragma unroll
       for (int ds = 0; ds < DS; ++ds) {
         const i16x8 at = frag_tr<D>(sm.k[buf], 0, 16 * ds, g, li);
 #pragma unroll
-        for (int qc = 0; qc < 4; ++qc) acc[ds][qc] = mma_f16(at, bq[qc], acc[ds][qc]);
+        for (int qc = 0; qc < QC; ++qc) acc[ds][qc] = mma_f16(at, bq[qc], acc[ds][qc]);
       }
     }
     // the stage after the next has landed (the next is converted), and every
@@ -772,19 +781,21 @@ __global__ __launch_bounds__(64 * kDqW, 1) void attn_bwd_dq_k(AttnArgs a, const 
 #pragma unroll
       for (int ds = 0; ds < DS; ++ds)
 #pragma unroll
-        for (int qc = 0; qc < 4; ++qc) *reinterpret_cast<f32x4*>(part + ((ds * 4 + qc) * 64 + lane) * 4) = acc[ds][qc] * f;
+        for (int qc = 0; qc < QC; ++qc)
+          *reinterpret_cast<f32x4*>(part + ((ds * QC + qc) * 64 + lane) * 4) = acc[ds][qc] * f;
     }
     return;
   }
   T* __restrict__ dqp = (T*)a.dq + b * a.sdq[0] + h * a.sdq[1];
   const float osc = ldexpf(a.scale, -((wact ? ktile[(int64_t)bh * nt + qtw] : 0) + ek));
-  // the wave's 64 query rows through its own 64 x D staging tile in the
+  // the wave's QW query rows through its own QW x D staging tile in the
   // (now idle) stage buffers
-  static_assert(sizeof(sm) >= kDqW * 64 * D * 2, "staging tiles fit the stage buffers");
-  short* const et = reinterpret_cast<short*>(&sm) + w * 64 * D;
+  static_assert(sizeof(sm) >= kDqW * QW * D * 2, "staging tiles fit the stage buffers");
+  short* const et = reinterpret_cast<short*>(&sm) + w * QW * D;
 #pragma unroll
-  for (int qc = 0; qc < 4; ++qc) {
-    // column 16 qc + li of the tile: half (qc >> 1), column 16 (qc & 1) + li in it
+  for (int qc = 0; qc < QC; ++qc) {
+    // column 16 qc + li of the wave's queries: 32-query half (qc >> 1), column
+    // 16 (qc & 1) + li in it
     const int r = 32 * (qc >> 1) + ds_col_query(16 * (qc & 1) + li);
 #pragma unroll
     for (int ds = 0; ds < DS; ++ds) {
@@ -793,7 +804,7 @@ __global__ __launch_bounds__(64 * kDqW, 1) void attn_bwd_dq_k(AttnArgs a, const 
     }
   }
   __syncthreads();  // orders the tile's writes before its reads
-  epi_rows_out<T, D, 64>(et, lane, dqp, a.sdq[2], 64 * qtw, T_);
+  epi_rows_out<T, D, QW>(et, lane, dqp, a.sdq[2], 64 * qtw + QW * qh, T_);
 }
 
 // ============================================================================
@@ -818,15 +829,19 @@ __global__ __launch_bounds__(64 * kDqW, 1) void attn_bwd_dq_k(AttnArgs a, const 
 // The D role computes dP one chunk ahead so that the reads of w issued after
 // the barrier overlap with MFMAs.
 // ============================================================================
-template <int D>
+template <int D, int KS>
 struct DkvSmem {
-  short q[2][kBN * D];      // Q16 tiles
-  short o[2][kBN * D];      // dO tiles
-  float st[2][2 * kBN];     // the tile's stats: 4 cinv of its queries, then -4 cinv Delta
-  f32x4 x[2][kNW][4][64];   // w: [chunk parity][key group][16-query half x ks][lane]
+  short q[2][kBN * D];         // Q16 tiles
+  short o[2][kBN * D];         // dO tiles
+  float st[2][2 * kBN];        // the tile's stats: 4 cinv of its queries, then -4 cinv Delta
+  f32x4 x[2][kNW][2 * KS][64];  // w: [chunk parity][key group][16-query half x ks][lane]
+  float km[kNW];               // KS = 1: the key groups' max |k| (pairs share an exponent)
 };
 
-template <typename T, int D, int MODE>
+// KR: keys per wave pair, 32 (D <= 128) or 16 (D = 256, whose B fragments and
+// accumulators of 32 keys would exceed the register budget); the two pairs of
+// a 32-key group then share one K16 exponent
+template <typename T, int D, int MODE, int KR = kRows>
 __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float* __restrict__ stats,
                                                          const f16* __restrict__ q16,
                                                          const int* __restrict__ qexp,
@@ -839,13 +854,15 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
   constexpr int DS = D / 16;
   constexpr bool kCausal = (MODE & kModeCausal) != 0;
   constexpr bool kKM = (MODE & kModeKeyMask) != 0;
-  __shared__ DkvSmem<D> sm;
+  constexpr int KS = KR / 16;     // 16-key groups per wave
+  constexpr int BK = kNW * KR;    // keys per block
+  __shared__ DkvSmem<D, KS> sm;
 
   const int T_ = a.T, H = a.H;
   int bl, rank;
   block_order((int)blockIdx.x, G, bl, rank);  // rank 0: the first keys (most queries)
   const int bh = bh0 + bl;
-  const int k0 = kb0 * 64 + rank * kBM;  // blocks cover the band's keys
+  const int k0 = kb0 * 64 + rank * BK;  // blocks cover the band's keys
   const int b = bh / H, h = bh - b * H;
   // the key group (and the tile conditions derived from it) as scalars; the
   // role test stays a per-lane value: as a scalar branch the two roles' code
@@ -854,7 +871,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
   const int grp = w % kNW;
   const bool prole = (tid >> 6) < kNW;
   const int g = lane >> 4, li = lane & 15;
-  const int kw = k0 + kRows * grp;
+  const int kw = k0 + KR * grp;
 
   const f16* qp = q16 + (int64_t)bh * T_ * D;
   const T* kp = (const T*)a.k + b * a.sk[0] + h * a.sk[1];
@@ -877,20 +894,24 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
   const int ktg = kw >> 6;
   const bool dst_ok = ktg < nt;
   f16* const dsh = dst + (int64_t)bl * ds_tiles_per_band(nt, kCausal, kb0, nk) * 4096;
-  const uint32_t dso = (uint32_t)((grp & 1) * 2048 + lane * 8);  // block 4 (grp & 1), lane's 16 bytes
+  // block 4 kh2 + 2 qh + ks of the tile (kh2: the 32-key half, ks: the
+  // 16-key group); dso: kh2's blocks plus the lane's 16 bytes, dsk: the
+  // wave's first 16-key group
+  const uint32_t dso = (uint32_t)(((kw & 63) >> 5) * 2048 + lane * 8);
+  const int dsk = (kw >> 4) & 1;
   f16* dtile = dsh;  // the current query tile's dS^T tile
 
   // B operands: K16^T (P role) or V^T (D role) fragments; lane (g, li) holds row
   // kw + 16 ks + li, columns 32 kk + 8 g .. +7
   // (P role: scaled by 2^ekw, the exponent tile_exp gives the wave's 32 keys)
-  i16x8 bfr[2][KK];
+  i16x8 bfr[KS][KK];
   int ekw = 0;
   {
     const __amdgpu_buffer_rsrc_t rk = rsrc(kp, row_bytes(T_, sk2, D));
     const __amdgpu_buffer_rsrc_t rv = rsrc(vp, row_bytes(T_, sv2, D));
     float km = 0.f;
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
+    for (int ks = 0; ks < KS; ++ks) {
       const uint32_t key = (uint32_t)(kw + 16 * ks + li);
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk) {
@@ -905,12 +926,22 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
     if (prole) {
 #pragma unroll
       for (int o = 32; o > 0; o >>= 1) km = fmaxf(km, __shfl_xor(km, o, 64));
+    }
+    if constexpr (KS == 1) {
+      // the 32-key group's two 16-key halves (waves grp and grp ^ 1) share one
+      // exponent: the max of both
+      if (prole && lane == 0) sm.km[grp] = km;
+      __syncthreads();
+      if (prole) km = fmaxf(km, sm.km[grp ^ 1]);
+    }
+    if (prole) {
       ekw = tile_exp(km);
       // the dQ kernel converts these 32 keys with the same exponent
-      if (lane == 0 && kw < T_) kexp[(int64_t)bh * ((T_ + 31) / 32) + (kw >> 5)] = ekw;
+      if (lane == 0 && kw < T_ && (KS == 2 || (grp & 1) == 0))
+        kexp[(int64_t)bh * ((T_ + 31) / 32) + (kw >> 5)] = ekw;
       const float fk = ldexpf(1.f, ekw);
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
+      for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
         for (int kk = 0; kk < KK; ++kk) bfr[ks][kk] = to_f16x8s<T>(bfr[ks][kk], fk);
     }
@@ -933,23 +964,27 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
   // rows are zero and the other keys' rows do not depend on it. The kernel
   // computes every key and stores zeros for dropped ones; a wave group whose
   // 32 keys are all dropped skips the work.
-  bool kval[2] = {true, true};
+  bool kval[KS];
   bool gany = true;
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) kval[ks] = true;
   if constexpr (kKM) {
     const uint8_t* kmb = a.km + (int64_t)b * a.skm;
+    bool any = false;
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
+    for (int ks = 0; ks < KS; ++ks) {
       const int key = kw + 16 * ks + li;
       kval[ks] = key < T_ && kmb[key] != 0;
+      any = any || kval[ks];
     }
-    gany = __builtin_amdgcn_ballot_w64(kval[0] || kval[1]) != 0ull;
+    gany = __builtin_amdgcn_ballot_w64(any) != 0ull;
   }
 
-  f32x4 acc[DS][2];  // dV^T (P role) or dK^T (D role)
+  f32x4 acc[DS][KS];  // dV^T (P role) or dK^T (D role)
 #pragma unroll
   for (int ds = 0; ds < DS; ++ds)
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) acc[ds][ks] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int ks = 0; ks < KS; ++ks) acc[ds][ks] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // the P role's waves stage the tiles: the D role's waves then have no loads
   // in flight inside the loop and never wait for their dS stores
@@ -971,15 +1006,15 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
   };
 
   // S (P role) or dP (D role) of the 16 queries at tile rows hr .. hr + 15
-  auto m1 = [&](auto role, int hr, f32x4 (&s_)[2], const short* as_) __attribute__((always_inline)) {
+  auto m1 = [&](auto role, int hr, f32x4 (&s_)[KS], const short* as_) __attribute__((always_inline)) {
     constexpr bool P = decltype(role)::value;
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) s_[ks] = P ? cbx : f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int ks = 0; ks < KS; ++ks) s_[ks] = P ? cbx : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {
       const i16x8 fa = lds16(as_ + soff<D>(hr + li, 32 * kk + 8 * g));
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
+      for (int ks = 0; ks < KS; ++ks) {
         if constexpr (P) s_[ks] = mma_f16(fa, bfr[ks][kk], s_[ks]);
         else s_[ks] = M::mma(fa, bfr[ks][kk], s_[ks]);
       }
@@ -988,12 +1023,12 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
   // P role: P (input dtype) of a 16-query half, and w into the exchange buffer.
   // DIAG: a chunk that straddles the diagonal (causal: keys past the query get
   // P = w = 0; non-causal: their bias becomes -slope (key - q)).
-  auto vp_ = [&](auto diag_tag, int qh, int hr, const f32x4 (&s_)[2], const float* st_, f32x4 (*xw)[64],
-                 int xg, uint32_t (&pp)[2][2]) __attribute__((always_inline)) {
+  auto vp_ = [&](auto diag_tag, int qh, int hr, const f32x4 (&s_)[KS], const float* st_, f32x4 (*xw)[64],
+                 int xg, uint32_t (&pp)[KS][2]) __attribute__((always_inline)) {
     constexpr bool DIAG = decltype(diag_tag)::value;
     const f32x4 c4v = *reinterpret_cast<const f32x4*>(st_ + hr + 4 * g);  // 4 cinv of queries hr + 4 g + j
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
+    for (int ks = 0; ks < KS; ++ks) {
       const float tterm = slx * (float)(kw + 16 * ks - qh);
       float pv[4];
       f32x4 wv;
@@ -1022,19 +1057,19 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
   };
   // acc^T += A^T B over the 32 queries at tile rows r0 .. r0 + 31, A = dO (P role)
   // or Q16 (D role) read transposed, B = P or dS
-  auto m2 = [&](auto role, int r0, const uint32_t (&pa)[2][2], const uint32_t (&pb)[2][2],
+  auto m2 = [&](auto role, int r0, const uint32_t (&pa)[KS][2], const uint32_t (&pb)[KS][2],
                 const short* as_) __attribute__((always_inline)) {
     constexpr bool P = decltype(role)::value;
-    i16x8 bf2[2];
+    i16x8 bf2[KS];
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) bf2[ks] = pack_frag(pa[ks][0], pa[ks][1], pb[ks][0], pb[ks][1]);
+    for (int ks = 0; ks < KS; ++ks) bf2[ks] = pack_frag(pa[ks][0], pa[ks][1], pb[ks][0], pb[ks][1]);
     i16x8 at[DS];
 #pragma unroll
     for (int ds = 0; ds < DS; ++ds) at[ds] = frag_tr<D>(as_, r0, 16 * ds, g, li);
 #pragma unroll
     for (int ds = 0; ds < DS; ++ds) {
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
+      for (int ks = 0; ks < KS; ++ks) {
         if constexpr (P) acc[ds][ks] = M::mma(at[ds], bf2[ks], acc[ds][ks]);
         else acc[ds][ks] = mma_f16(at[ds], bf2[ks], acc[ds][ks]);
       }
@@ -1045,9 +1080,9 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
 #pragma unroll
     for (int st = 0; st < DS / 2 - 1; ++st) {
       __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 2 * KS, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 2 * KS, 0);
   };
 
   // chunk c: queries qbase + 32 c .. +31, tile (c / 2) in buffer (c / 2) & 1,
@@ -1060,12 +1095,12 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
   };
   // no key of the wave lies past a query of the chunk (non-causal: or every key does)
   auto fullc = [&](int c) __attribute__((always_inline)) {
-    return qbase + 32 * c >= kw + kRows - 1 || (!kCausal && kw > qbase + 32 * c + 31);
+    return qbase + 32 * c >= kw + KR - 1 || (!kCausal && kw > qbase + 32 * c + 31);
   };
   if (n_it > 0) issue(0, qbase);
   if (prole) dma_wait();
   __syncthreads();
-  f32x4 dpA[2][2], dpB[2][2];  // D role: dP of the current and the next chunk
+  f32x4 dpA[2][KS], dpB[2][KS];  // D role: dP of the current and the next chunk
   if (!prole && needc(0)) {
     m1(std::false_type{}, 0, dpA[0], sm.o[0]);
     m1(std::false_type{}, 16, dpA[1], sm.o[0]);
@@ -1074,14 +1109,14 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
   // unrolled by four), so that the tile buffer, the rows within it and the
   // exchange buffer -- and with them every LDS address -- are a per-lane
   // register plus an immediate
-  auto step = [&](int c, auto cm_tag, f32x4 (&pcur)[2][2], f32x4 (&pnext)[2][2]) __attribute__((always_inline)) {
+  auto step = [&](int c, auto cm_tag, f32x4 (&pcur)[2][KS], f32x4 (&pnext)[2][KS]) __attribute__((always_inline)) {
     constexpr int CM = decltype(cm_tag)::value;
     constexpr int buf = CM >> 1, r0 = 32 * (CM & 1);
     const int it = c >> 1;
     const int qc = qbase + 32 * c;
     const bool need = needc(c), full = need && fullc(c);
     f32x4 (*xw)[64] = sm.x[CM & 1][grp];
-    uint32_t pa[2][2], pb[2][2];
+    uint32_t pa[KS][2], pb[KS][2];
     if constexpr ((CM & 1) == 0) {
       // a new query tile: its Q16 and dS exponents (both roles track them)
       const int eqt = qexp_h[(qbase >> 6) + it], kqt = ktile_h[(qbase >> 6) + it];
@@ -1099,7 +1134,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
 #pragma unroll
         for (int ds = 0; ds < DS; ++ds)
 #pragma unroll
-          for (int ks = 0; ks < 2; ++ks) acc[ds][ks] *= f;
+          for (int ks = 0; ks < KS; ++ks) acc[ds][ks] *= f;
       }
       eq = eqt;
       kq = kqt;
@@ -1110,15 +1145,15 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
       slx = above ? -slope : slope;
     }
     if (prole && need) {
-      f32x4 sA[2], sB[2];
+      f32x4 sA[KS], sB[KS];
       m1(std::true_type{}, r0, sA, sm.q[buf]);
       m1(std::true_type{}, r0 + 16, sB, sm.q[buf]);
       if (full) {
         vp_(std::false_type{}, qc, r0, sA, sm.st[buf], xw, 0, pa);
-        vp_(std::false_type{}, qc + 16, r0 + 16, sB, sm.st[buf], xw, 2, pb);
+        vp_(std::false_type{}, qc + 16, r0 + 16, sB, sm.st[buf], xw, KS, pb);
       } else {
         vp_(std::true_type{}, qc, r0, sA, sm.st[buf], xw, 0, pa);
-        vp_(std::true_type{}, qc + 16, r0 + 16, sB, sm.st[buf], xw, 2, pb);
+        vp_(std::true_type{}, qc + 16, r0 + 16, sB, sm.st[buf], xw, KS, pb);
       }
     }
     if constexpr ((CM & 1) == 0) {
@@ -1136,9 +1171,9 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
       // w of this chunk (read whether or not the chunk is needed: the buffer
       // always exists, and a conditional read leaves the compiler zeroing the
       // registers on the other path every chunk)
-      f32x4 wv[4];
+      f32x4 wv[2 * KS];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) wv[u] = xw[u][lane];
+      for (int u = 0; u < 2 * KS; ++u) wv[u] = xw[u][lane];
       if (needc(c + 1)) {
         constexpr int r1 = 32 * ((CM + 1) & 1);
         const short* os1 = sm.o[((CM + 1) >> 1) & 1];
@@ -1150,15 +1185,15 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
         for (int hh = 0; hh < 2; ++hh) {
           const f32x4 c4v = *reinterpret_cast<const f32x4*>(sm.st[buf] + r0 + 16 * hh + 4 * g);
           const f32x4 ndv = *reinterpret_cast<const f32x4*>(sm.st[buf] + kBN + r0 + 16 * hh + 4 * g);
-          uint32_t (&dp)[2][2] = hh ? pb : pa;
+          uint32_t (&dp)[KS][2] = hh ? pb : pa;
 #pragma unroll
-          for (int ks = 0; ks < 2; ++ks) {
+          for (int ks = 0; ks < KS; ++ks) {
             float dv[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
               // w = t^3 r^2 from t alone: r = 1 / (|s| + 1) equals t for s < 0
               // and 2 - t for s >= 0, i.e. min(t, 2 - t) (exact given t)
-              dv[j] = wv[2 * hh + ks][j] * fmaf(pcur[hh][ks][j], c4v[j], ndv[j]);
+              dv[j] = wv[KS * hh + ks][j] * fmaf(pcur[hh][ks][j], c4v[j], ndv[j]);
             }
             dp[ks][0] = pack2_f16(dv[0], dv[1]);
             dp[ks][1] = pack2_f16(dv[2], dv[3]);
@@ -1166,7 +1201,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
         }
         if constexpr (kKM) {
 #pragma unroll
-          for (int ks = 0; ks < 2; ++ks)
+          for (int ks = 0; ks < KS; ++ks)
             if (!kval[ks]) pa[ks][0] = pa[ks][1] = pb[ks][0] = pb[ks][1] = 0u;
         }
         // dS^T for the dQ kernel: 16 bytes per lane and ks (streaming stores:
@@ -1174,17 +1209,18 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
         if (dst_ok) {
           f16* const tb = dtile + (r0 >> 5) * 1024;
 #pragma unroll
-          for (int ks = 0; ks < 2; ++ks)
+          for (int ks = 0; ks < KS; ++ks)
             __builtin_nontemporal_store(pack_frag(pa[ks][0], pa[ks][1], pb[ks][0], pb[ks][1]),
-                                        reinterpret_cast<i16x8*>(tb + dso + 512 * ks));
+                                        reinterpret_cast<i16x8*>(tb + dso + 512 * (dsk + ks)));
         }
         m2(std::false_type{}, r0, pa, pb, sm.q[buf]);
-      } else if (dst_ok && c < n_ch && (!kCausal || (c >> 1) >= (grp >> 1))) {
+      } else if (dst_ok && c < n_ch && (!kCausal || (c >> 1) >= ((KR * grp) >> 6))) {
         // a skipped chunk inside a kept tile: its dS is zero
         f16* const tb = dtile + (r0 >> 5) * 1024;
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
-          __builtin_nontemporal_store(i16x8{0, 0, 0, 0, 0, 0, 0, 0}, reinterpret_cast<i16x8*>(tb + dso + 512 * ks));
+        for (int ks = 0; ks < KS; ++ks)
+          __builtin_nontemporal_store(i16x8{0, 0, 0, 0, 0, 0, 0, 0},
+                                      reinterpret_cast<i16x8*>(tb + dso + 512 * (dsk + ks)));
       }
     }
   };
@@ -1202,15 +1238,16 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
   T* __restrict__ outp = prole ? (T*)a.dv + b * a.sdv[0] + h * a.sdv[1] : (T*)a.dk + b * a.sdk[0] + h * a.sdk[1];
   const int64_t ostr = prole ? a.sdv[2] : a.sdk[2];
   const float osc = prole ? 1.f : ldexpf(scale, -(kq + eq));  // dK: dS's 2^kq and Q16's 2^eq undone (exact)
-  // the wave's 32 rows (keys) through its own 32 x D staging tile in the now
-  // idle tile buffers (8 waves x 32 x D x 2 bytes = the Q16 and dO buffers)
-  static_assert(sizeof(sm.q) + sizeof(sm.o) >= 8 * 32 * D * 2 && offsetof(DkvSmem<D>, q) == 0 &&
-                    offsetof(DkvSmem<D>, o) == sizeof(sm.q),
+  // the wave's KR rows (keys) through its own KR x D staging tile in the now
+  // idle tile buffers (8 waves x KR x D x 2 bytes within the Q16 and dO buffers)
+  typedef DkvSmem<D, KS> Smem;
+  static_assert(sizeof(sm.q) + sizeof(sm.o) >= 8 * KR * D * 2 && offsetof(Smem, q) == 0 &&
+                    offsetof(Smem, o) == sizeof(sm.q),
                 "staging tiles fit the tile buffers");
-  short* const et = reinterpret_cast<short*>(&sm) + w * 32 * D;
+  short* const et = reinterpret_cast<short*>(&sm) + w * KR * D;
   __syncthreads();  // every wave is done with the tile buffers
 #pragma unroll
-  for (int ks = 0; ks < 2; ++ks) {
+  for (int ks = 0; ks < KS; ++ks) {
 #pragma unroll
     for (int ds = 0; ds < DS; ++ds) {
       f32x4 v = acc[ds][ks];
@@ -1220,14 +1257,14 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
     }
   }
   __syncthreads();  // orders the tile's writes before its reads
-  epi_rows_out<T, D, 32>(et, lane, outp, ostr, kw, T_);
+  epi_rows_out<T, D, KR>(et, lane, outp, ostr, kw, T_);
 }
 
 // ============================================================================
 // Launchers
 // ============================================================================
-bool attn_mfma_supported(int D) { return D == 32 || D == 64 || D == 128; }
-bool attn_mfma_fwd_supported(int D) { return attn_mfma_supported(D) || D == 256; }
+bool attn_mfma_supported(int D) { return D == 32 || D == 64 || D == 128 || D == 256; }
+bool attn_mfma_fwd_supported(int D) { return attn_mfma_supported(D); }
 
 // Backward workspace (each part 256-byte aligned): per-row stats (per 64-row
 // tile two float[64]: 4 cinv, then -4 cinv Delta), the
@@ -1338,14 +1375,17 @@ int launch_bwd(const AttnArgs& a, void* ws, hipStream_t st) {
   if (int rc = check_launch("kat_attn_bwd (stats scale)")) return rc;
   // per group of heads (and per band of key tiles): dK, dV (and the dS^T
   // tiles), then dQ from those tiles
-  const int nt = (a.T + 63) / 64, nqb = (a.T + kDqM - 1) / kDqM;
+  constexpr int KR = D == 256 ? 16 : kRows, BK = kNW * KR;  // keys per wave pair and per dK/dV block
+  constexpr int BQ = dq_block_queries<D>();                 // queries per dQ block
+  const int nt = (a.T + 63) / 64, nqb = (a.T + BQ - 1) / BQ;
   for (int bh0 = 0; bh0 < BH; bh0 += w.group) {
     const int G = std::min(w.group, BH - bh0);
     for (int kb0 = 0; kb0 < nt; kb0 += w.band) {
       const int nk = std::min(w.band, nt - kb0);
-      const int64_t nb = (std::min<int64_t>((int64_t)(kb0 + nk) * 64, a.T) - (int64_t)kb0 * 64 + kBM - 1) / kBM;
-      const int64_t nbq = nqb - (kCausal ? kb0 / kQB : 0);
-      hipLaunchKernelGGL((attn_bwd_dkv_k<T, D, MODE>), dim3((unsigned)(nb * G)), dim3(512), 0, st, a, w.stats,
+      const int64_t nb = (std::min<int64_t>((int64_t)(kb0 + nk) * 64, a.T) - (int64_t)kb0 * 64 + BK - 1) / BK;
+      // causal: the query blocks wholly before the band have no tiles in it
+      const int64_t nbq = nqb - (kCausal ? (int64_t)kb0 * 64 / BQ : 0);
+      hipLaunchKernelGGL((attn_bwd_dkv_k<T, D, MODE, KR>), dim3((unsigned)(nb * G)), dim3(512), 0, st, a, w.stats,
                          w.q16, w.qexp, w.ktile, w.kexp, w.dst, bh0, G, kb0, nk);
       if (int rc = check_launch("kat_attn_bwd (dkv, mfma)")) return rc;
       hipLaunchKernelGGL((attn_bwd_dq_k<T, D, MODE>), dim3((unsigned)(nbq * G)), dim3(64 * kDqW), 0, st, a,
@@ -1379,6 +1419,7 @@ template <typename T> int attn_fwd_mfma(const AttnArgs& a, hipStream_t st) {
 
 template <typename T> int attn_bwd_mfma(const AttnArgs& a, void* ws, hipStream_t st) {
   if ((int64_t)((a.T + 63) / 64) * a.B * a.H > 0x7fffffffLL || !offsets_ok(a, true)) return KAT_EUNSUPPORTED;
+  if (a.D == 256) KAT_MODE_SWITCH(a, return (launch_bwd<T, 256, MODE>(a, ws, st)));
   if (a.D == 128) KAT_MODE_SWITCH(a, return (launch_bwd<T, 128, MODE>(a, ws, st)));
   if (a.D == 64) KAT_MODE_SWITCH(a, return (launch_bwd<T, 64, MODE>(a, ws, st)));
   if (a.D == 32) KAT_MODE_SWITCH(a, return (launch_bwd<T, 32, MODE>(a, ws, st)));

@@ -52,20 +52,18 @@ _MFMA_OFFSET_LIMIT = 0x7FFFFFFF
 _MFMA_ROW_PAD = 128
 
 
-# head dims the MFMA kernels cover: the forward also takes 256
-MFMA_FWD_DIMS = (32, 64, 128, 256)
-MFMA_BWD_DIMS = (32, 64, 128)
+# head dims the MFMA kernels cover (forward and backward)
+MFMA_DIMS = (32, 64, 128, 256)
 
 
-def _tiled_reason(shapes_strides_ptrs, D, T, elem, dims=MFMA_BWD_DIMS):
+def _tiled_reason(shapes_strides_ptrs, D, T, elem):
     """Why a bf16 / fp16 attention call would leave the MFMA kernels for the
     tiled ones (None if it takes them), from each operand's (b, h, t) strides
-    and data pointer: the head dim (``dims``: those of the call's kernels),
-    16-byte row alignment, and the 31-bit byte offsets the MFMA kernels use
-    within one (b, h) slice."""
-    if D not in dims:
+    and data pointer: the head dim, 16-byte row alignment, and the 31-bit byte
+    offsets the MFMA kernels use within one (b, h) slice."""
+    if D not in MFMA_DIMS:
         return (f"head dim {D} (the MFMA kernels cover "
-                f"{', '.join(str(d) for d in dims[:-1])} and {dims[-1]})")
+                f"{', '.join(str(d) for d in MFMA_DIMS[:-1])} and {MFMA_DIMS[-1]})")
     for strides, ptr in shapes_strides_ptrs:
         if ptr % 16 or any((st * elem) % 16 for st in strides):
             return "rows not 16-byte aligned (a view with an odd offset or stride)"
@@ -79,10 +77,9 @@ def _tiled_reason(shapes_strides_ptrs, D, T, elem, dims=MFMA_BWD_DIMS):
     return None
 
 
-def _warn_if_tiled(tensors, D, dtype, mfma_inputs=None, dims=MFMA_BWD_DIMS):
+def _warn_if_tiled(tensors, D, dtype, mfma_inputs=None):
     """bf16 / fp16 attention runs on the MFMA kernels when the head dim is 32,
-    64 or 128 (the forward: also 256), every [B, H, T, D] operand has 16-byte
-    aligned rows and the
+    64, 128 or 256, every [B, H, T, D] operand has 16-byte aligned rows and the
     inputs the kernels address by 31-bit offsets (q, k, v; and O, dO in the
     backward: ``mfma_inputs``) keep each (b, h) slice below 2^31 bytes;
     otherwise libkat falls back to the tiled kernels, which are correct but
@@ -94,9 +91,9 @@ def _warn_if_tiled(tensors, D, dtype, mfma_inputs=None, dims=MFMA_BWD_DIMS):
     T = tensors[0].shape[2]
     elem = tensors[0].element_size()
     align = [(t.stride()[:3], t.data_ptr()) for t in tensors]
-    reason = _tiled_reason(align, D, T, elem, dims)
+    reason = _tiled_reason(align, D, T, elem)
     if reason is None and mfma_inputs is not None:
-        reason = _tiled_reason([(t.stride()[:3], 0) for t in mfma_inputs], D, T, elem, dims)
+        reason = _tiled_reason([(t.stride()[:3], 0) for t in mfma_inputs], D, T, elem)
     if reason is None:
         return
     if (dtype, reason) not in _WARNED:
@@ -121,7 +118,7 @@ def _attn_fwd_into(q, k, v, out, L, alibi_slopes, scale, causal, eps, key_mask=N
     honours ``causal``; otherwise kat_attn_fwd, always causal as the reference."""
     lib = _lib.load()
     B, H, T, D = q.shape
-    _warn_if_tiled((q, k, v, out), D, q.dtype, mfma_inputs=(q, k, v), dims=MFMA_FWD_DIMS)
+    _warn_if_tiled((q, k, v, out), D, q.dtype, mfma_inputs=(q, k, v))
     slopes = alibi_slopes.to(device=q.device, dtype=torch.float32).contiguous()
     assert slopes.numel() == H, "alibi_slopes must have n_heads entries"
     strides = _lib.i64_array(_bht_strides(q) + _bht_strides(k) + _bht_strides(v) +

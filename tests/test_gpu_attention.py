@@ -125,7 +125,7 @@ def _check_lowp(o, L, dq, dk, dv, q, k, v, do, slopes, scale, sel=None, chunk=No
 def _pin_mfma(monkeypatch, D):
     # bf16 / fp16 calls whose head dim the MFMA kernels cover must run on them:
     # with KAT_ATTN_IMPL=mfma a fallback to the tiled kernels is an error
-    if D in (32, 64, 128):
+    if D in (32, 64, 128, 256):
         monkeypatch.setenv("KAT_ATTN_IMPL", "mfma")
 
 
@@ -142,7 +142,8 @@ def test_golden_bf16(gpu, name, monkeypatch):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("B,H,T,D", [(1, 2, 64, 64), (1, 3, 200, 128), (2, 2, 333, 64),
                                      (1, 2, 257, 32), (2, 3, 1000, 32), (1, 1, 1, 32),
-                                     (1, 1, 1, 128), (1, 2, 1000, 128)])
+                                     (1, 1, 1, 128), (1, 2, 1000, 128), (1, 2, 200, 256),
+                                     (2, 2, 333, 256), (1, 1, 1, 256), (1, 2, 1000, 256)])
 def test_lowp_shapes(gpu, dtype, B, H, T, D, monkeypatch):
     _pin_mfma(monkeypatch, D)
     q, k, v, do = _inputs(7 * T + D, B, H, T, D, dtype)
@@ -214,7 +215,7 @@ def test_backward_is_deterministic(gpu, monkeypatch):
         assert torch.equal(x, y)
 
 
-@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("D", [64, 128, 256])
 @pytest.mark.parametrize("masked", [False, True])
 def test_mfma_backward_is_invariant_to_the_upstream_gradient_scale(gpu, D, masked, monkeypatch):
     # dQ, dK, dV are linear in dO. A training step's dO is ~1e-5 .. 1e-7 per
@@ -280,7 +281,7 @@ def _scaled_check(q, k, v, do, slopes, scale, factors):
         assert excess <= 0, (name, float(err.max()), excess)
 
 
-@pytest.mark.parametrize("D", [32, 64, 128])
+@pytest.mark.parametrize("D", [32, 64, 128, 256])
 @pytest.mark.parametrize("case", ["v1e4", "do1e-6", "q1e5_k1e-5", "qk1e-4", "combined", "v1e3_do1e2"])
 def test_mfma_backward_input_range_bf16(gpu, D, case, monkeypatch):
     _pin_mfma(monkeypatch, D)
@@ -297,20 +298,24 @@ def test_mfma_backward_input_range_bf16(gpu, D, case, monkeypatch):
     _scaled_check(q, k, v, do, slopes, scale, factors)
 
 
-@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("D", [64, 128, 256])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_mfma_backward_key_groups_of_different_magnitude(gpu, D, dtype, monkeypatch):
+@pytest.mark.parametrize("width", [32, 16])
+def test_mfma_backward_key_groups_of_different_magnitude(gpu, D, dtype, width, monkeypatch):
     # K's fp16 form carries one exponent per 32 keys, chosen by the dK/dV
     # kernel and reused by the dQ kernel, which rescales its accumulators
     # whenever the next 32 keys bring another exponent. Keys whose magnitude
-    # cycles 2^s, 1, 2^-s from one 32-key group to the next give every group
-    # a different exponent (also inside each 64-key tile): a wrong exponent
-    # for any group would move that group's share of dq or dk by 2^s.
+    # cycles 2^s, 1, 2^-s from one group of `width` keys to the next give every
+    # 32-key group a different exponent (also inside each 64-key tile): a wrong
+    # exponent for any group would move that group's share of dq or dk by 2^s.
+    # width 16: the two 16-key halves of a 32-key group differ (at D = 256 two
+    # wave pairs own them and must agree on the group's exponent: one from
+    # the smaller half would overflow the larger half's fp16 copy).
     _pin_mfma(monkeypatch, D)
     B, H, T = 1, 2, 300
     q, k, v, do = (t.float() for t in _inputs(47 + D, B, H, T, D, torch.float32))
     sh = 12 if dtype == torch.float16 else 20
-    gsc = torch.tensor([2.0 ** (sh * (1 - (j // 32) % 3)) for j in range(T)])
+    gsc = torch.tensor([2.0 ** (sh * (1 - (j // width) % 3)) for j in range(T)])
     k = k * gsc.view(1, 1, T, 1).to(k.device)
     q, k, v, do = (t.to(dtype) for t in (q, k, v, do))
     slopes = F.compute_alibi_slopes(H)
@@ -333,12 +338,12 @@ def test_mfma_backward_key_groups_of_different_magnitude(gpu, D, dtype, monkeypa
             # lies so far below its query tile's largest that fp16 holds it in
             # its subnormal range -- dS has one exponent per query tile, none
             # per key, the documented limit)
-            for j0 in range(0, T, 32):
-                gg, gr = got[:, :, j0:j0 + 32], ref[:, :, j0:j0 + 32]
+            for j0 in range(0, T, width):
+                gg, gr = got[:, :, j0:j0 + width], ref[:, :, j0:j0 + width]
                 assert _rel_max(gg, gr) <= 2e-2, (name, j0, _rel_max(gg, gr))
 
 
-@pytest.mark.parametrize("D", [32, 64, 128])
+@pytest.mark.parametrize("D", [32, 64, 128, 256])
 def test_mfma_backward_input_range_fp16(gpu, D, monkeypatch):
     _pin_mfma(monkeypatch, D)
     B, H, T = 1, 2, 300
@@ -351,7 +356,7 @@ def test_mfma_backward_input_range_fp16(gpu, D, monkeypatch):
                   {"o": fv, "dq": fv * fd * fk, "dk": fv * fd * fq, "dv": fd})
 
 
-@pytest.mark.parametrize("D", [32, 64, 128])
+@pytest.mark.parametrize("D", [32, 64, 128, 256])
 def test_mfma_attention_is_exactly_equivariant_to_power_of_two_scales(gpu, D, monkeypatch):
     # inputs on a grid of 1/16 are exact in fp16 at every scale used below, so
     # the fp16 copies hold the same significands whatever their exponent: then
@@ -390,7 +395,7 @@ def test_tiled_fallback_warns_once(gpu):
 
 
 @pytest.mark.parametrize("mode", ["plain", "masked", "noncausal"])
-@pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 128), (torch.float16, 64)])
+@pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 128), (torch.float16, 64), (torch.bfloat16, 256)])
 def test_mfma_backward_head_groups_are_bit_identical(gpu, mode, dtype, D, monkeypatch):
     # the backward keeps the dS^T tiles of one group of heads at a time in the
     # workspace (dK/dV stores them, dQ reads them back); a small cap
@@ -432,7 +437,7 @@ def test_mfma_backward_head_groups_are_bit_identical(gpu, mode, dtype, D, monkey
 
 
 @pytest.mark.parametrize("mode", ["plain", "masked", "noncausal"])
-@pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 128), (torch.float16, 64)])
+@pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 128), (torch.float16, 64), (torch.bfloat16, 256)])
 def test_mfma_backward_key_bands_are_bit_identical(gpu, mode, dtype, D, monkeypatch):
     # when one head's dS^T tiles exceed the cap, the backward runs dK/dV + dQ
     # per band of key tiles (multiples of 8 tiles = 512 keys), dQ keeping fp32
@@ -523,7 +528,7 @@ def test_mfma_backward_at_65536_in_bands_matches_fp32_tiled(gpu, monkeypatch):
     print("T = 65536 in bands vs fp32 tiled: " + ", ".join(f"{n} {e:.3e} / {r:.3e}" for n, (e, r) in errs.items()))
 
 
-@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("D", [64, 128, 256])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_mfma_backward_query_tiles_of_different_magnitude(gpu, D, dtype, monkeypatch):
     # dS enters the fp16 products with one exponent per 64-query tile, chosen

@@ -1,5 +1,6 @@
-"""GPU parity of the tiled attention kernels beyond the MFMA path: fp64
-tensors and head dims above 256 (up to 1024).
+"""GPU parity of the tiled attention kernels beyond the MFMA path -- fp64
+tensors and head dims above 256 (up to 1024) -- and of the MFMA kernels at
+head dim 256.
 
 The reference takes any float dtype -- its kernels load with
 ``.to(tl.float32)`` and store in the input dtype (forward.py:103,155) -- and
@@ -166,9 +167,11 @@ def test_head_dim_above_1024_is_rejected(gpu):
         F.rational_attention_forward(q, q, q, torch.ones(1, device=dev), 1.0)
 
 
-# ------------------------------------------------ MFMA forward at D = 256 ----
-# The MFMA forward also covers D = 256 (8-wave blocks of 16-query waves); the
-# backward at D = 256 runs the tiled kernels. Bar: check_lowp on o (the
+# ------------------------------------------------------ MFMA at D = 256 ----
+# The MFMA kernels also cover D = 256: the forward in 8-wave blocks of
+# 16-query waves, the backward with 16 keys per dK/dV wave pair and 32 queries
+# per dQ wave (the backward's parity cases at D = 256 sit with the other head
+# dims in test_gpu_attention.py). Bar: check_lowp on o and the gradients (the
 # north-star 2e-2 max-abs + 1/2 ulp, relative L2 <= 5e-3), L within 1e-2.
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
@@ -220,18 +223,69 @@ def test_mfma_forward_d256_long_matches_tiled(gpu, monkeypatch):
     assert _rel(L_m, L_t) <= 1e-3
 
 
-def test_d256_training_step_mfma_forward_tiled_backward(gpu):
-    # fwd + bwd through autograd at D = 256: the forward on the MFMA kernel,
-    # the backward on the tiled kernels (which warns once); gradients against
-    # the oracle at the bf16 bar
+def test_d256_training_step_on_the_mfma_kernels(gpu, monkeypatch):
+    # fwd + bwd through autograd at D = 256, both on the MFMA kernels (no
+    # fallback warning); gradients against the oracle at the bf16 bar
+    import warnings
+    monkeypatch.setenv("KAT_ATTN_IMPL", "mfma")
     B, H, T, D = 1, 2, 200, 256
     q, k, v, do = _inputs(37, B, H, T, D, torch.bfloat16)
     slopes = F.compute_alibi_slopes(H)
     scale = 1.0 / math.sqrt(D)
-    with pytest.warns(RuntimeWarning, match="head dim 256"):
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
         o, _, dq, dk, dv = _run(q, k, v, do, slopes.to(dev), scale)
     ro, rL = O.attention_fwd(q, k, v, slopes, scale, dtype=torch.float32)
     check_lowp(o, ro, torch.bfloat16, "o")
     rq, rk, rv = O.attention_bwd(q, k, v, o, rL, do, slopes, scale, dtype=torch.float32)
     for name, got, ref in (("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
         check_lowp(got, ref, torch.bfloat16, name)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_mfma_backward_d256_masked(gpu, causal, monkeypatch):
+    # padding mask (a whole key tile and a whole 16-key half dropped), causal
+    # and not, against the oracle's masked backward
+    from fastalgebraictransformer_amd.backward import _attn_bwd_into
+    from fastalgebraictransformer_amd.forward import _attn_fwd_into, _key_mask_arg
+    monkeypatch.setenv("KAT_ATTN_IMPL", "mfma")
+    B, H, T, D = 2, 2, 333, 256
+    q, k, v, do = _inputs(61, B, H, T, D, torch.bfloat16)
+    slopes = F.compute_alibi_slopes(H)
+    scale = 1.0 / math.sqrt(D)
+    m = torch.ones(B, T, dtype=torch.int32)
+    m[0, 200:] = 0
+    m[1, 5::7] = 0
+    m[1, 64:128] = 0
+    m[1, 144:160] = 0
+    km = _key_mask_arg(m, B, T, dev)
+    o = torch.empty_like(q)
+    L = torch.empty(B, H, T, dtype=torch.float32, device=dev)
+    _attn_fwd_into(q, k, v, o, L, slopes.to(dev), scale, causal, 1e-6, km, extended=True)
+    g = [torch.full_like(q, float("nan")) for _ in range(3)]
+    _attn_bwd_into(q, k, v, o, L, do, *g, slopes.to(dev), scale, causal, 1e-6, km, extended=True)
+    torch.cuda.synchronize()
+    ro, _ = O.attention_fwd(q, k, v, slopes, scale, dtype=torch.float32, causal=causal, key_mask=m)
+    check_lowp(o, ro, torch.bfloat16, "o")
+    rg = O.attention_bwd(q, k, v, o, L, do, slopes, scale, dtype=torch.float32, causal=causal,
+                         key_mask=m)
+    for name, got, ref in zip(("dq", "dk", "dv"), g, rg):
+        check_lowp(got, ref, torch.bfloat16, name)
+
+
+def test_mfma_backward_d256_long_matches_tiled(gpu, monkeypatch):
+    # T = 4096: the MFMA backward against the fp32 tiled kernels on the same
+    # bf16 inputs (an independent implementation), at the bf16 bar
+    B, H, T, D = 1, 2, 4096, 256
+    q, k, v, do = _inputs(67, B, H, T, D, torch.bfloat16)
+    slopes = F.compute_alibi_slopes(8)[2:4].to(dev)
+    scale = 1.0 / math.sqrt(D)
+    monkeypatch.setenv("KAT_ATTN_IMPL", "mfma")
+    o, L = F.rational_attention_forward(q, k, v, slopes, scale)
+    g_m = F.rational_attention_backward(q, k, v, o, L, do, slopes, scale)
+    monkeypatch.setenv("KAT_ATTN_IMPL", "tiled")
+    f32 = [t.float() for t in (q, k, v, do)]
+    g_t = F.rational_attention_backward(f32[0], f32[1], f32[2], o.float(), L, f32[3], slopes, scale)
+    torch.cuda.synchronize()
+    for name, x, y in zip(("dq", "dk", "dv"), g_m, g_t):
+        check_lowp(x, y, torch.bfloat16, name)

@@ -222,6 +222,8 @@ def test_tiled_fallback_reasons_mirror_the_mfma_limits():
     contiguous = [((16 * T * D, T * D, D), 0)]
     assert _tiled_reason(contiguous, D, T, 2) is None
     assert "head dim 96" in _tiled_reason(contiguous, 96, T, 2)
+    assert _tiled_reason([((16 * T * 256, T * 256, 256), 0)], 256, T, 2) is None
+    assert "head dim 512" in _tiled_reason([((T * 512, T * 512, 512), 0)], 512, T, 2)
     assert "16-byte" in _tiled_reason([((T * D, T * D, D), 8)], D, T, 2)
     assert "16-byte" in _tiled_reason([((T * D, T * D, D + 1), 0)], D, T, 2)
     # the model's packed qkv [B, T, 3, H, D] (H = 16, D = 128): row stride 6144
