@@ -130,19 +130,21 @@ __global__ __launch_bounds__(64 * NW, NW == 4 && QS == 2 ? 2 : 1) void attn_fwd_
   const T* kp = (const T*)a.k + b * a.sk[0] + h * a.sk[1];
   const T* vp = (const T*)a.v + b * a.sv[0] + h * a.sv[1];
   const uint32_t sq2 = (uint32_t)a.sq[2], sk2 = (uint32_t)a.sk[2], sv2 = (uint32_t)a.sv[2];
-  const uint32_t kbytes = row_bytes(T_, sk2, D), vbytes = row_bytes(T_, sv2, D);
+  const int DR = a.D;  // the head dim (<= D; columns DR .. D - 1 read as zeros)
+  const uint32_t kbytes = row_bytes(T_, sk2, DR), vbytes = row_bytes(T_, sv2, DR);
   const float slope = a.slopes[h];
   const float scale = a.scale;
 
   // Q^T fragments (B operand): lane (g, li) holds Q[qw + 16 qs + li][32 kk + 8 g .. +7]
   i16x8 qf[QS][KK];
   {
-    const __amdgpu_buffer_rsrc_t rq = rsrc(qp, row_bytes(T_, sq2, D));
+    const __amdgpu_buffer_rsrc_t rq = rsrc(qp, row_bytes(T_, sq2, DR));
 #pragma unroll
     for (int qs = 0; qs < QS; ++qs)
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk)
-        qf[qs][kk] = load16(rq, ((uint32_t)(qw + 16 * qs + li) * sq2 + 32 * kk + 8 * g) * 2);
+        qf[qs][kk] = load16(rq, col_off(((uint32_t)(qw + 16 * qs + li) * sq2 + 32 * kk + 8 * g) * 2,
+                                        32 * kk + 8 * g, DR));
   }
   // element (qs, j) of a 16-key half starting at key kh: key = kh + 4 g + j,
   // q = qw + 16 qs + li; bias slope (key - q) = per-lane part + uniform part
@@ -169,8 +171,8 @@ __global__ __launch_bounds__(64 * NW, NW == 4 && QS == 2 ? 2 : 1) void attn_fwd_
   for (int qs = 0; qs < QS; ++qs) lsum[qs] = 0.f;
 
   TileDma<D, NW> dk, dv;
-  dk.init(w, lane, sk2);
-  dv.init(w, lane, sv2);
+  dk.init(w, lane, sk2, DR);
+  dv.init(w, lane, sv2, DR);
 
   // S^T of the 16 keys at tile rows hr .. hr + 15
   auto m1 = [&](int hr, f32x4 (&s_)[QS], const short* ks_) __attribute__((always_inline)) {
@@ -335,7 +337,7 @@ __global__ __launch_bounds__(64 * NW, NW == 4 && QS == 2 ? 2 : 1) void attn_fwd_
     }
   }
   __syncthreads();  // orders the tile's writes before its reads
-  epi_rows_out<T, D, RW>(et, lane, op, a.so[2], qw, T_);
+  epi_rows_out<T, D, RW>(et, lane, op, a.so[2], qw, T_, DR);
 }
 
 // Everything the backward's MFMA kernels take besides the inputs (the
@@ -386,6 +388,7 @@ __global__ __launch_bounds__(256) void attn_bwd_prep_k(AttnArgs a, BwdWs ws) {
   const int b = bh / a.H, h = bh - b * a.H;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int sub = tid % LPR, d = 8 * sub;
+  const bool din = d < a.D;  // columns past the head dim: zeros (the fp16 copy keeps D columns)
   const T* vp = (const T*)a.v + b * a.sv[0] + h * a.sv[1];
   const T* qp = (const T*)a.q + b * a.sq[0] + h * a.sq[1];
   const T* op = (const T*)a.o + b * a.so[0] + h * a.so[1];
@@ -398,7 +401,7 @@ __global__ __launch_bounds__(256) void attn_bwd_prep_k(AttnArgs a, BwdWs ws) {
     const int row = 64 * t + RPP * u + tid / LPR;
     qv[u] = i16x8{0, 0, 0, 0, 0, 0, 0, 0};
     float vs = 0.f, dsum = 0.f, dsq = 0.f;
-    if (row < a.T) {
+    if (row < a.T && din) {
       // every input row is read once here: non-temporal loads (streamed, not
       // kept in L2)
       qv[u] = ld_nt16(qp + (int64_t)row * a.sq[2] + d);
@@ -650,7 +653,8 @@ __global__ __launch_bounds__(64 * kDqW, 1) void attn_bwd_dq_k(AttnArgs a, const 
   const bool wact = qtw < nt;
   const T* kp = (const T*)a.k + b * a.sk[0] + h * a.sk[1];
   const uint32_t sk2 = (uint32_t)a.sk[2];
-  const uint32_t kbytes = row_bytes(T_, sk2, D);
+  const int DR = a.D;  // the head dim (<= D; columns DR .. D - 1 read as zeros, not stored)
+  const uint32_t kbytes = row_bytes(T_, sk2, DR);
   const f16* run = dst + ((int64_t)bl * ds_tiles_per_band(nt, kCausal, kb0, nk) +
                            ds_run_base(q0 / (kQB * 64), kCausal, kb0, nk)) * 4096;
   const int ng = (T_ + 31) / 32;  // 32-key groups (exponents)
@@ -670,7 +674,7 @@ __global__ __launch_bounds__(64 * kDqW, 1) void attn_bwd_dq_k(AttnArgs a, const 
 
   KDma dk;
   SDma dd;  // the wave's own dS rows
-  dk.init(kw_ ? w : 0, lane, sk2);
+  dk.init(kw_ ? w : 0, lane, sk2, DR);
   // LDS slot (row, p) of the swizzled [32][QW] stage tile takes data chunk
   // c = p ^ swz(row) of key row `row`, which the stored layout keeps in 1 KB
   // block 2 (c / 4) + row / 16 at position 16 (c % 4) + row % 16 (QW = 32:
@@ -804,7 +808,7 @@ __global__ __launch_bounds__(64 * kDqW, 1) void attn_bwd_dq_k(AttnArgs a, const 
     }
   }
   __syncthreads();  // orders the tile's writes before its reads
-  epi_rows_out<T, D, QW>(et, lane, dqp, a.sdq[2], 64 * qtw + QW * qh, T_);
+  epi_rows_out<T, D, QW>(et, lane, dqp, a.sdq[2], 64 * qtw + QW * qh, T_, DR);
 }
 
 // ============================================================================
@@ -879,7 +883,8 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
   const T* dop = (const T*)a.dout + b * a.sdo[0] + h * a.sdo[1];
   const float* stp = stats + (int64_t)bh * ((T_ + 63) / 64) * 128;
   const uint32_t sk2 = (uint32_t)a.sk[2], sv2 = (uint32_t)a.sv[2], sdo2 = (uint32_t)a.sdo[2];
-  const uint32_t qbytes = row_bytes(T_, D, D), obytes = row_bytes(T_, sdo2, D);
+  const int DR = a.D;  // the head dim (<= D; columns DR .. D - 1 read as zeros, not stored)
+  const uint32_t qbytes = row_bytes(T_, D, D), obytes = row_bytes(T_, sdo2, DR);
   const uint32_t stbytes = (uint32_t)((T_ + 63) / 64) * 512u;
   const float slope = a.slopes[h];
   const float scale = a.scale;
@@ -907,19 +912,20 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
   i16x8 bfr[KS][KK];
   int ekw = 0;
   {
-    const __amdgpu_buffer_rsrc_t rk = rsrc(kp, row_bytes(T_, sk2, D));
-    const __amdgpu_buffer_rsrc_t rv = rsrc(vp, row_bytes(T_, sv2, D));
+    const __amdgpu_buffer_rsrc_t rk = rsrc(kp, row_bytes(T_, sk2, DR));
+    const __amdgpu_buffer_rsrc_t rv = rsrc(vp, row_bytes(T_, sv2, DR));
     float km = 0.f;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const uint32_t key = (uint32_t)(kw + 16 * ks + li);
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk) {
+        const int col = 32 * kk + 8 * g;
         if (prole) {
-          bfr[ks][kk] = load16(rk, (key * sk2 + 32 * kk + 8 * g) * 2);
+          bfr[ks][kk] = load16(rk, col_off((key * sk2 + col) * 2, col, DR));
           km = fmaxf(km, absmax8<T>(bfr[ks][kk]));
         } else {
-          bfr[ks][kk] = load16(rv, (key * sv2 + 32 * kk + 8 * g) * 2);
+          bfr[ks][kk] = load16(rv, col_off((key * sv2 + col) * 2, col, DR));
         }
       }
     }
@@ -990,7 +996,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
   // in flight inside the loop and never wait for their dS stores
   TileDma<D, kNW> dq_, do_;
   dq_.init(w, lane, D);
-  do_.init(w, lane, sdo2);
+  do_.init(w, lane, sdo2, DR);
   // stats of a 64-query tile: 512 bytes, lanes 0..31 of wave 0
   const uint32_t st_off = (uint32_t)lane * 16u;
   auto issue = [&](int buf, int qrow0) __attribute__((always_inline)) {
@@ -1257,14 +1263,17 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
     }
   }
   __syncthreads();  // orders the tile's writes before its reads
-  epi_rows_out<T, D, KR>(et, lane, outp, ostr, kw, T_);
+  epi_rows_out<T, D, KR>(et, lane, outp, ostr, kw, T_, DR);
 }
 
 // ============================================================================
 // Launchers
 // ============================================================================
-bool attn_mfma_supported(int D) { return D == 32 || D == 64 || D == 128 || D == 256; }
+// head dims that are multiples of 8 up to 256 run in the kernels of the next
+// layout width (32, 64, 128 or 256 columns), the columns past D as zeros
+bool attn_mfma_supported(int D) { return D >= 8 && D <= 256 && D % 8 == 0; }
 bool attn_mfma_fwd_supported(int D) { return attn_mfma_supported(D); }
+static int layout_dim(int64_t D) { return D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : 256; }
 
 // Backward workspace (each part 256-byte aligned): per-row stats (per 64-row
 // tile two float[64]: 4 cinv, then -4 cinv Delta), the
@@ -1338,7 +1347,7 @@ static BwdWs bwd_ws(void* base, int64_t B, int64_t H, int64_t T, int64_t D, bool
 }
 
 size_t attn_mfma_workspace(int64_t B, int64_t H, int64_t T, int64_t D, bool causal) {
-  return bwd_ws(nullptr, B, H, T, D, causal).bytes;
+  return bwd_ws(nullptr, B, H, T, layout_dim(D), causal).bytes;
 }
 
 namespace {
@@ -1351,7 +1360,7 @@ bool offsets_ok(const AttnArgs& a, bool bwd) {
   const int64_t* s2[5] = {&a.sq[2], &a.sk[2], &a.sv[2], &a.sdo[2], &a.so[2]};
   for (int t = 0; t < (bwd ? 5 : 3); ++t)
     if (*s2[t] < a.D || ((int64_t)a.T + std::max(kBM, kFwdBM)) * *s2[t] * 2 > lim) return false;
-  return (int64_t)a.T * a.D * 2 < lim && (int64_t)a.T * 8 < lim;
+  return (int64_t)a.T * layout_dim(a.D) * 2 < lim && (int64_t)a.T * 8 < lim;
 }
 
 template <typename T, int D, int MODE> int launch_fwd(const AttnArgs& a, hipStream_t st) {
@@ -1364,7 +1373,7 @@ template <typename T, int D, int MODE> int launch_fwd(const AttnArgs& a, hipStre
 template <typename T, int D, int MODE>
 int launch_bwd(const AttnArgs& a, void* ws, hipStream_t st) {
   constexpr bool kCausal = (MODE & kModeCausal) != 0;
-  const BwdWs w = bwd_ws(ws, a.B, a.H, a.T, a.D, kCausal);
+  const BwdWs w = bwd_ws(ws, a.B, a.H, a.T, D, kCausal);
   const int BH = a.B * a.H;
   const int64_t tiles = (int64_t)BH * ((a.T + 63) / 64);
   // prep: fp16 copies, exponents, Delta and the row stats, the dS bound parts
@@ -1410,19 +1419,23 @@ int launch_bwd(const AttnArgs& a, void* ws, hipStream_t st) {
 template <typename T> int attn_fwd_mfma(const AttnArgs& a, hipStream_t st) {
   if ((int64_t)((a.T + kFwdBM - 1) / kFwdBM) * a.B * a.H > 0x7fffffffLL || !offsets_ok(a, false))
     return KAT_EUNSUPPORTED;
-  if (a.D == 256) KAT_MODE_SWITCH(a, return (launch_fwd<T, 256, MODE>(a, st)));
-  if (a.D == 128) KAT_MODE_SWITCH(a, return (launch_fwd<T, 128, MODE>(a, st)));
-  if (a.D == 64) KAT_MODE_SWITCH(a, return (launch_fwd<T, 64, MODE>(a, st)));
-  if (a.D == 32) KAT_MODE_SWITCH(a, return (launch_fwd<T, 32, MODE>(a, st)));
+  if (!attn_mfma_supported(a.D)) return KAT_EUNSUPPORTED;
+  const int D = layout_dim(a.D);
+  if (D == 256) KAT_MODE_SWITCH(a, return (launch_fwd<T, 256, MODE>(a, st)));
+  if (D == 128) KAT_MODE_SWITCH(a, return (launch_fwd<T, 128, MODE>(a, st)));
+  if (D == 64) KAT_MODE_SWITCH(a, return (launch_fwd<T, 64, MODE>(a, st)));
+  if (D == 32) KAT_MODE_SWITCH(a, return (launch_fwd<T, 32, MODE>(a, st)));
   return KAT_EUNSUPPORTED;
 }
 
 template <typename T> int attn_bwd_mfma(const AttnArgs& a, void* ws, hipStream_t st) {
   if ((int64_t)((a.T + 63) / 64) * a.B * a.H > 0x7fffffffLL || !offsets_ok(a, true)) return KAT_EUNSUPPORTED;
-  if (a.D == 256) KAT_MODE_SWITCH(a, return (launch_bwd<T, 256, MODE>(a, ws, st)));
-  if (a.D == 128) KAT_MODE_SWITCH(a, return (launch_bwd<T, 128, MODE>(a, ws, st)));
-  if (a.D == 64) KAT_MODE_SWITCH(a, return (launch_bwd<T, 64, MODE>(a, ws, st)));
-  if (a.D == 32) KAT_MODE_SWITCH(a, return (launch_bwd<T, 32, MODE>(a, ws, st)));
+  if (!attn_mfma_supported(a.D)) return KAT_EUNSUPPORTED;
+  const int D = layout_dim(a.D);
+  if (D == 256) KAT_MODE_SWITCH(a, return (launch_bwd<T, 256, MODE>(a, ws, st)));
+  if (D == 128) KAT_MODE_SWITCH(a, return (launch_bwd<T, 128, MODE>(a, ws, st)));
+  if (D == 64) KAT_MODE_SWITCH(a, return (launch_bwd<T, 64, MODE>(a, ws, st)));
+  if (D == 32) KAT_MODE_SWITCH(a, return (launch_bwd<T, 32, MODE>(a, ws, st)));
   return KAT_EUNSUPPORTED;
 }
 

@@ -136,6 +136,12 @@ __device__ __forceinline__ i16x8 pack_frag(uint32_t a, uint32_t b, uint32_t c, u
 // end without branches.
 // ---------------------------------------------------------------------------
 constexpr int kRsrcWord3 = 0x00020000;  // gfx9 raw buffer: 32-bit data format
+// A buffer offset at or past every resource's num_records (the kernels keep
+// extents below 2^31): the load returns zeros. The columns a tile or fragment
+// holds beyond the head dim of a call (kernels built for a wider layout, e.g.
+// D = 96 in the D = 128 kernels) take it, so they read as zeros.
+constexpr uint32_t kOobOff = 0x80000000u;
+__device__ __forceinline__ uint32_t col_off(uint32_t off, int col, int cols) { return col < cols ? off : kOobOff; }
 
 // resource for kernel-side loads through the compiler builtin
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, uint32_t bytes) {
@@ -244,12 +250,13 @@ template <int D, int NW, int ROWS = 64> struct TileDma {
   static constexpr int SEGS = ROWS / RPS / NW;  // segments per wave
   static_assert(SEGS >= 1 && SEGS * RPS * NW == ROWS, "tile rows must split evenly over the waves");
   uint32_t off[SEGS];
-  __device__ __forceinline__ void init(int w, int lane, uint32_t stride) {
+  // cols: the matrix's columns (<= D); chunks past them load zeros
+  __device__ __forceinline__ void init(int w, int lane, uint32_t stride, int cols = D) {
 #pragma unroll
     for (int u = 0; u < SEGS; ++u) {
       const int row = (w * SEGS + u) * RPS + lane / CPR;
       const int c = (lane % CPR) ^ swz<D>(row);
-      off[u] = (row * stride + 8 * c) * 2;
+      off[u] = col_off((row * stride + 8 * c) * 2, 8 * c, cols);
     }
   }
   // base: first row of the matrix; bytes: its extent; row0: first tile row
@@ -296,7 +303,7 @@ __device__ __forceinline__ void epi_put(short* tile, int off, uint32_t lo, uint3
   *reinterpret_cast<u32x2*>(tile + off) = u32x2{lo, hi};
 }
 // rows 0 .. R - 1 of the tile to base[(row0 + r) * stride], rows with
-// row0 + r >= nrows skipped; the tile must be complete (written by this wave,
+// row0 + r >= nrows and columns at or past cols skipped; the tile must be complete (written by this wave,
 // with a barrier or an LDS wait in between). Non-temporal stores: the outputs
 // are not re-read by the kernel that writes them, and write-back stores left
 // their lines in L2 where the still-running blocks keep their K / V, Q16 / dO
@@ -304,17 +311,19 @@ __device__ __forceinline__ void epi_put(short* tile, int off, uint32_t lo, uint3
 // shape, forward 0.5%).
 template <typename T, int D, int R>
 __device__ __forceinline__ void epi_rows_out(const short* tile, int lane, T* __restrict__ base, int64_t stride,
-                                             int row0, int nrows) {
+                                             int row0, int nrows, int cols = D) {
   constexpr int CPR = D / 8, RPI = 64 / CPR;  // chunks per row, rows per instruction
 #pragma unroll
   for (int i = 0; i < R / RPI; ++i) {
     const int r = i * RPI + lane / CPR, c = lane % CPR;
     const i16x8 v = *reinterpret_cast<const i16x8*>(tile + eoff<D>(r, 8 * c));
-    if (row0 + r < nrows) __builtin_nontemporal_store(v, reinterpret_cast<i16x8*>(base + (int64_t)(row0 + r) * stride + 8 * c));
+    if (row0 + r < nrows && 8 * c < cols)
+      __builtin_nontemporal_store(v, reinterpret_cast<i16x8*>(base + (int64_t)(row0 + r) * stride + 8 * c));
   }
 }
 
-// extent in bytes of T rows of D 16-bit elements at a row stride (elements)
+// extent in bytes of T rows of D 16-bit elements at a row stride (elements);
+// D: the matrix's own columns
 __device__ __forceinline__ uint32_t row_bytes(int T, uint32_t stride, int D) {
   return ((uint32_t)(T - 1) * stride + (uint32_t)D) * 2u;
 }

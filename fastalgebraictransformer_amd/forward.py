@@ -52,8 +52,11 @@ _MFMA_OFFSET_LIMIT = 0x7FFFFFFF
 _MFMA_ROW_PAD = 128
 
 
-# head dims the MFMA kernels cover (forward and backward)
-MFMA_DIMS = (32, 64, 128, 256)
+def _mfma_head_dim(D):
+    """Head dims the MFMA kernels cover (forward and backward): multiples of 8
+    up to 256 (run in the kernels of the next layout width, 32, 64, 128 or
+    256 columns, with the columns past D read as zeros)."""
+    return 8 <= D <= 256 and D % 8 == 0
 
 
 def _tiled_reason(shapes_strides_ptrs, D, T, elem):
@@ -61,9 +64,8 @@ def _tiled_reason(shapes_strides_ptrs, D, T, elem):
     tiled ones (None if it takes them), from each operand's (b, h, t) strides
     and data pointer: the head dim, 16-byte row alignment, and the 31-bit byte
     offsets the MFMA kernels use within one (b, h) slice."""
-    if D not in MFMA_DIMS:
-        return (f"head dim {D} (the MFMA kernels cover "
-                f"{', '.join(str(d) for d in MFMA_DIMS[:-1])} and {MFMA_DIMS[-1]})")
+    if not _mfma_head_dim(D):
+        return f"head dim {D} (the MFMA kernels cover multiples of 8 up to 256)"
     for strides, ptr in shapes_strides_ptrs:
         if ptr % 16 or any((st * elem) % 16 for st in strides):
             return "rows not 16-byte aligned (a view with an odd offset or stride)"
@@ -78,8 +80,8 @@ def _tiled_reason(shapes_strides_ptrs, D, T, elem):
 
 
 def _warn_if_tiled(tensors, D, dtype, mfma_inputs=None):
-    """bf16 / fp16 attention runs on the MFMA kernels when the head dim is 32,
-    64, 128 or 256, every [B, H, T, D] operand has 16-byte aligned rows and the
+    """bf16 / fp16 attention runs on the MFMA kernels when the head dim is a
+    multiple of 8 up to 256, every [B, H, T, D] operand has 16-byte aligned rows and the
     inputs the kernels address by 31-bit offsets (q, k, v; and O, dO in the
     backward: ``mfma_inputs``) keep each (b, h) slice below 2^31 bytes;
     otherwise libkat falls back to the tiled kernels, which are correct but

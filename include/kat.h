@@ -150,7 +150,9 @@ int kat_add_men_bwd(const void* dy, const void* dh, const void* h, const void* w
  * l_strides: 3 int64 = (b, h, t) strides of L. slopes: fp32 [H].
  * Replaces the host wrapper + rational_attention_fwd_kernel[(B,H,T)] launch at
  * forward.py:267-319 (kernel forward.py:49-159). dtype KAT_BF16/KAT_F16 use
- * the MFMA kernels (D in {32, 64, 128, 256}, 16-byte aligned rows); KAT_F32,
+ * the MFMA kernels (D a multiple of 8 up to 256, 16-byte aligned rows; a D
+ * between the layout widths 32, 64, 128 and 256 runs in the kernels of the
+ * next width, the columns past D read as zeros and not stored); KAT_F32,
  * KAT_F64 and other D (<= 1024; larger D returns KAT_EUNSUPPORTED) use the
  * tiled kernels, in fp32 arithmetic (fp64 for KAT_F64; the reference computes
  * in fp32 for every dtype, forward.py:103, and stores in the input dtype,
@@ -183,7 +185,7 @@ size_t kat_attn_bwd_workspace_size(int64_t B, int64_t H, int64_t T, int64_t D, i
  * Replaces the host wrapper + the dq and dkv launches at backward.py:273-341
  * (kernels backward.py:62-158 and 165-266). Deterministic. The MFMA and tiled
  * paths split the calls as kat_attn_fwd's (MFMA: KAT_BF16 / KAT_F16, D in
- * {32, 64, 128, 256}, 16-byte aligned rows). On the MFMA path
+ * a multiple of 8 up to 256, 16-byte aligned rows). On the MFMA path
  * dS is computed once (by the dK/dV kernel, which stores it for dQ), and it
  * and the copies of Q and K its products take enter the MFMA in fp16, each
  * with a power-of-two scale chosen from the data (per 64-row tile for Q, per

@@ -123,9 +123,10 @@ def _check_lowp(o, L, dq, dk, dv, q, k, v, do, slopes, scale, sel=None, chunk=No
 
 
 def _pin_mfma(monkeypatch, D):
-    # bf16 / fp16 calls whose head dim the MFMA kernels cover must run on them:
-    # with KAT_ATTN_IMPL=mfma a fallback to the tiled kernels is an error
-    if D in (32, 64, 128, 256):
+    # bf16 / fp16 calls whose head dim the MFMA kernels cover (multiples of 8
+    # up to 256) must run on them: with KAT_ATTN_IMPL=mfma a fallback to the
+    # tiled kernels is an error
+    if D % 8 == 0 and D <= 256:
         monkeypatch.setenv("KAT_ATTN_IMPL", "mfma")
 
 
@@ -143,7 +144,9 @@ def test_golden_bf16(gpu, name, monkeypatch):
 @pytest.mark.parametrize("B,H,T,D", [(1, 2, 64, 64), (1, 3, 200, 128), (2, 2, 333, 64),
                                      (1, 2, 257, 32), (2, 3, 1000, 32), (1, 1, 1, 32),
                                      (1, 1, 1, 128), (1, 2, 1000, 128), (1, 2, 200, 256),
-                                     (2, 2, 333, 256), (1, 1, 1, 256), (1, 2, 1000, 256)])
+                                     (2, 2, 333, 256), (1, 1, 1, 256), (1, 2, 1000, 256),
+                                     (1, 3, 200, 96), (2, 2, 333, 80), (1, 2, 300, 48),
+                                     (1, 2, 257, 192), (1, 1, 1, 96)])
 def test_lowp_shapes(gpu, dtype, B, H, T, D, monkeypatch):
     _pin_mfma(monkeypatch, D)
     q, k, v, do = _inputs(7 * T + D, B, H, T, D, dtype)
@@ -281,7 +284,7 @@ def _scaled_check(q, k, v, do, slopes, scale, factors):
         assert excess <= 0, (name, float(err.max()), excess)
 
 
-@pytest.mark.parametrize("D", [32, 64, 128, 256])
+@pytest.mark.parametrize("D", [32, 64, 80, 128, 256])
 @pytest.mark.parametrize("case", ["v1e4", "do1e-6", "q1e5_k1e-5", "qk1e-4", "combined", "v1e3_do1e2"])
 def test_mfma_backward_input_range_bf16(gpu, D, case, monkeypatch):
     _pin_mfma(monkeypatch, D)
@@ -356,7 +359,7 @@ def test_mfma_backward_input_range_fp16(gpu, D, monkeypatch):
                   {"o": fv, "dq": fv * fd * fk, "dk": fv * fd * fq, "dv": fd})
 
 
-@pytest.mark.parametrize("D", [32, 64, 128, 256])
+@pytest.mark.parametrize("D", [32, 64, 96, 128, 256])
 def test_mfma_attention_is_exactly_equivariant_to_power_of_two_scales(gpu, D, monkeypatch):
     # inputs on a grid of 1/16 are exact in fp16 at every scale used below, so
     # the fp16 copies hold the same significands whatever their exponent: then
@@ -378,14 +381,15 @@ def test_mfma_attention_is_exactly_equivariant_to_power_of_two_scales(gpu, D, mo
 
 
 def test_tiled_fallback_warns_once(gpu):
-    # a bf16 call outside the MFMA kernels' envelope (here D = 48) runs the
-    # fp32 tiled kernels; the wrapper says so, once per reason
+    # a bf16 call outside the MFMA kernels' envelope (here D = 100, not a
+    # multiple of 8) runs the fp32 tiled kernels; the wrapper says so, once
+    # per reason
     import warnings
     from fastalgebraictransformer_amd import forward as fw
     fw._WARNED.clear()
-    q, k, v, _ = _inputs(5, 1, 2, 40, 48, torch.bfloat16)
+    q, k, v, _ = _inputs(5, 1, 2, 40, 100, torch.bfloat16)
     slopes = F.compute_alibi_slopes(2).to(dev)
-    with pytest.warns(RuntimeWarning, match="head dim 48"):
+    with pytest.warns(RuntimeWarning, match="head dim 100"):
         F.rational_attention_forward(q, k, v, slopes, 0.17)
     with warnings.catch_warnings():
         warnings.simplefilter("error")

@@ -18,7 +18,8 @@ def _randn(shape, dtype, seed):
     return torch.randn(*shape, generator=g).to(dtype).cuda()
 
 
-@pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 128), (torch.float16, 64), (torch.float32, 64)])
+@pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 128), (torch.float16, 64), (torch.float32, 64),
+                                     (torch.bfloat16, 96), (torch.float16, 40)])
 @pytest.mark.parametrize("T", [1, 300])
 def test_packed_attention_matches_views(gpu, dtype, D, T):
     B, H = 2, 3
@@ -68,7 +69,7 @@ def test_packed_swiglu_matches_chunks(gpu, dtype, rows, f):
 # elementwise, relative L2 <= 5e-3).
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("D", [64, 128, 96])
 @pytest.mark.parametrize("masked", [False, True])
 def test_packed_attention_vs_oracle(gpu, dtype, D, masked, monkeypatch):
     import oracle as O

@@ -1,10 +1,13 @@
 """A seeded random sweep of attention shapes against the oracle: sequence
 lengths that are not multiples of the kernels' tiles, head dims 32 / 64 / 128
 (bf16 / fp16 on the MFMA kernels, fp32 on the tiled kernels), 1 to 16
-heads, bf16 / fp16 / fp32, causal or with a padding mask or non-causal. The
-draw is fixed (seed below), so a failure names a reproducible case. Bars as
-in test_gpu_attention.py: fp32 <= 1e-5 of max|ref|; bf16 / fp16
-2e-2 + 1/2 ulp elementwise and relative L2 <= 5e-3."""
+heads, bf16 / fp16 / fp32, causal or with a padding mask or non-causal; and a
+second sweep over head dims between the layout widths (multiples of 8 up to
+256, which the MFMA kernels of the next width run with the columns past D
+read as zeros and not stored). The draws are fixed (seeds below), so a
+failure names a reproducible case. Bars as in test_gpu_attention.py: fp32 <=
+1e-5 of max|ref|; bf16 / fp16 2e-2 + 1/2 ulp elementwise and relative L2 <=
+5e-3."""
 
 import math
 import random
@@ -20,12 +23,12 @@ pytestmark = pytest.mark.gpu
 dev = "cuda"
 
 
-def _draw(n, seed=2024):
+def _draw(n, seed=2024, dims=(32, 64, 128), dtypes=("bf16", "bf16", "fp16", "fp32")):
     rnd = random.Random(seed)
     cases = []
     for i in range(n):
-        dtype = rnd.choice(["bf16", "bf16", "fp16", "fp32"])
-        D = rnd.choice([32, 64, 128])
+        dtype = rnd.choice(dtypes)
+        D = rnd.choice(dims)
         H = rnd.choice([1, 3, 12, 16])
         B = rnd.choice([1, 2])
         T = rnd.randrange(1, 600)
@@ -36,6 +39,20 @@ def _draw(n, seed=2024):
 
 @pytest.mark.parametrize("i,dtype,B,H,T,D,mode", _draw(24))
 def test_random_shape(gpu, i, dtype, B, H, T, D, mode):
+    _check_case(i, dtype, B, H, T, D, mode)
+
+
+_PADDED_DIMS = (8, 16, 24, 40, 48, 56, 72, 80, 96, 104, 112, 120, 136, 160, 192, 200, 224, 248)
+
+
+@pytest.mark.parametrize("i,dtype,B,H,T,D,mode",
+                         _draw(20, seed=77, dims=_PADDED_DIMS, dtypes=("bf16", "fp16")))
+def test_random_shape_padded_head_dim(gpu, i, dtype, B, H, T, D, mode, monkeypatch):
+    monkeypatch.setenv("KAT_ATTN_IMPL", "mfma")  # a fallback to the tiled kernels is an error
+    _check_case(100 + i, dtype, B, H, T, D, mode)
+
+
+def _check_case(i, dtype, B, H, T, D, mode):
     dt = {"bf16": torch.bfloat16, "fp16": torch.float16, "fp32": torch.float32}[dtype]
     g = torch.Generator().manual_seed(1000 + i)
     q, k, v, do = (torch.randn(B, H, T, D, generator=g).to(dt).to(dev) for _ in range(4))

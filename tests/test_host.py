@@ -221,9 +221,10 @@ def test_tiled_fallback_reasons_mirror_the_mfma_limits():
     T, D = 4096, 128
     contiguous = [((16 * T * D, T * D, D), 0)]
     assert _tiled_reason(contiguous, D, T, 2) is None
-    assert "head dim 96" in _tiled_reason(contiguous, 96, T, 2)
-    assert _tiled_reason([((16 * T * 256, T * 256, 256), 0)], 256, T, 2) is None
-    assert "head dim 512" in _tiled_reason([((T * 512, T * 512, 512), 0)], 512, T, 2)
+    for Dm in (8, 48, 80, 96, 256):  # multiples of 8 up to 256
+        assert _tiled_reason([((16 * T * Dm, T * Dm, Dm), 0)], Dm, T, 2) is None, Dm
+    for Dt in (4, 100, 264, 512):
+        assert f"head dim {Dt}" in _tiled_reason([((T * 512, T * 512, 512), 0)], Dt, T, 2), Dt
     assert "16-byte" in _tiled_reason([((T * D, T * D, D), 8)], D, T, 2)
     assert "16-byte" in _tiled_reason([((T * D, T * D, D + 1), 0)], D, T, 2)
     # the model's packed qkv [B, T, 3, H, D] (H = 16, D = 128): row stride 6144
