@@ -61,7 +61,11 @@ __device__ __forceinline__ VecT<T, EPL> ld_row_nt(const T* p) {
   return __builtin_bit_cast(VecT<T, EPL>, __builtin_nontemporal_load(reinterpret_cast<const i32x4_t*>(p)));
 }
 
-// partials: part[(bh * splits + split) * (D + 1) + d] = sum_j f_j v_j[d], [.. + D] = sum_j f_j
+// partials: part[(bh * splits + split) * (D + 1) + d] = sum_j f_j v_j[d], [.. + D] = sum_j f_j.
+// D is the layout width; a head dim a.D below it leaves the lanes past a.D
+// with a zero query (so they add nothing to the scores) and their columns'
+// partials unused (the combine stores a.D columns). Those lanes read the
+// row's first columns, so that no load leaves the row.
 template <typename T, int D>
 __global__ __launch_bounds__(kDecThreads) void attn_decode_part_k(DecodeArgs a, float* __restrict__ part) {
   typedef DecShape<T, D> S;
@@ -78,12 +82,14 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_part_k(DecodeArgs a, 
   const float ipos = (float)(n - 1);  // the query's position
   const float slope = a.slopes[h];
 
+  const bool din = sub * EPL < a.D;
+  const int col0 = din ? sub * EPL : 0;
   float qv[EPL];
-  load_acc<T, EPL>((const T*)a.q + b * a.sq[0] + h * a.sq[1] + sub * EPL, qv);
+  load_acc<T, EPL>((const T*)a.q + b * a.sq[0] + h * a.sq[1] + col0, qv);
 #pragma unroll
-  for (int e = 0; e < EPL; ++e) qv[e] *= a.scale;
-  const T* kp = (const T*)a.k + b * a.sk[0] + h * a.sk[1] + sub * EPL;
-  const T* vp = (const T*)a.v + b * a.sv[0] + h * a.sv[1] + sub * EPL;
+  for (int e = 0; e < EPL; ++e) qv[e] = din ? qv[e] * a.scale : 0.f;
+  const T* kp = (const T*)a.k + b * a.sk[0] + h * a.sk[1] + col0;
+  const T* vp = (const T*)a.v + b * a.sv[0] + h * a.sv[1] + col0;
 
   float acc[EPL];
 #pragma unroll
@@ -178,7 +184,7 @@ __global__ __launch_bounds__(kDecCombThreads) void attn_decode_combine_k(DecodeA
 #pragma unroll
   for (int k = 0; k < (D + kDecCombThreads) / kDecCombThreads; ++k) {
     const int col = (int)threadIdx.x + k * kDecCombThreads;
-    if (col < D) o[col] = from_acc<T>(t[k] * inv);
+    if (col < a.D) o[col] = from_acc<T>(t[k] * inv);
   }
 }
 
@@ -198,15 +204,21 @@ static void decode_split(int64_t B, int64_t H, int64_t T, int rpp, int& splits, 
   chunk = (int)c;
 }
 
-static int decode_rpp(int D, int dtype) {
-  const int epl = 16 / dtype_size(dtype);
-  return (64 / (D / epl)) * kDecWaves;
+// the kernels' layout width for a head dim: 64, 128 or 256 (16-bit types; any
+// multiple of 8 up to 256) or 32, 64 or 128 (fp32; multiples of 4 up to 128);
+// 0 if none serves
+static int decode_layout(int64_t D, int dtype) {
+  if (dtype == KAT_F32) return D < 4 || D > 128 || D % 4 ? 0 : D <= 32 ? 32 : D <= 64 ? 64 : 128;
+  if (dtype == KAT_BF16 || dtype == KAT_F16) return D < 8 || D > 256 || D % 8 ? 0 : D <= 64 ? 64 : D <= 128 ? 128 : 256;
+  return 0;
 }
 
-static bool decode_supported(int64_t D, int dtype) {
-  if (dtype != KAT_F32 && dtype != KAT_BF16 && dtype != KAT_F16) return false;
-  return D == 64 || D == 128 || (D == 256 && dtype != KAT_F32) || (D == 32 && dtype == KAT_F32);
+static int decode_rpp(int D, int dtype) {
+  const int epl = 16 / dtype_size(dtype);
+  return (64 / (decode_layout(D, dtype) / epl)) * kDecWaves;
 }
+
+static bool decode_supported(int64_t D, int dtype) { return decode_layout(D, dtype) != 0; }
 
 template <typename T, int D> static int launch_decode(const DecodeArgs& a, float* part, hipStream_t st) {
   hipLaunchKernelGGL((attn_decode_part_k<T, D>), dim3((unsigned)a.splits, (unsigned)(a.B * a.H)),
@@ -218,7 +230,7 @@ template <typename T, int D> static int launch_decode(const DecodeArgs& a, float
 }
 
 template <typename T> static int decode_d(const DecodeArgs& a, float* part, hipStream_t st) {
-  switch (a.D) {
+  switch (decode_layout(a.D, sizeof(T) == 4 ? KAT_F32 : KAT_BF16)) {
     case 32: if constexpr (sizeof(T) == 4) return launch_decode<T, 32>(a, part, st); break;
     case 64: return launch_decode<T, 64>(a, part, st);
     case 128: return launch_decode<T, 128>(a, part, st);
@@ -236,7 +248,7 @@ extern "C" size_t kat_attn_decode_workspace_size(int64_t B, int64_t H, int64_t T
   if (B <= 0 || H <= 0 || T <= 0 || !decode_supported(D, dtype)) return 0;
   int splits, chunk;
   decode_split(B, H, T, decode_rpp((int)D, dtype), splits, chunk);
-  return (size_t)(B * H) * (size_t)splits * (size_t)(D + 1) * sizeof(float);
+  return (size_t)(B * H) * (size_t)splits * (size_t)(decode_layout(D, dtype) + 1) * sizeof(float);
 }
 
 // Argument checks and launch shared by kat_attn_decode and
@@ -282,7 +294,7 @@ static int decode_impl(const char* nm, const void* q, const void* k, const void*
   a.scale = scale;
   a.eps = eps;
   decode_split(B, H, std::max<int64_t>(T, 1), decode_rpp((int)D, dtype), a.splits, a.chunk);
-  const size_t need = (size_t)(B * H) * (size_t)a.splits * (size_t)(D + 1) * sizeof(float);
+  const size_t need = (size_t)(B * H) * (size_t)a.splits * (size_t)(decode_layout(D, dtype) + 1) * sizeof(float);
   int rc = KAT_OK;
   float* part = get_part(need, rc);
   if (!part) return rc;  // get_part recorded the message

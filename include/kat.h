@@ -244,10 +244,10 @@ int kat_attn_bwd_masked(const void* q, const void* k, const void* v, const void*
  * q, out: [B, H, D] with (b, h) strides; k, v: [B, H, T, D] caches with
  * (b, h, t) strides (any layout, e.g. token-major [B, T, H, D]); unit
  * d-stride and 16-byte aligned rows. strides: 10 int64 = q (b, h), k (b, h, t),
- * v (b, h, t), out (b, h). L: [B*H] fp32 or NULL. dtype KAT_F32 (D in
- * {32, 64, 128}), KAT_BF16 / KAT_F16 (D in {64, 128, 256}). Keys are split
- * into chunks across work-groups and the partial sums added in a fixed order
- * (deterministic); the workspace holds the partials. */
+ * v (b, h, t), out (b, h). L: [B*H] fp32 or NULL. dtype KAT_F32 (D a
+ * multiple of 4 up to 128), KAT_BF16 / KAT_F16 (D a multiple of 8 up to 256).
+ * Keys are split into chunks across work-groups and the partial sums added in
+ * a fixed order (deterministic); the workspace holds the partials. */
 size_t kat_attn_decode_workspace_size(int64_t B, int64_t H, int64_t T, int64_t D, int dtype);
 int kat_attn_decode(const void* q, const void* k, const void* v, void* out, float* L,
                     const float* slopes, const int32_t* lengths, void* workspace,

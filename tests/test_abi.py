@@ -53,6 +53,14 @@ def test_workspace_sizes():
     assert lib.kat_attn_bwd_workspace_size(4, 16, 4096, 64, 2) >= rows * 8 + rows * 64 * 2 + 64 * tiles * 8192
     assert lib.kat_attn_bwd_workspace_size(4, 16, 4096, 128, 0) < rows * 16
     assert lib.kat_attn_bwd_workspace_size(0, 16, 4096, 128, 1) == 0
+    # decode partials: B*H*splits rows of (layout width + 1) floats; a head
+    # dim between the widths takes its width's layout, others are unsupported
+    assert lib.kat_attn_decode_workspace_size(2, 3, 1000, 96, 1) == \
+        lib.kat_attn_decode_workspace_size(2, 3, 1000, 128, 1) > 0
+    assert lib.kat_attn_decode_workspace_size(2, 3, 1000, 20, 0) == \
+        lib.kat_attn_decode_workspace_size(2, 3, 1000, 32, 0) > 0
+    for D, dt in ((100, 1), (264, 1), (256 + 8, 2), (132, 0), (18, 0)):
+        assert lib.kat_attn_decode_workspace_size(2, 3, 1000, D, dt) == 0, (D, dt)
     n = lib.kat_men_bwd_workspace_size(16384, 4096, 1)
     assert n > 0 and n % (4096 * 4) == 0
     assert lib.kat_men_bwd_workspace_size(8, 96, 3) % (96 * 8) == 0

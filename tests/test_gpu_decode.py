@@ -37,8 +37,12 @@ def _oracle_last_row(q, kc, vc, slopes, scale, n):
     return o[:, :, n - 1], L[:, :, n - 1]
 
 
+# the layout widths, and head dims between them (fp32: multiples of 4 up to
+# 128; bf16 / fp16: multiples of 8 up to 256), whose columns past D are the
+# next head's data in the token-major caches below
 CASES = [(torch.float32, 32), (torch.float32, 64), (torch.float32, 128), (torch.bfloat16, 64),
-         (torch.bfloat16, 128), (torch.bfloat16, 256), (torch.float16, 128)]
+         (torch.bfloat16, 128), (torch.bfloat16, 256), (torch.float16, 128), (torch.float32, 20),
+         (torch.float32, 100), (torch.bfloat16, 8), (torch.bfloat16, 96), (torch.float16, 200)]
 
 
 @pytest.mark.parametrize("n", [1, 5, 200, 1000])
