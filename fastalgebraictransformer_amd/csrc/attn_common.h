@@ -48,15 +48,16 @@ int attn_bwd_generic(const AttnArgs& a, const typename AccT<T>::type* delta, hip
 // bf16 / fp16 MFMA kernels; return KAT_EUNSUPPORTED when the shape is not covered.
 // The backward runs its own prep pass; ws holds attn_mfma_workspace() bytes for
 // the call's mode: per-row stats (per 64-row tile: 4 cinv, then -4 cinv Delta),
-// an fp16 copy of Q ([B*H][T][D]),
+// an fp16 copy of Q ([B*H][T][W], W the layout width 32, 64, 128 or 256 the
+// head dim runs in, columns past D zero),
 // per-tile exponents and dS-bound parts, per-32-key K exponents, the fp16 dS
 // tiles of a group of heads or of one band of a head's keys (at most 4 GiB of
 // them, or one band of 512 keys), and for banded calls one head's fp32 dQ
 // partial sums.
 template <typename T> int attn_fwd_mfma(const AttnArgs& a, hipStream_t st);
 template <typename T> int attn_bwd_mfma(const AttnArgs& a, void* ws, hipStream_t st);
-bool attn_mfma_supported(int D);      // head dims of the MFMA backward (and forward)
-bool attn_mfma_fwd_supported(int D);  // head dims of the MFMA forward
+bool attn_mfma_supported(int D);      // head dims of the MFMA kernels: multiples of 8 up to 256
+bool attn_mfma_fwd_supported(int D);  // the same set, for the forward's dispatch
 size_t attn_mfma_workspace(int64_t B, int64_t H, int64_t T, int64_t D, bool causal);
 
 }  // namespace kat

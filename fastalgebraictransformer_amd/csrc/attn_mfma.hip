@@ -1376,7 +1376,7 @@ int launch_bwd(const AttnArgs& a, void* ws, hipStream_t st) {
   const BwdWs w = bwd_ws(ws, a.B, a.H, a.T, D, kCausal);
   const int BH = a.B * a.H;
   const int64_t tiles = (int64_t)BH * ((a.T + 63) / 64);
-  // prep: fp16 copies, exponents, Delta and the row stats, the dS bound parts
+  // prep: the fp16 copy of Q, exponents, Delta and the row stats, the dS bound parts
   hipLaunchKernelGGL((attn_bwd_prep_k<T, D>), dim3((unsigned)tiles), dim3(256), 0, st, a, w);
   if (int rc = check_launch("kat_attn_bwd (prep)")) return rc;
   const int cpb = (a.T + 255) / 256;
