@@ -146,7 +146,9 @@ def test_golden_bf16(gpu, name, monkeypatch):
                                      (1, 1, 1, 128), (1, 2, 1000, 128), (1, 2, 200, 256),
                                      (2, 2, 333, 256), (1, 1, 1, 256), (1, 2, 1000, 256),
                                      (1, 3, 200, 96), (2, 2, 333, 80), (1, 2, 300, 48),
-                                     (1, 2, 257, 192), (1, 1, 1, 96)])
+                                     (1, 2, 257, 192), (1, 1, 1, 96), (2, 2, 100, 24),
+                                     (1, 2, 257, 120), (1, 2, 300, 160), (1, 2, 200, 224),
+                                     (1, 2, 130, 248)])
 def test_lowp_shapes(gpu, dtype, B, H, T, D, monkeypatch):
     _pin_mfma(monkeypatch, D)
     q, k, v, do = _inputs(7 * T + D, B, H, T, D, dtype)

@@ -242,14 +242,16 @@ def test_d256_training_step_on_the_mfma_kernels(gpu, monkeypatch):
         check_lowp(got, ref, torch.bfloat16, name)
 
 
+@pytest.mark.parametrize("D", [256, 160, 96])
 @pytest.mark.parametrize("causal", [True, False])
-def test_mfma_backward_d256_masked(gpu, causal, monkeypatch):
+def test_mfma_backward_masked_wide_and_between(gpu, D, causal, monkeypatch):
     # padding mask (a whole key tile and a whole 16-key half dropped), causal
-    # and not, against the oracle's masked backward
+    # and not, against the oracle's masked backward: D = 256, and head dims
+    # that run the layout widths 256 / 128 with narrower MFMA loops
     from fastalgebraictransformer_amd.backward import _attn_bwd_into
     from fastalgebraictransformer_amd.forward import _attn_fwd_into, _key_mask_arg
     monkeypatch.setenv("KAT_ATTN_IMPL", "mfma")
-    B, H, T, D = 2, 2, 333, 256
+    B, H, T = 2, 2, 333
     q, k, v, do = _inputs(61, B, H, T, D, torch.bfloat16)
     slopes = F.compute_alibi_slopes(H)
     scale = 1.0 / math.sqrt(D)
