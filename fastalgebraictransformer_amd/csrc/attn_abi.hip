@@ -1,13 +1,15 @@
 // C ABI of the rational-attention kernels: argument checks and kernel choice.
 //
 // Kernel choice: bf16 / fp16 tensors with a head dim the MFMA kernels cover
-// (and 16-byte aligned rows) go to the MFMA kernels; everything else (fp32,
-// fp64, other head dims up to 1024, unaligned views) to the tiled kernels
-// (fp32 arithmetic; fp64 for fp64 tensors).
+// (and 16-byte aligned rows) go to the MFMA kernels, and so does the fp32
+// forward (the fp32 matrix instruction; head dims that are multiples of 4 up
+// to 128); everything else (the fp32 backward, fp64, other head dims up to
+// 1024, unaligned views) to the tiled kernels (fp32 arithmetic; fp64 for fp64
+// tensors).
 // KAT_ATTN_IMPL in the environment overrides the choice: "tiled" forces the
-// tiled kernels, "mfma" makes a bf16 / fp16 call that cannot take the MFMA
-// kernels fail with KAT_EUNSUPPORTED instead of falling back (both used by the
-// tests to pin which kernels they exercise).
+// tiled kernels, "mfma" makes a call that has an MFMA path (bf16 / fp16, and
+// the fp32 forward) but cannot take it fail with KAT_EUNSUPPORTED instead of
+// falling back (both used by the tests to pin which kernels they exercise).
 
 #include <stdlib.h>
 #include <string.h>
@@ -87,6 +89,16 @@ template <typename T> static int attn_fwd_t(const AttnArgs& a, hipStream_t st) {
   return attn_fwd_generic<T>(a, st);
 }
 
+static int attn_fwd_f32(const AttnArgs& a, hipStream_t st) {
+  if (!force_tiled() && attn_f32_mfma_supported(a.D) && rows16<float>(a.q, a.sq) &&
+      rows16<float>(a.k, a.sk) && rows16<float>(a.v, a.sv) && rows16<float>(a.o, a.so)) {
+    const int rc = attn_fwd_mfma_f32(a, st);
+    if (rc != KAT_EUNSUPPORTED) return rc;
+  }
+  if (require_mfma()) return fail(KAT_EUNSUPPORTED, "kat_attn_fwd: shape / layout not covered by the fp32 MFMA kernel");
+  return attn_fwd_generic<float>(a, st);
+}
+
 // Delta and cinv (accumulation type) at the start of the workspace, then the
 // tiled backward kernels
 template <typename T>
@@ -137,7 +149,7 @@ static int attn_fwd_impl(const char* nm, const void* q, const void* k, const voi
   a.causal = causal ? 1 : 0;
   const hipStream_t st = as_stream(stream);
   switch (dtype) {
-    case KAT_F32: return attn_fwd_generic<float>(a, st);
+    case KAT_F32: return attn_fwd_f32(a, st);
     case KAT_F64: return attn_fwd_generic<double>(a, st);
     case KAT_BF16: return attn_fwd_t<bf16>(a, st);
     case KAT_F16: return attn_fwd_t<f16>(a, st);

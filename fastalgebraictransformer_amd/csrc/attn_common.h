@@ -60,4 +60,9 @@ bool attn_mfma_supported(int D);      // head dims of the MFMA kernels: multiple
 bool attn_mfma_fwd_supported(int D);  // the same set, for the forward's dispatch
 size_t attn_mfma_workspace(int64_t B, int64_t H, int64_t T, int64_t D, bool causal);
 
+// fp32 forward on the fp32 matrix instruction (head dims: multiples of 4 up to
+// 128); KAT_EUNSUPPORTED when the shape is not covered.
+bool attn_f32_mfma_supported(int D);
+int attn_fwd_mfma_f32(const AttnArgs& a, hipStream_t st);
+
 }  // namespace kat

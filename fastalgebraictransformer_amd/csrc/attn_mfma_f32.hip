@@ -1,0 +1,280 @@
+// fp32 rational attention forward on gfx950 matrix cores: v_mfma_f32_16x16x4_f32.
+//
+// The fp32 form of the MFMA forward (attn_mfma_kernels.h): the same math
+// (forward.py:110-159: s = scale q.k - slope (i - j), f = sigma(s)^4 = t^4 / 16
+// with t = 1 + s / (|s| + 1), no running maximum, o = sum f v / (L + eps)), with
+// fp32 operands, products and sums throughout -- the precision of the
+// reference's fp32 kernel, which loads every operand .to(tl.float32)
+// (forward.py:103,126,146) -- on the fp32 matrix instruction instead of the
+// VALU (the tiled kernels in attn_generic.hip: ~3 TFLOP/s at config 1).
+//
+// Block: 4 waves of 16 queries (64 queries; small problems such as config 1,
+// B=2, H=12, S=512, still give 192 blocks). K and V stream through LDS in
+// tiles of KT keys (64; 32 at D = 128), double-buffered LDS-DMA. Per 16-key
+// group of a tile a wave computes
+//   S^T[key][q] = K Q^T      A = K (LDS, one ds_read_b128 per 4 k-steps)
+//                            B = Q^T (VGPRs for the whole kernel)
+//   f = t^4 of S^T (the C layout: lane (g, li) holds keys 4 g + j, query li)
+//   O^T[d][q] += V^T f^T     A = V^T (LDS, ds_read_b32)  B = f itself: the
+//                            k-index of the 16x16x4 product is the lane group
+//                            g, and lane (g, li) holds key 4 g + j in step j,
+//                            so S^T's C registers are O^T's B operand as they
+//                            stand (no conversion, no shuffle).
+// In QK^T the k-steps take the head dim in the order d = 16 m + 4 g + j
+// (block m, step j, lane group g): a lane's four steps of block m read 16
+// contiguous bytes of its key row, and its Q fragment is the float4 at the same
+// columns of its query row.
+// LDS tiles reuse the 16-bit tile helpers of attn_mfma_dev.h with rows of 2 D
+// 16-bit units (the same swizzle: the row reads above are those of the bf16
+// kernels' A fragments, and the four rows 4 g + j of a V read land in four
+// different bank groups).
+
+#include <algorithm>
+
+#include "attn_common.h"
+#include "attn_mfma_dev.h"
+#include "kat_internal.h"
+
+namespace kat {
+
+using namespace mfma;
+
+namespace {
+
+constexpr int kF32W = 4;                // waves per block
+constexpr int kF32Q = 16;               // queries per wave
+constexpr int kF32BM = kF32W * kF32Q;   // queries per block
+constexpr int kModeCausalF = 1;
+constexpr int kModeKeyMaskF = 2;
+template <int D> constexpr int f32_kt() { return D >= 128 ? 32 : 64; }  // keys per LDS tile
+
+__device__ __forceinline__ f32x4 mma_f32(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+template <int D, int MODE>
+__global__ __launch_bounds__(64 * kF32W, 2) void attn_fwd_f32_k(AttnArgs a) {
+  constexpr int D16 = 2 * D;  // a row in 16-bit units, the unit of the tile helpers
+  constexpr int KT = f32_kt<D>();
+  constexpr int M = D / 16;  // 16-column blocks of d: 4 k-steps of QK^T each; O^T subtiles
+  constexpr bool kCausal = (MODE & kModeCausalF) != 0;
+  constexpr bool kKM = (MODE & kModeKeyMaskF) != 0;
+  constexpr uint64_t kAll = KT == 64 ? ~0ull : (1ull << KT) - 1ull;  // every key of a tile valid
+  __shared__ short sk[2][KT * D16];
+  __shared__ short sv[2][KT * D16];
+
+  const int T_ = a.T, H = a.H;
+  int bh, rank;
+  block_order((int)blockIdx.x, a.B * H, bh, rank);
+  const int n_qt = (T_ + kF32BM - 1) / kF32BM;
+  const int q0 = (n_qt - 1 - rank) * kF32BM;
+  const int b = bh / H, h = bh - b * H;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int g = lane >> 4, li = lane & 15;
+  const int qw = q0 + kF32Q * w;
+
+  const float* qp = (const float*)a.q + b * a.sq[0] + h * a.sq[1];
+  const float* kp = (const float*)a.k + b * a.sk[0] + h * a.sk[1];
+  const float* vp = (const float*)a.v + b * a.sv[0] + h * a.sv[1];
+  const int DR = a.D;  // the head dim (<= D; columns DR .. D - 1 read as zeros)
+  const uint32_t sq2 = (uint32_t)a.sq[2], sk2 = (uint32_t)a.sk[2], sv2 = (uint32_t)a.sv[2];
+  // extents and strides in 16-bit units for the tile helpers
+  const uint32_t kbytes = row_bytes(T_, 2 * sk2, 2 * DR), vbytes = row_bytes(T_, 2 * sv2, 2 * DR);
+  const float slope = a.slopes[h];
+  const float scale = a.scale;
+
+  // Q^T fragments: lane (g, li) holds Q[qw + li][16 m + 4 g .. + 3] (step j of block m: element j)
+  f32x4 qf[M];
+  {
+    const __amdgpu_buffer_rsrc_t rq = rsrc(qp, row_bytes(T_, 2 * sq2, 2 * DR));
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const int col = 16 * m + 4 * g;
+      qf[m] = __builtin_bit_cast(f32x4, load16(rq, col_off(((uint32_t)(qw + li) * sq2 + col) * 4, col, DR)));
+    }
+  }
+  // element j of a 16-key group starting at key kh: key = kh + 4 g + j, query
+  // qw + li; bias slope (key - q) = per-lane part (fed to QK^T as its C input,
+  // divided by scale) + a uniform part
+  f32x4 cb;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) cb[j] = (slope / scale) * (float)(4 * g + j - li);
+  f32x4 cbx = cb;   // the bias in use (negated above the diagonal in non-causal mode)
+  float sgn = 1.f;
+  uint64_t vm = ~0ull;  // key validity of the current tile (bit r: key kcur + r)
+  int kcur = 0;
+  const uint8_t* kmb = kKM ? a.km + (int64_t)b * a.skm : nullptr;
+
+  f32x4 oacc[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) oacc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float lsum = 0.f;
+
+  TileDma<D16, kF32W, KT> dk, dv;
+  dk.init(w, lane, 2 * sk2, 2 * DR);
+  dv.init(w, lane, 2 * sv2, 2 * DR);
+
+  // one 16-key group at tile row hr (key kh): S^T, its f, and O^T += V^T f^T
+  auto group = [&](auto masked_tag, int hr, int kh, const short* ks_, const short* vs_) __attribute__((always_inline)) {
+    constexpr bool MASKED = decltype(masked_tag)::value;
+    constexpr bool kVM = kKM || !kCausal;
+    f32x4 s_ = cbx;
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const f32x4 kf = *reinterpret_cast<const f32x4*>(ks_ + soff<D16>(hr + li, 32 * m + 8 * g));
+#pragma unroll
+      for (int j = 0; j < 4; ++j) s_ = mma_f32(kf[j], qf[m][j], s_);
+    }
+    uint32_t nib = 0;
+    if constexpr (MASKED && kVM) nib = (uint32_t)(vm >> (kh - kcur + 4 * g));
+    const float tterm = (kCausal ? slope : sgn * slope) * (float)(kh - qw);
+    float f[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float s = fmaf(s_[j], scale, tterm);
+      if constexpr (MASKED && !kCausal) {
+        const float sd = sgn * (float)((kh + 4 * g + j) - (qw + li));
+        if (sd > 0.f) s = fmaf(-2.f * slope, sd, s);
+      }
+      const float r = __builtin_amdgcn_rcpf(fabsf(s) + 1.f);
+      const float t = fmaf(s, r, 1.f);
+      const float t2 = t * t;
+      f[j] = t2 * t2;
+      if (MASKED && kCausal && kh + 4 * g + j > qw + li) f[j] = 0.f;
+      if (MASKED && kVM && !((nib >> j) & 1u)) f[j] = 0.f;
+    }
+    lsum += (f[0] + f[1]) + (f[2] + f[3]);
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float vv = *reinterpret_cast<const float*>(vs_ + soff<D16>(hr + 4 * g + j, 32 * m + 2 * li));
+        oacc[m] = mma_f32(vv, f[j], oacc[m]);
+      }
+  };
+  auto tile = [&](auto masked_tag, int k0, const short* ks_, const short* vs_) __attribute__((always_inline)) {
+#pragma unroll
+    for (int hr = 0; hr < KT; hr += 16) group(masked_tag, hr, k0 + hr, ks_, vs_);
+  };
+  // which variant a tile takes (as in the bf16 forward): causal without a
+  // padding mask -- below the diagonal plain, straddling it masked, above it
+  // skipped; otherwise a tile wholly on one side of the diagonal with every
+  // key valid is plain, one with no valid key skipped, any other masked
+  auto tile_step = [&](int k0, const short* ks_, const short* vs_) __attribute__((always_inline)) {
+    if constexpr (kCausal && !kKM) {
+      if (k0 + KT - 1 <= qw)
+        tile(std::false_type{}, k0, ks_, vs_);
+      else if (k0 <= qw + kF32Q - 1)
+        tile(std::true_type{}, k0, ks_, vs_);
+    } else {
+      bool plain;
+      if constexpr (kCausal) {
+        plain = k0 + KT - 1 <= qw;
+      } else {
+        const bool above = k0 > qw + kF32Q - 1;
+        if (above && sgn > 0.f) {
+          cbx = -cbx;
+          sgn = -1.f;
+        }
+        plain = above || k0 + KT - 1 <= qw;
+      }
+      plain = plain && vm == kAll;
+      if (vm == 0ull || (kCausal && k0 > qw + kF32Q - 1)) {
+      } else if (plain) {
+        tile(std::false_type{}, k0, ks_, vs_);
+      } else {
+        tile(std::true_type{}, k0, ks_, vs_);
+      }
+    }
+  };
+
+  const int n_kt = kCausal ? (std::min(q0 + kF32BM, T_) + KT - 1) / KT : (T_ + KT - 1) / KT;
+  // this lane's padding-mask byte of key tile kt (0 past the tile or the end)
+  auto kmbyte = [&](int kt) __attribute__((always_inline)) {
+    const int j = kt * KT + lane;
+    return (kKM && lane < KT && j < T_) ? (uint32_t)kmb[j] : 0u;
+  };
+  uint32_t kmn = kmbyte(0);
+  dk.issue(sk[0], kp, kbytes, 0, 2 * sk2, w);
+  dv.issue(sv[0], vp, vbytes, 0, 2 * sv2, w);
+  dma_wait();
+  __syncthreads();
+  auto step = [&](int kt, auto buf_tag) __attribute__((always_inline)) {
+    constexpr int buf = decltype(buf_tag)::value;
+    if (kt + 1 < n_kt) {
+      dk.issue(sk[buf ^ 1], kp, kbytes, (kt + 1) * KT, 2 * sk2, w);
+      dv.issue(sv[buf ^ 1], vp, vbytes, (kt + 1) * KT, 2 * sv2, w);
+    }
+    const int k0 = kt * KT;
+    kcur = k0;
+    if constexpr (kKM) {
+      vm = __builtin_amdgcn_ballot_w64(kmn != 0u);
+      if (kt + 1 < n_kt) kmn = kmbyte(kt + 1);
+    } else if constexpr (!kCausal) {
+      vm = T_ - k0 >= KT ? kAll : (1ull << (T_ - k0)) - 1ull;
+    }
+    tile_step(k0, sk[buf], sv[buf]);
+    dma_wait();
+    __syncthreads();
+  };
+  for (int kt = 0; kt < n_kt; kt += 2) {
+    step(kt, std::integral_constant<int, 0>{});
+    if (kt + 1 < n_kt) step(kt + 1, std::integral_constant<int, 1>{});
+  }
+
+  // epilogue: L' across the 4 lane groups; lane (g, li) holds O^T[16 m + 4 g + jj][li]
+  float l = lsum;
+  l += __shfl_xor(l, 16, 64);
+  l += __shfl_xor(l, 32, 64);
+  const int qrow = qw + li;
+  if (qrow >= T_) return;
+  const float inv = 1.f / (l + 16.f * a.eps);
+  float* __restrict__ Lp = a.L + b * a.sl[0] + h * a.sl[1];
+  if (g == 0) Lp[(int64_t)qrow * a.sl[2]] = l * 0.0625f;
+  float* __restrict__ op = (float*)a.o + b * a.so[0] + h * a.so[1] + (int64_t)qrow * a.so[2];
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    const int col = 16 * m + 4 * g;
+    if (col < DR) *reinterpret_cast<f32x4*>(op + col) = oacc[m] * inv;
+  }
+}
+
+// layout widths of the fp32 kernels: 32, 64, 128 (a head dim between them,
+// a multiple of 4, runs in the next width with its columns past D as zeros)
+int f32_width(int D) { return D <= 32 ? 32 : D <= 64 ? 64 : 128; }
+
+#define KAT_F32_MODE_SWITCH(a, ...)                                                     \
+  switch ((a.causal ? kModeCausalF : 0) | (a.km != nullptr ? kModeKeyMaskF : 0)) {      \
+    case kModeCausalF: { constexpr int MODE = kModeCausalF; __VA_ARGS__; }              \
+    case kModeCausalF | kModeKeyMaskF: { constexpr int MODE = kModeCausalF | kModeKeyMaskF; __VA_ARGS__; } \
+    case kModeKeyMaskF: { constexpr int MODE = kModeKeyMaskF; __VA_ARGS__; }            \
+    default: { constexpr int MODE = 0; __VA_ARGS__; }                                   \
+  }
+
+template <int D, int MODE> int launch_fwd_f32(const AttnArgs& a, hipStream_t st) {
+  const int64_t nb = (int64_t)((a.T + kF32BM - 1) / kF32BM) * a.B * a.H;
+  hipLaunchKernelGGL((attn_fwd_f32_k<D, MODE>), dim3((unsigned)nb), dim3(64 * kF32W), 0, st, a);
+  return check_launch("kat_attn_fwd (fp32 mfma)");
+}
+
+}  // namespace
+
+bool attn_f32_mfma_supported(int D) { return D >= 4 && D <= 128 && D % 4 == 0; }
+
+int attn_fwd_mfma_f32(const AttnArgs& a, hipStream_t st) {
+  if (!attn_f32_mfma_supported(a.D)) return KAT_EUNSUPPORTED;
+  // 31-bit byte offsets per (b, h) slice for every row the tiles address
+  const int64_t lim = 0x7fffffffLL;
+  const int64_t* s2[3] = {&a.sq[2], &a.sk[2], &a.sv[2]};
+  for (int t = 0; t < 3; ++t)
+    if (*s2[t] < a.D || ((int64_t)a.T + 128) * *s2[t] * 4 > lim) return KAT_EUNSUPPORTED;
+  if ((int64_t)((a.T + kF32BM - 1) / kF32BM) * a.B * a.H > 0x7fffffffLL) return KAT_EUNSUPPORTED;
+  switch (f32_width(a.D)) {
+    case 32: KAT_F32_MODE_SWITCH(a, return (launch_fwd_f32<32, MODE>(a, st)));
+    case 64: KAT_F32_MODE_SWITCH(a, return (launch_fwd_f32<64, MODE>(a, st)));
+    case 128: KAT_F32_MODE_SWITCH(a, return (launch_fwd_f32<128, MODE>(a, st)));
+  }
+  return KAT_EUNSUPPORTED;
+}
+
+}  // namespace kat

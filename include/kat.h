@@ -152,11 +152,13 @@ int kat_add_men_bwd(const void* dy, const void* dh, const void* h, const void* w
  * forward.py:267-319 (kernel forward.py:49-159). dtype KAT_BF16/KAT_F16 use
  * the MFMA kernels (D a multiple of 8 up to 256, 16-byte aligned rows; a D
  * between the layout widths 32, 64, 128 and 256 runs in the kernels of the
- * next width, the columns past D read as zeros and not stored); KAT_F32,
- * KAT_F64 and other D (<= 1024; larger D returns KAT_EUNSUPPORTED) use the
- * tiled kernels, in fp32 arithmetic (fp64 for KAT_F64; the reference computes
- * in fp32 for every dtype, forward.py:103, and stores in the input dtype,
- * :155). L is fp32 for every dtype.
+ * next width, the columns past D read as zeros and not stored); KAT_F32 with
+ * D a multiple of 4 up to 128 and 16-byte aligned rows uses the fp32 MFMA
+ * kernel (v_mfma_f32_16x16x4_f32: fp32 products and sums); KAT_F64 and the
+ * other calls (D <= 1024; larger D returns KAT_EUNSUPPORTED) use the tiled
+ * kernels, in fp32 arithmetic (fp64 for KAT_F64; the reference computes in
+ * fp32 for every dtype, forward.py:103, and stores in the input dtype, :155).
+ * L is fp32 for every dtype.
  * ---------------------------------------------------------------------- */
 int kat_attn_fwd(const void* q, const void* k, const void* v, void* out, float* L,
                  const float* slopes, int64_t B, int64_t H, int64_t T, int64_t D,
