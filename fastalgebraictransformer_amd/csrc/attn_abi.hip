@@ -1,15 +1,14 @@
 // C ABI of the rational-attention kernels: argument checks and kernel choice.
 //
 // Kernel choice: bf16 / fp16 tensors with a head dim the MFMA kernels cover
-// (and 16-byte aligned rows) go to the MFMA kernels, and so does the fp32
-// forward (the fp32 matrix instruction; head dims that are multiples of 4 up
-// to 128); everything else (the fp32 backward, fp64, other head dims up to
-// 1024, unaligned views) to the tiled kernels (fp32 arithmetic; fp64 for fp64
-// tensors).
+// (and 16-byte aligned rows) go to the MFMA kernels, and so do fp32 tensors
+// (the fp32 matrix instruction; head dims that are multiples of 4 up to 128);
+// everything else (fp64, other head dims up to 1024, unaligned views) to the
+// tiled kernels (fp32 arithmetic; fp64 for fp64 tensors).
 // KAT_ATTN_IMPL in the environment overrides the choice: "tiled" forces the
-// tiled kernels, "mfma" makes a call that has an MFMA path (bf16 / fp16, and
-// the fp32 forward) but cannot take it fail with KAT_EUNSUPPORTED instead of
-// falling back (both used by the tests to pin which kernels they exercise).
+// tiled kernels, "mfma" makes a bf16 / fp16 / fp32 call that cannot take the
+// MFMA kernels fail with KAT_EUNSUPPORTED instead of falling back (both used
+// by the tests to pin which kernels they exercise).
 
 #include <stdlib.h>
 #include <string.h>
@@ -109,6 +108,20 @@ static int attn_bwd_tiled(const AttnArgs& a, void* ws, hipStream_t st) {
   A* cinv = reinterpret_cast<A*>(reinterpret_cast<char*>(ws) + stat_bytes(a.B, a.H, a.T, dt));
   if (int rc = attn_delta<T>(a, delta, cinv, st)) return rc;
   return attn_bwd_generic<T>(a, delta, st);
+}
+
+static int attn_bwd_f32(const AttnArgs& a, void* ws, hipStream_t st) {
+  if (!force_tiled() && attn_f32_mfma_supported(a.D) && rows16<float>(a.q, a.sq) &&
+      rows16<float>(a.k, a.sk) && rows16<float>(a.v, a.sv) && rows16<float>(a.dout, a.sdo) &&
+      rows16<float>(a.dq, a.sdq) && rows16<float>(a.dk, a.sdk) && rows16<float>(a.dv, a.sdv)) {
+    float* delta = reinterpret_cast<float*>(ws);
+    float* cinv = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + stat_bytes(a.B, a.H, a.T, KAT_F32));
+    if (int rc = attn_delta<float>(a, delta, cinv, st)) return rc;
+    const int rc = attn_bwd_mfma_f32(a, delta, cinv, st);
+    if (rc != KAT_EUNSUPPORTED) return rc;
+  }
+  if (require_mfma()) return fail(KAT_EUNSUPPORTED, "kat_attn_bwd: shape / layout not covered by the fp32 MFMA kernels");
+  return attn_bwd_tiled<float>(a, ws, st);
 }
 
 template <typename T>
@@ -222,7 +235,7 @@ static int attn_bwd_impl(const char* nm, const void* q, const void* k, const voi
   a.causal = causal ? 1 : 0;
   const hipStream_t st = as_stream(stream);
   switch (dtype) {
-    case KAT_F32: return attn_bwd_tiled<float>(a, workspace, st);
+    case KAT_F32: return attn_bwd_f32(a, workspace, st);
     case KAT_F64: return attn_bwd_tiled<double>(a, workspace, st);
     case KAT_BF16: return attn_bwd_t<bf16>(a, workspace, st);
     case KAT_F16: return attn_bwd_t<f16>(a, workspace, st);

@@ -186,8 +186,11 @@ size_t kat_attn_bwd_workspace_size(int64_t B, int64_t H, int64_t T, int64_t D, i
  * strides: 24 int64 = (b, h, t) strides of q, k, v, out, dout, dq, dk, dv.
  * Replaces the host wrapper + the dq and dkv launches at backward.py:273-341
  * (kernels backward.py:62-158 and 165-266). Deterministic. The MFMA and tiled
- * paths split the calls as kat_attn_fwd's (MFMA: KAT_BF16 / KAT_F16, D in
- * a multiple of 8 up to 256, 16-byte aligned rows). On the MFMA path
+ * paths split the calls as kat_attn_fwd's (MFMA: KAT_BF16 / KAT_F16 with D a
+ * multiple of 8 up to 256, KAT_F32 with D a multiple of 4 up to 128, 16-byte
+ * aligned rows; the fp32 backward recomputes S and dP with fp32 products and
+ * the reference's g, and needs only the tiled path's workspace). On the
+ * bf16 / fp16 MFMA path
  * dS is computed once (by the dK/dV kernel, which stores it for dQ), and it
  * and the copies of Q and K its products take enter the MFMA in fp16, each
  * with a power-of-two scale chosen from the data (per 64-row tile for Q, per

@@ -1,12 +1,12 @@
-"""GPU parity of the fp32 attention forward on the fp32 matrix instruction
-(v_mfma_f32_16x16x4_f32; csrc/attn_mfma_f32.hip).
+"""GPU parity of the fp32 attention forward and backward on the fp32 matrix
+instruction (v_mfma_f32_16x16x4_f32; csrc/attn_mfma_f32.hip).
 
 fp32 operands, products and sums, as the reference's fp32 kernel computes
 (forward.py:103,126,146 load every operand .to(tl.float32)). Bar: the fp32 bar
 of test_gpu_attention.py, <= 1e-5 of max|ref| on o and L against the fp64
 oracle; and against the fp32 tiled kernels (an independent fp32
-implementation) on the same inputs. KAT_ATTN_IMPL=mfma pins the MFMA kernel (a
-fallback is an error); the backward of these calls runs the tiled kernels.
+implementation) on the same inputs. KAT_ATTN_IMPL=mfma pins the MFMA kernels
+(a fallback is an error).
 """
 
 import math
@@ -114,3 +114,75 @@ def test_fp32_strided_views_and_fallbacks(gpu, monkeypatch):
         o_z, _ = F.rational_attention_forward(z, z, z, slopes[:2], 1.0 / math.sqrt(Dt))
         ro, _ = O.attention_fwd(z, z, z, slopes[:2].cpu(), 1.0 / math.sqrt(Dt))
         assert _rel_max(o_z, ro) <= 1e-5, Dt
+
+
+def _bwd(q, k, v, o, L, do, slopes, scale, mode, km):
+    from fastalgebraictransformer_amd.backward import _attn_bwd_into
+    from fastalgebraictransformer_amd.forward import _key_mask_arg
+    B, H, T, D = q.shape
+    g = [torch.full_like(q, float("nan")) for _ in range(3)]
+    kmd = _key_mask_arg(km, B, T, dev) if km is not None else None
+    _attn_bwd_into(q, k, v, o, L, do, *g, slopes, scale, mode != "noncausal", 1e-6, kmd,
+                   extended=mode != "causal")
+    torch.cuda.synchronize()
+    return g
+
+
+@pytest.mark.parametrize("mode", ["causal", "masked", "noncausal"])
+@pytest.mark.parametrize("B,H,T,D", [(2, 3, 77, 64), (1, 2, 512, 64), (2, 2, 600, 128),
+                                     (1, 3, 300, 32), (2, 2, 200, 96), (1, 2, 130, 20),
+                                     (1, 1, 1, 64), (2, 2, 257, 4), (1, 2, 190, 48)])
+def test_fp32_mfma_backward_matches_oracle(gpu, B, H, T, D, mode, monkeypatch):
+    # dq, dk, dv against the fp64 oracle's backward on the kernel's own (o, L)
+    # at 1e-5 of max|ref|, and against the tiled fp32 kernels on the same
+    # inputs; a dropped key's gradients are exactly 0
+    monkeypatch.setenv("KAT_ATTN_IMPL", "mfma")
+    q, k, v = _inputs(11 * T + D, B, H, T, D)
+    g = torch.Generator().manual_seed(17 * T + D)
+    do = torch.randn(B, H, T, D, generator=g).to(dev)
+    slopes = F.compute_alibi_slopes(H)
+    scale = 1.0 / math.sqrt(D)
+    km = _mask(B, T, T + D) if mode == "masked" else None
+    with torch.no_grad():
+        o, L = _fwd(q, k, v, slopes.to(dev), scale, mode, km)
+    got = _bwd(q, k, v, o, L, do, slopes.to(dev), scale, mode, km)
+    ref = O.attention_bwd(q, k, v, o, L, do, slopes, scale, causal=mode != "noncausal", key_mask=km)
+    for name, x, r in zip(("dq", "dk", "dv"), got, ref):
+        assert bool(torch.isfinite(x).all()), name
+        if T == 1 and name != "dv":
+            # one key: dP - Delta = dO.v (1 - p) cancels to eps-level, so dq and dk
+            # are rounding noise around ~0 and a bar relative to their max is void
+            assert float((x.cpu().double() - r).abs().max()) <= 1e-5, name
+            continue
+        assert _rel_max(x, r) <= 1e-5, (name, _rel_max(x, r))
+    if km is not None:
+        dropped = (km == 0).to(dev)[:, None, :, None].expand(B, H, T, D)
+        assert int(torch.count_nonzero(got[1][dropped])) == 0
+        assert int(torch.count_nonzero(got[2][dropped])) == 0
+    monkeypatch.setenv("KAT_ATTN_IMPL", "tiled")
+    tiled = _bwd(q, k, v, o, L, do, slopes.to(dev), scale, mode, km)
+    for name, x, t in zip(("dq", "dk", "dv"), got, tiled):
+        if T > 1 or name == "dv":
+            assert _rel_max(x, t) <= 1e-5, (name, _rel_max(x, t))
+
+
+def test_fp32_mfma_training_step_config1(gpu, monkeypatch):
+    # config 1's shape through autograd (fwd + bwd), both on the fp32 MFMA
+    # kernels, against the fp64 oracle (tests.py:210-211 bars and 1e-5 of max)
+    monkeypatch.setenv("KAT_ATTN_IMPL", "mfma")
+    B, H, T, D = 2, 12, 512, 64
+    q, k, v = _inputs(1, B, H, T, D)
+    g = torch.Generator().manual_seed(2)
+    do = torch.randn(B, H, T, D, generator=g).to(dev)
+    slopes = torch.tensor([2.0 ** (-8.0 * (i + 1) / H) for i in range(H)], dtype=torch.float32)
+    scale = 1.0 / math.sqrt(D)
+    qq, kk, vv = (t.clone().requires_grad_(True) for t in (q, k, v))
+    o = F.rational_attention(qq, kk, vv, slopes.to(dev), scale)
+    o.backward(do)
+    torch.cuda.synchronize()
+    ro, rL = O.attention_fwd(q, k, v, slopes, scale)
+    rq, rk, rv = O.attention_bwd(q, k, v, ro, rL, do, slopes, scale)
+    assert _rel_max(o, ro) <= 1e-5
+    for name, x, r in (("dq", qq.grad, rq), ("dk", kk.grad, rk), ("dv", vv.grad, rv)):
+        assert _rel_max(x, r) <= 1e-5, (name, _rel_max(x, r))
+        assert float((x.cpu().double() - r).abs().max()) < 1e-2  # tests.py:211

@@ -134,8 +134,7 @@ def test_masked_lowp(gpu, dtype, B, H, T, D, kind, causal, impl, monkeypatch):
 @pytest.mark.parametrize("impl", ["mfma", "tiled"])
 @pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 128), (torch.float32, 64)])
 def test_unmasked_and_all_ones_match_reference_entry_point(gpu, dtype, D, impl, monkeypatch):
-    # fp32 with impl "mfma": the forward on the fp32 MFMA kernel, the backward
-    # on the tiled kernels (fp32 has no MFMA backward)
+    # fp32 with impl "mfma": the fp32 MFMA kernels (forward and recompute backward)
     monkeypatch.setenv("KAT_ATTN_IMPL", impl)
     B, H, T = 2, 3, 190
     q, k, v, do = _inputs(9, B, H, T, D, dtype)
