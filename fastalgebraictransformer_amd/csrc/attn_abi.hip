@@ -2,7 +2,7 @@
 //
 // Kernel choice: bf16 / fp16 tensors with a head dim the MFMA kernels cover
 // (and 16-byte aligned rows) go to the MFMA kernels, and so do fp32 tensors
-// (the fp32 matrix instruction; head dims that are multiples of 4 up to 128);
+// (the fp32 matrix instruction; head dims that are multiples of 4 up to 256);
 // everything else (fp64, other head dims up to 1024, unaligned views) to the
 // tiled kernels (fp32 arithmetic; fp64 for fp64 tensors).
 // KAT_ATTN_IMPL in the environment overrides the choice: "tiled" forces the

@@ -61,7 +61,7 @@ bool attn_mfma_fwd_supported(int D);  // the same set, for the forward's dispatc
 size_t attn_mfma_workspace(int64_t B, int64_t H, int64_t T, int64_t D, bool causal);
 
 // fp32 forward and backward on the fp32 matrix instruction (head dims:
-// multiples of 4 up to 128); KAT_EUNSUPPORTED when the shape is not covered.
+// multiples of 4 up to 256); KAT_EUNSUPPORTED when the shape is not covered.
 // The backward takes Delta and cinv from attn_delta<float>.
 bool attn_f32_mfma_supported(int D);
 int attn_fwd_mfma_f32(const AttnArgs& a, hipStream_t st);

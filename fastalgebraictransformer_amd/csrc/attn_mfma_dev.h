@@ -204,10 +204,12 @@ __device__ __forceinline__ void dma_wait() { __builtin_amdgcn_s_waitcnt(0x0F70);
 // the row reads, and rows 0-3 and 4-7 take disjoint chunk pairs in the
 // transposed reads.
 // ---------------------------------------------------------------------------
-// D = 256 (rows of 512 bytes = 128 banks: a chunk's bank depends only on its
-// index mod 16, as for D = 128) takes the D = 128 map on the low 4 chunk bits.
+// D = 256 and 512 (rows of 512 / 1024 bytes: a chunk's bank depends only on
+// its index mod 16, as for D = 128; 512 16-bit units are the fp32 kernels'
+// rows of 256 floats) take the D = 128 map on the low 4 chunk bits.
 template <int D> __device__ __forceinline__ int swz(int row) {
-  static_assert(D == 32 || D == 64 || D == 128 || D == 256, "swizzle defined for D = 32, 64, 128, 256");
+  static_assert(D == 32 || D == 64 || D == 128 || D == 256 || D == 512,
+                "swizzle defined for D = 32, 64, 128, 256, 512");
   constexpr bool W = D >= 128;
   constexpr int i0 = W ? 8 : D == 64 ? 1 : 0, i1 = W ? 3 : D == 64 ? 2 : 0,
                 i2 = W ? 5 : D == 64 ? 4 : 2, i3 = W ? 11 : D == 64 ? 5 : 1;

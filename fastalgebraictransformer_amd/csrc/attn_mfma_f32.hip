@@ -11,7 +11,8 @@
 //
 // Block: 4 waves of 16 queries (64 queries; small problems such as config 1,
 // B=2, H=12, S=512, still give 192 blocks). K and V stream through LDS in
-// tiles of KT keys (64; 32 at D = 128), double-buffered LDS-DMA. Per 16-key
+// tiles of KT keys (64; 32 at D = 128, 16 at D = 256), double-buffered
+// LDS-DMA. Per 16-key
 // group of a tile a wave computes
 //   S^T[key][q] = K Q^T      A = K (LDS, one ds_read_b128 per 4 k-steps)
 //                            B = Q^T (VGPRs for the whole kernel)
@@ -47,14 +48,31 @@ constexpr int kF32Q = 16;               // queries per wave
 constexpr int kF32BM = kF32W * kF32Q;   // queries per block
 constexpr int kModeCausalF = 1;
 constexpr int kModeKeyMaskF = 2;
-template <int D> constexpr int f32_kt() { return D >= 128 ? 32 : 64; }  // keys per LDS tile
+template <int D> constexpr int f32_kt() { return D >= 256 ? 16 : D >= 128 ? 32 : 64; }  // keys per LDS tile
 
 __device__ __forceinline__ f32x4 mma_f32(float a, float b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// Schedule of a loop over M d blocks that each take NR LDS reads and NM
+// MFMAs on them: the reads run one block ahead of the MFMAs (0x100: LDS reads,
+// 0x008: MFMA), and nothing moves across the call (reads hoisted further keep
+// too many values live: spills at D >= 128).
+template <int M, int NR, int NM> __device__ __forceinline__ void f32_interleave() {
+  __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);
+#pragma unroll
+  for (int m = 0; m < M - 1; ++m) {
+    __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, NM, 0);
+  }
+  __builtin_amdgcn_sched_group_barrier(0x008, NM, 0);
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// D = 256: one block per CU (one wave per SIMD, 512 registers: the Q fragments
+// and O accumulators take 128)
 template <int D, int MODE>
-__global__ __launch_bounds__(64 * kF32W, 2) void attn_fwd_f32_k(AttnArgs a) {
+__global__ __launch_bounds__(64 * kF32W, D >= 256 ? 1 : 2) void attn_fwd_f32_k(AttnArgs a) {
   constexpr int D16 = 2 * D;  // a row in 16-bit units, the unit of the tile helpers
   constexpr int KT = f32_kt<D>();
   constexpr int M = D / 16;  // 16-column blocks of d: 4 k-steps of QK^T each; O^T subtiles
@@ -126,6 +144,7 @@ __global__ __launch_bounds__(64 * kF32W, 2) void attn_fwd_f32_k(AttnArgs a) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) s_ = mma_f32(kf[j], qf[m][j], s_);
     }
+    f32_interleave<M, 1, 4>();
     uint32_t nib = 0;
     if constexpr (MASKED && kVM) nib = (uint32_t)(vm >> (kh - kcur + 4 * g));
     const int kq = kh - qw;
@@ -148,6 +167,7 @@ __global__ __launch_bounds__(64 * kF32W, 2) void attn_fwd_f32_k(AttnArgs a) {
         const float vv = *reinterpret_cast<const float*>(vs_ + soff<D16>(hr + 4 * g + j, 32 * m + 2 * li));
         oacc[m] = mma_f32(vv, f[j], oacc[m]);
       }
+    f32_interleave<M, 4, 4>();
   };
   auto tile = [&](auto masked_tag, int k0, const short* ks_, const short* vs_) __attribute__((always_inline)) {
 #pragma unroll
@@ -244,7 +264,7 @@ __global__ __launch_bounds__(64 * kF32W, 2) void attn_fwd_f32_k(AttnArgs a) {
 // Delta and cinv come from attn_delta (the tiled path's first pass).
 // ============================================================================
 constexpr int kF32KB = kF32W * 16;  // keys per dK/dV block
-template <int D> constexpr int f32_qt() { return D >= 128 ? 32 : 64; }  // queries per LDS tile
+template <int D> constexpr int f32_qt() { return D >= 256 ? 16 : D >= 128 ? 32 : 64; }  // queries per LDS tile
 
 // p and dS of one score (s: the biased, scaled score)
 __device__ __forceinline__ void p_ds(float s, float dp, float ci, float dl, float eps2, float& p, float& ds) {
@@ -256,7 +276,7 @@ __device__ __forceinline__ void p_ds(float s, float dp, float ci, float dl, floa
 }
 
 template <int D, int MODE>
-__global__ __launch_bounds__(64 * kF32W, 2) void attn_bwd_dq_f32_k(AttnArgs a, const float* __restrict__ delta,
+__global__ __launch_bounds__(64 * kF32W, D >= 256 ? 1 : 2) void attn_bwd_dq_f32_k(AttnArgs a, const float* __restrict__ delta,
                                                                  const float* __restrict__ cinv) {
   constexpr int D16 = 2 * D;
   constexpr int KT = f32_kt<D>();
@@ -335,6 +355,7 @@ __global__ __launch_bounds__(64 * kF32W, 2) void attn_bwd_dq_f32_k(AttnArgs a, c
         dp = mma_f32(vf[j], gf[m][j], dp);
       }
     }
+    f32_interleave<M, 2, 8>();
     uint32_t nib = 0;
     if constexpr (MASKED && kVM) nib = (uint32_t)(vm >> (kh - kcur + 4 * g));
     const int kq = kh - qw;
@@ -354,6 +375,7 @@ __global__ __launch_bounds__(64 * kF32W, 2) void attn_bwd_dq_f32_k(AttnArgs a, c
         const float kv = *reinterpret_cast<const float*>(ks_ + soff<D16>(hr + 4 * g + j, 32 * m + 2 * li));
         qacc[m] = mma_f32(kv, dsv[j], qacc[m]);
       }
+    f32_interleave<M, 4, 4>();
   };
   auto tile = [&](auto masked_tag, int k0, const short* ks_, const short* vs_) __attribute__((always_inline)) {
 #pragma unroll
@@ -418,8 +440,10 @@ __global__ __launch_bounds__(64 * kF32W, 2) void attn_bwd_dq_f32_k(AttnArgs a, c
   }
 }
 
+// D = 256: the K^T and V^T fragments and the dV^T and dK^T accumulators alone
+// take 256 VGPRs, so one block per CU (one wave per SIMD, 512 registers)
 template <int D, int MODE>
-__global__ __launch_bounds__(64 * kF32W, 2) void attn_bwd_dkv_f32_k(AttnArgs a, const float* __restrict__ delta,
+__global__ __launch_bounds__(64 * kF32W, D >= 256 ? 1 : 2) void attn_bwd_dkv_f32_k(AttnArgs a, const float* __restrict__ delta,
                                                                   const float* __restrict__ cinv) {
   constexpr int D16 = 2 * D;
   constexpr int QT = f32_qt<D>();
@@ -500,6 +524,7 @@ __global__ __launch_bounds__(64 * kF32W, 2) void attn_bwd_dkv_f32_k(AttnArgs a, 
         dp = mma_f32(ga[j], vf[m][j], dp);
       }
     }
+    f32_interleave<M, 2, 8>();
     const f32x4 c4v = *reinterpret_cast<const f32x4*>(st_ + hr + 4 * g);
     const f32x4 dlv = *reinterpret_cast<const f32x4*>(st_ + QT + hr + 4 * g);
     const int kq = kw - qh;
@@ -522,17 +547,7 @@ __global__ __launch_bounds__(64 * kF32W, 2) void attn_bwd_dkv_f32_k(AttnArgs a, 
         vacc[m] = mma_f32(*reinterpret_cast<const float*>(gs_ + off), pv[j], vacc[m]);
         kacc[m] = mma_f32(*reinterpret_cast<const float*>(qs_ + off), dsv[j], kacc[m]);
       }
-    // the column reads run one d block ahead of the MFMAs that take them
-    // (0x100: LDS reads, 0x008: MFMA), and nothing moves across groups:
-    // reads hoisted further keep too many values live (spills at D = 128)
-    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
-#pragma unroll
-    for (int m = 0; m < M - 1; ++m) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
-    }
-    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
-    __builtin_amdgcn_sched_barrier(0);
+    f32_interleave<M, 8, 8>();
   };
   // a query tile: its 16-query groups (causal: those with a query at or
   // after one of the wave's keys)
@@ -593,9 +608,9 @@ __global__ __launch_bounds__(64 * kF32W, 2) void attn_bwd_dkv_f32_k(AttnArgs a, 
   }
 }
 
-// layout widths of the fp32 kernels: 32, 64, 128 (a head dim between them,
-// a multiple of 4, runs in the next width with its columns past D as zeros)
-int f32_width(int D) { return D <= 32 ? 32 : D <= 64 ? 64 : 128; }
+// layout widths of the fp32 kernels: 32, 64, 128, 256 (a head dim between
+// them, a multiple of 4, runs in the next width with its columns past D as zeros)
+int f32_width(int D) { return D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : 256; }
 
 #define KAT_F32_MODE_SWITCH(a, ...)                                                     \
   switch ((a.causal ? kModeCausalF : 0) | (a.km != nullptr ? kModeKeyMaskF : 0)) {      \
@@ -632,7 +647,7 @@ bool f32_offsets_ok(const AttnArgs& a, bool bwd) {
 
 }  // namespace
 
-bool attn_f32_mfma_supported(int D) { return D >= 4 && D <= 128 && D % 4 == 0; }
+bool attn_f32_mfma_supported(int D) { return D >= 4 && D <= 256 && D % 4 == 0; }
 
 int attn_bwd_mfma_f32(const AttnArgs& a, const float* delta, const float* cinv, hipStream_t st) {
   if (!attn_f32_mfma_supported(a.D) || !f32_offsets_ok(a, true)) return KAT_EUNSUPPORTED;
@@ -640,6 +655,7 @@ int attn_bwd_mfma_f32(const AttnArgs& a, const float* delta, const float* cinv, 
     case 32: KAT_F32_MODE_SWITCH(a, return (launch_bwd_f32<32, MODE>(a, delta, cinv, st)));
     case 64: KAT_F32_MODE_SWITCH(a, return (launch_bwd_f32<64, MODE>(a, delta, cinv, st)));
     case 128: KAT_F32_MODE_SWITCH(a, return (launch_bwd_f32<128, MODE>(a, delta, cinv, st)));
+    case 256: KAT_F32_MODE_SWITCH(a, return (launch_bwd_f32<256, MODE>(a, delta, cinv, st)));
   }
   return KAT_EUNSUPPORTED;
 }
@@ -650,6 +666,7 @@ int attn_fwd_mfma_f32(const AttnArgs& a, hipStream_t st) {
     case 32: KAT_F32_MODE_SWITCH(a, return (launch_fwd_f32<32, MODE>(a, st)));
     case 64: KAT_F32_MODE_SWITCH(a, return (launch_fwd_f32<64, MODE>(a, st)));
     case 128: KAT_F32_MODE_SWITCH(a, return (launch_fwd_f32<128, MODE>(a, st)));
+    case 256: KAT_F32_MODE_SWITCH(a, return (launch_fwd_f32<256, MODE>(a, st)));
   }
   return KAT_EUNSUPPORTED;
 }

@@ -153,7 +153,7 @@ int kat_add_men_bwd(const void* dy, const void* dh, const void* h, const void* w
  * the MFMA kernels (D a multiple of 8 up to 256, 16-byte aligned rows; a D
  * between the layout widths 32, 64, 128 and 256 runs in the kernels of the
  * next width, the columns past D read as zeros and not stored); KAT_F32 with
- * D a multiple of 4 up to 128 and 16-byte aligned rows uses the fp32 MFMA
+ * D a multiple of 4 up to 256 and 16-byte aligned rows uses the fp32 MFMA
  * kernel (v_mfma_f32_16x16x4_f32: fp32 products and sums); KAT_F64 and the
  * other calls (D <= 1024; larger D returns KAT_EUNSUPPORTED) use the tiled
  * kernels, in fp32 arithmetic (fp64 for KAT_F64; the reference computes in
@@ -187,7 +187,7 @@ size_t kat_attn_bwd_workspace_size(int64_t B, int64_t H, int64_t T, int64_t D, i
  * Replaces the host wrapper + the dq and dkv launches at backward.py:273-341
  * (kernels backward.py:62-158 and 165-266). Deterministic. The MFMA and tiled
  * paths split the calls as kat_attn_fwd's (MFMA: KAT_BF16 / KAT_F16 with D a
- * multiple of 8 up to 256, KAT_F32 with D a multiple of 4 up to 128, 16-byte
+ * multiple of 8 up to 256, KAT_F32 with D a multiple of 4 up to 256, 16-byte
  * aligned rows; the fp32 backward recomputes S and dP with fp32 products and
  * the reference's g, and needs only the tiled path's workspace). On the
  * bf16 / fp16 MFMA path

@@ -51,7 +51,8 @@ def _fwd(q, k, v, slopes, scale, mode, km):
 @pytest.mark.parametrize("mode", ["causal", "masked", "noncausal"])
 @pytest.mark.parametrize("B,H,T,D", [(2, 3, 77, 64), (1, 2, 512, 64), (2, 2, 1000, 128),
                                      (1, 3, 300, 32), (2, 2, 200, 96), (1, 2, 130, 20),
-                                     (1, 1, 1, 64), (2, 2, 257, 4), (1, 2, 190, 48)])
+                                     (1, 1, 1, 64), (2, 2, 257, 4), (1, 2, 190, 48),
+                                     (2, 2, 333, 256), (1, 2, 200, 160), (1, 1, 1, 256)])
 def test_fp32_mfma_forward_matches_oracle(gpu, B, H, T, D, mode, monkeypatch):
     monkeypatch.setenv("KAT_ATTN_IMPL", "mfma")
     q, k, v = _inputs(7 * T + D, B, H, T, D)
@@ -92,7 +93,7 @@ def test_fp32_strided_views_and_fallbacks(gpu, monkeypatch):
     # and match the contiguous call bit for bit; a view whose rows are not
     # 16-byte aligned falls back to the tiled kernels (an error under
     # KAT_ATTN_IMPL=mfma); a head dim that is not a multiple of 4, or above
-    # 128, runs the tiled kernels
+    # 256, runs the tiled kernels
     B, T, H, D = 2, 150, 3, 64
     g = torch.Generator().manual_seed(5)
     x = torch.randn(B, T, 3, H, D, generator=g).to(dev)
@@ -109,7 +110,7 @@ def test_fp32_strided_views_and_fallbacks(gpu, monkeypatch):
     o_u, _ = F.rational_attention_forward(y, y, y, slopes, 0.125)
     ro, _ = O.attention_fwd(y, y, y, slopes.cpu(), 0.125)
     assert _rel_max(o_u, ro) <= 1e-5
-    for Dt in (18, 160):
+    for Dt in (18, 260):
         z = torch.randn(1, 2, 70, Dt, generator=g).to(dev)
         o_z, _ = F.rational_attention_forward(z, z, z, slopes[:2], 1.0 / math.sqrt(Dt))
         ro, _ = O.attention_fwd(z, z, z, slopes[:2].cpu(), 1.0 / math.sqrt(Dt))
@@ -131,7 +132,8 @@ def _bwd(q, k, v, o, L, do, slopes, scale, mode, km):
 @pytest.mark.parametrize("mode", ["causal", "masked", "noncausal"])
 @pytest.mark.parametrize("B,H,T,D", [(2, 3, 77, 64), (1, 2, 512, 64), (2, 2, 600, 128),
                                      (1, 3, 300, 32), (2, 2, 200, 96), (1, 2, 130, 20),
-                                     (1, 1, 1, 64), (2, 2, 257, 4), (1, 2, 190, 48)])
+                                     (1, 1, 1, 64), (2, 2, 257, 4), (1, 2, 190, 48),
+                                     (2, 2, 333, 256), (1, 2, 200, 160), (1, 1, 1, 256)])
 def test_fp32_mfma_backward_matches_oracle(gpu, B, H, T, D, mode, monkeypatch):
     # dq, dk, dv against the fp64 oracle's backward on the kernel's own (o, L)
     # at 1e-5 of max|ref|, and against the tiled fp32 kernels on the same
