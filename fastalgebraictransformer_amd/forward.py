@@ -52,20 +52,22 @@ _MFMA_OFFSET_LIMIT = 0x7FFFFFFF
 _MFMA_ROW_PAD = 128
 
 
-def _mfma_head_dim(D):
-    """Head dims the MFMA kernels cover (forward and backward): multiples of 8
-    up to 256 (run in the kernels of the next layout width, 32, 64, 128 or
-    256 columns, with the columns past D read as zeros)."""
-    return 8 <= D <= 256 and D % 8 == 0
+def _mfma_head_dim(D, elem=2):
+    """Head dims the MFMA kernels cover (forward and backward): 16-byte rows
+    up to 256 columns -- multiples of 8 for bf16 / fp16 (``elem`` 2), of 4
+    for fp32 (``elem`` 4) -- run in the kernels of the next layout width (32,
+    64, 128 or 256 columns) with the columns past D read as zeros."""
+    step = 16 // elem
+    return step <= D <= 256 and D % step == 0
 
 
 def _tiled_reason(shapes_strides_ptrs, D, T, elem):
-    """Why a bf16 / fp16 attention call would leave the MFMA kernels for the
-    tiled ones (None if it takes them), from each operand's (b, h, t) strides
-    and data pointer: the head dim, 16-byte row alignment, and the 31-bit byte
-    offsets the MFMA kernels use within one (b, h) slice."""
-    if not _mfma_head_dim(D):
-        return f"head dim {D} (the MFMA kernels cover multiples of 8 up to 256)"
+    """Why a bf16 / fp16 / fp32 attention call would leave the MFMA kernels
+    for the tiled ones (None if it takes them), from each operand's (b, h, t)
+    strides and data pointer: the head dim, 16-byte row alignment, and the
+    31-bit byte offsets the MFMA kernels use within one (b, h) slice."""
+    if not _mfma_head_dim(D, elem):
+        return f"head dim {D} (the MFMA kernels cover multiples of {16 // elem} up to 256)"
     for strides, ptr in shapes_strides_ptrs:
         if ptr % 16 or any((st * elem) % 16 for st in strides):
             return "rows not 16-byte aligned (a view with an odd offset or stride)"
@@ -74,21 +76,22 @@ def _tiled_reason(shapes_strides_ptrs, D, T, elem):
         if st < D or (T + _MFMA_ROW_PAD) * st * elem > _MFMA_OFFSET_LIMIT:
             return (f"row stride {st} at T = {T}: a (b, h) slice spans 2^31 bytes or more "
                     "(the MFMA kernels address a slice with 31-bit offsets)")
-    if T * D * 2 >= _MFMA_OFFSET_LIMIT or T * 8 >= _MFMA_OFFSET_LIMIT:
+    if elem == 2 and (T * D * 2 >= _MFMA_OFFSET_LIMIT or T * 8 >= _MFMA_OFFSET_LIMIT):
         return f"T = {T}: per-head workspace rows exceed 31-bit offsets"
     return None
 
 
 def _warn_if_tiled(tensors, D, dtype, mfma_inputs=None):
-    """bf16 / fp16 attention runs on the MFMA kernels when the head dim is a
-    multiple of 8 up to 256, every [B, H, T, D] operand has 16-byte aligned rows and the
+    """bf16 / fp16 (fp32) attention runs on the MFMA kernels when the head dim
+    is a multiple of 8 (4) up to 256, every [B, H, T, D] operand has 16-byte aligned rows and the
     inputs the kernels address by 31-bit offsets (q, k, v; and O, dO in the
     backward: ``mfma_inputs``) keep each (b, h) slice below 2^31 bytes;
     otherwise libkat falls back to the tiled kernels, which are correct but
     about an order of magnitude slower. Warn once per dtype and reason, so a model with
     another head dim, a misaligned view or a very long packed sequence does
     not lose that silently."""
-    if dtype not in (torch.bfloat16, torch.float16) or os.environ.get("KAT_ATTN_IMPL") == "tiled":
+    if dtype not in (torch.bfloat16, torch.float16, torch.float32) or \
+            os.environ.get("KAT_ATTN_IMPL") == "tiled":
         return
     T = tensors[0].shape[2]
     elem = tensors[0].element_size()
@@ -100,7 +103,7 @@ def _warn_if_tiled(tensors, D, dtype, mfma_inputs=None):
         return
     if (dtype, reason) not in _WARNED:
         _WARNED.add((dtype, reason))
-        warnings.warn(f"rational attention in {dtype}: {reason}; running the fp32 tiled "
+        warnings.warn(f"rational attention in {dtype}: {reason}; running the tiled "
                       "kernels, about 10x slower than the MFMA path", RuntimeWarning, stacklevel=3)
 
 

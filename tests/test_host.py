@@ -225,6 +225,12 @@ def test_tiled_fallback_reasons_mirror_the_mfma_limits():
         assert _tiled_reason([((16 * T * Dm, T * Dm, Dm), 0)], Dm, T, 2) is None, Dm
     for Dt in (4, 100, 264, 512):
         assert f"head dim {Dt}" in _tiled_reason([((T * 512, T * 512, 512), 0)], Dt, T, 2), Dt
+    # fp32 (4-byte elements): multiples of 4 up to 256
+    for Dm in (4, 20, 100, 256):
+        assert _tiled_reason([((16 * T * Dm, T * Dm, Dm), 0)], Dm, T, 4) is None, Dm
+    for Dt in (2, 18, 260):
+        assert f"head dim {Dt}" in _tiled_reason([((T * 512, T * 512, 512), 0)], Dt, T, 4), Dt
+    assert "31-bit" in _tiled_reason([((T * 6144, 128, 6144), 0)], 128, 0x7FFFFFFF // (6144 * 4), 4)
     assert "16-byte" in _tiled_reason([((T * D, T * D, D), 8)], D, T, 2)
     assert "16-byte" in _tiled_reason([((T * D, T * D, D + 1), 0)], D, T, 2)
     # the model's packed qkv [B, T, 3, H, D] (H = 16, D = 128): row stride 6144
