@@ -22,6 +22,8 @@ throughput 7*B*H*S^2*D / step time in TFLOP/s. The same JSON line carries:
                  (B=2, H=16, S=8192, D=128, bf16);
   * head_dims  -- fwd+bwd at D = 32, 64 and 256 (bf16, S=4096, the headline's
                  B*H*D, so the same flops), all on the MFMA kernels;
+  * fp32_attention -- fwd+bwd in fp32 (B=4, H=16, S=2048, D=64) on the fp32
+                 MFMA kernels, against the 157.3 TFLOP/s fp32 peak;
   * attention_variants -- fwd+bwd of the padding-mask / non-causal attention
                  extension at the same shape (right-padded batch, non-causal,
                  both), TFLOP/s over the (query, key) pairs each attends;
@@ -84,15 +86,15 @@ def measured_traffic():
     return out
 
 
-def attention_inputs(torch, B, H, T, D, dev, seed=0):
+def attention_inputs(torch, B, H, T, D, dev, seed=0, dtype=None):
     g = torch.Generator().manual_seed(seed)
-    ts = [torch.randn(B, H, T, D, generator=g).to(torch.bfloat16) for _ in range(4)]
+    ts = [torch.randn(B, H, T, D, generator=g).to(dtype or torch.bfloat16) for _ in range(4)]
     return [t.to(dev) for t in ts]
 
 
-def bench_attention(torch, F, steps, warmup, B=4, H=16, T=4096, D=128):
+def bench_attention(torch, F, steps, warmup, B=4, H=16, T=4096, D=128, dtype=None):
     dev = torch.device("cuda:0")
-    q, k, v, do = attention_inputs(torch, B, H, T, D, dev)
+    q, k, v, do = attention_inputs(torch, B, H, T, D, dev, dtype=dtype)
     for t in (q, k, v):
         t.requires_grad_(True)
     slopes = torch.tensor([2.0 ** (-(i + 1) / 2) for i in range(H)], dtype=torch.float32,
@@ -678,7 +680,7 @@ def main():
     ap.add_argument("--no-config5", action="store_true",
                     help="skip the attention fwd+bwd at the 1.3B model's shape (B=2, H=16, S=8192)")
     ap.add_argument("--no-head-dims", action="store_true",
-                    help="skip the attention fwd+bwd at D = 32, 64 and 256")
+                    help="skip the attention fwd+bwd at D = 32, 64 and 256 and in fp32")
     ap.add_argument("--no-device", action="store_true", help="skip the MFMA / copy probes")
     ap.add_argument("--no-config1", action="store_true",
                     help="skip the config-1 fp32 attention timing (B=2, H=12, S=512, D=64)")
@@ -760,6 +762,15 @@ def main():
                             "TFLOPs": round(th, 2), "frac_mfma_peak": round(th / PEAK_BF16_TFLOPS, 4),
                             "fwd_ms": round(ah["fwd_ms"], 4), "bwd_ms": round(ah["bwd_ms"], 4)}
         line["head_dims"] = hd
+        af = bench_attention(torch, F, 10, 3, B=4, H=16, T=2048, D=64, dtype=torch.float32)
+        tf = af["flops_step"] / (af["ms"] * 1e-3) / 1e12
+        line["fp32_attention"] = {
+            "shape": {"B": 4, "H": 16, "S": 2048, "D": 64}, "dtype": "fp32",
+            "kernels": "fp32 MFMA (v_mfma_f32_16x16x4_f32)", "ms_per_step": round(af["ms"], 4),
+            "TFLOPs": round(tf, 2), "frac_fp32_peak": round(tf / PEAK_FP32_TFLOPS, 4),
+            "fwd_ms": round(af["fwd_ms"], 4), "bwd_ms": round(af["bwd_ms"], 4),
+            "fwd_TFLOPs": round(af["flops_fwd"] / (af["fwd_ms"] * 1e-3) / 1e12, 2),
+            "bwd_TFLOPs": round(af["flops_bwd"] / (af["bwd_ms"] * 1e-3) / 1e12, 2)}
     if not args.no_config1:
         line["config1_fp32"] = bench_config1(torch, F)
     if not args.no_variants:

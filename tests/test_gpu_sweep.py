@@ -1,10 +1,11 @@
 """A seeded random sweep of attention shapes against the oracle: sequence
 lengths that are not multiples of the kernels' tiles, head dims 32 / 64 / 128
-(bf16 / fp16 on the MFMA kernels, fp32 on the tiled kernels), 1 to 16
+(bf16 / fp16 and fp32 on the MFMA kernels), 1 to 16
 heads, bf16 / fp16 / fp32, causal or with a padding mask or non-causal; and a
 second sweep over head dims between the layout widths (multiples of 8 up to
 256, which the MFMA kernels of the next width run with the columns past D
-read as zeros and not stored). The draws are fixed (seeds below), so a
+read as zeros and not stored), and one over fp32 head dims (multiples of 4
+up to 256) pinned to the fp32 MFMA kernels. The draws are fixed (seeds below), so a
 failure names a reproducible case. Bars as in test_gpu_attention.py: fp32 <=
 1e-5 of max|ref|; bf16 / fp16 2e-2 + 1/2 ulp elementwise and relative L2 <=
 5e-3."""
@@ -52,6 +53,16 @@ def test_random_shape_padded_head_dim(gpu, i, dtype, B, H, T, D, mode, monkeypat
     _check_case(100 + i, dtype, B, H, T, D, mode)
 
 
+_FP32_DIMS = (4, 12, 20, 32, 44, 64, 76, 96, 128, 140, 200, 256)
+
+
+@pytest.mark.parametrize("i,dtype,B,H,T,D,mode", _draw(16, seed=303, dims=_FP32_DIMS, dtypes=("fp32",)))
+def test_random_shape_fp32_mfma(gpu, i, dtype, B, H, T, D, mode, monkeypatch):
+    # fp32 head dims (multiples of 4 up to 256) on the fp32 MFMA kernels
+    monkeypatch.setenv("KAT_ATTN_IMPL", "mfma")
+    _check_case(200 + i, dtype, B, H, T, D, mode)
+
+
 def _check_case(i, dtype, B, H, T, D, mode):
     dt = {"bf16": torch.bfloat16, "fp16": torch.float16, "fp32": torch.float32}[dtype]
     g = torch.Generator().manual_seed(1000 + i)
@@ -70,8 +81,11 @@ def _check_case(i, dtype, B, H, T, D, mode):
                                         key_mask=None if km is None else km.to(dev), causal=causal)
     o.backward(do)
     torch.cuda.synchronize()
-    ro, rL = O.attention_fwd(q, k, v, slopes, scale, dtype=torch.float32, causal=causal, key_mask=km)
-    rq, rk, rv = O.attention_bwd(q, k, v, o, rL, do, slopes, scale, dtype=torch.float32,
+    # the oracle in fp64 for fp32 inputs (a truth below both fp32
+    # implementations' rounding), in fp32 for the 16-bit ones
+    odt = torch.float64 if dt == torch.float32 else torch.float32
+    ro, rL = O.attention_fwd(q, k, v, slopes, scale, dtype=odt, causal=causal, key_mask=km)
+    rq, rk, rv = O.attention_bwd(q, k, v, o, rL, do, slopes, scale, dtype=odt,
                                  causal=causal, key_mask=km)
     for name, got, ref in (("o", o, ro), ("dq", qq.grad, rq), ("dk", kk.grad, rk),
                            ("dv", vv.grad, rv)):
