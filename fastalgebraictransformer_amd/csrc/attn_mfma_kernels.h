@@ -19,7 +19,7 @@
 //
 // Common structure of the forward and dK/dV kernels (the dQ kernel is a plain
 // streaming GEMM, described at it). Each wave owns 32 rows (queries, or keys
-// for dK/dV) whose
+// for dK/dV; 16 or 64 keys at some head dims, see dkv_keys) whose
 // operand fragments stay in VGPRs as the B operand of v_mfma_f32_16x16x32; the
 // streamed side is staged 64 rows at a time by LDS-DMA into a swizzled,
 // double-buffered LDS tile and read as the A operand, either row-wise
@@ -843,14 +843,19 @@ template <int D, int KS>
 struct DkvSmem {
   short q[2][kBN * D];         // Q16 tiles
   short o[2][kBN * D];         // dO tiles
-  float st[2][2 * kBN];        // the tile's stats: 4 cinv of its queries, then -4 cinv Delta
   f32x4 x[2][kNW][2 * KS][64];  // w: [chunk parity][key group][16-query half x ks][lane]
+  float st[2][2 * kBN];        // the tile's stats: 4 cinv of its queries, then -4 cinv Delta
   float km[kNW];               // KS = 1: the key groups' max |k| (pairs share an exponent)
 };
 
-// KR: keys per wave pair, 32 (D <= 128) or 16 (D = 256, whose B fragments and
-// accumulators of 32 keys would exceed the register budget); the two pairs of
-// a 32-key group then share one K16 exponent
+// KR: keys per wave pair. 32 at D = 32 and 128; 64 at D = 64 (twice the
+// MFMAs per LDS read of the streamed Q16 / dO tiles, in the registers D = 128
+// takes for 32 keys: backward 9-10% faster than 32 keys; at D = 32, whose
+// time is the per-score VALU work, 64 keys measured 10-13% slower); 16 at
+// D = 256 (whose B fragments and accumulators of 32 keys would exceed the
+// register budget), the two pairs of a 32-key group then sharing one K16
+// exponent. K16 exponents are per 32 keys at every KR.
+template <int D> constexpr int dkv_keys() { return D == 256 ? 16 : D == 64 ? 64 : kRows; }
 template <typename T, int D, int MODE, int KR = kRows, int DE = D>
 __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float* __restrict__ stats,
                                                          const f16* __restrict__ q16,
@@ -865,6 +870,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
   constexpr bool kCausal = (MODE & kModeCausal) != 0;
   constexpr bool kKM = (MODE & kModeKeyMask) != 0;
   constexpr int KS = KR / 16;     // 16-key groups per wave
+  constexpr int NE = (KS + 1) / 2;  // K16 exponents per wave (one per 32 keys; 16-key group ks takes ks / 2)
   constexpr int BK = kNW * KR;    // keys per block
   __shared__ DkvSmem<D, KS> sm;
 
@@ -905,22 +911,31 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
   const int ktg = kw >> 6;
   const bool dst_ok = ktg < nt;
   f16* const dsh = dst + (int64_t)bl * ds_tiles_per_band(nt, kCausal, kb0, nk) * 4096;
-  // block 4 kh2 + 2 qh + ks of the tile (kh2: the 32-key half, ks: the
-  // 16-key group); dso: kh2's blocks plus the lane's 16 bytes, dsk: the
-  // wave's first 16-key group
-  const uint32_t dso = (uint32_t)(((kw & 63) >> 5) * 2048 + lane * 8);
-  const int dsk = (kw >> 4) & 1;
+  // block 4 kh2 + 2 qh + kg of the tile (kh2: the 32-key half, kg: the
+  // 16-key group within it); dso[ks]: the offset of 16-key group ks's block
+  // (without the 32-query half qh) plus the lane's 16 bytes
+  uint32_t dso[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    const int ko = (kw & 63) + 16 * ks;
+    dso[ks] = (uint32_t)((ko >> 5) * 2048 + ((ko >> 4) & 1) * 512 + lane * 8);
+  }
   f16* dtile = dsh;  // the current query tile's dS^T tile
 
   // B operands: K16^T (P role) or V^T (D role) fragments; lane (g, li) holds row
   // kw + 16 ks + li, columns 32 kk + 8 g .. +7
-  // (P role: scaled by 2^ekw, the exponent tile_exp gives the wave's 32 keys)
+  // (P role: scaled by 2^ekw[ks / 2], the exponent tile_exp gives their 32 keys)
   i16x8 bfr[KS][KK];
-  int ekw = 0;
+  int ekw[NE];
   {
     const __amdgpu_buffer_rsrc_t rk = rsrc(kp, row_bytes(T_, sk2, DR));
     const __amdgpu_buffer_rsrc_t rv = rsrc(vp, row_bytes(T_, sv2, DR));
-    float km = 0.f;
+    float km[NE];
+#pragma unroll
+    for (int e = 0; e < NE; ++e) {
+      km[e] = 0.f;
+      ekw[e] = 0;
+    }
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const uint32_t key = (uint32_t)(kw + 16 * ks + li);
@@ -929,7 +944,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
         const int col = 32 * kk + 8 * g;
         if (prole) {
           bfr[ks][kk] = load16(rk, col_off((key * sk2 + col) * 2, col, DR));
-          km = fmaxf(km, absmax8<T>(bfr[ks][kk]));
+          km[ks / 2] = fmaxf(km[ks / 2], absmax8<T>(bfr[ks][kk]));
         } else {
           bfr[ks][kk] = load16(rv, col_off((key * sv2 + col) * 2, col, DR));
         }
@@ -937,25 +952,31 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
     }
     if (prole) {
 #pragma unroll
-      for (int o = 32; o > 0; o >>= 1) km = fmaxf(km, __shfl_xor(km, o, 64));
+      for (int e = 0; e < NE; ++e)
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) km[e] = fmaxf(km[e], __shfl_xor(km[e], o, 64));
     }
     if constexpr (KS == 1) {
       // the 32-key group's two 16-key halves (waves grp and grp ^ 1) share one
       // exponent: the max of both
-      if (prole && lane == 0) sm.km[grp] = km;
+      if (prole && lane == 0) sm.km[grp] = km[0];
       __syncthreads();
-      if (prole) km = fmaxf(km, sm.km[grp ^ 1]);
+      if (prole) km[0] = fmaxf(km[0], sm.km[grp ^ 1]);
     }
     if (prole) {
-      ekw = tile_exp(km);
-      // the dQ kernel converts these 32 keys with the same exponent
-      if (lane == 0 && kw < T_ && (KS == 2 || (grp & 1) == 0))
-        kexp[(int64_t)bh * ((T_ + 31) / 32) + (kw >> 5)] = ekw;
-      const float fk = ldexpf(1.f, ekw);
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
+      for (int e = 0; e < NE; ++e) {
+        ekw[e] = tile_exp(km[e]);
+        // the dQ kernel converts these 32 keys with the same exponent
+        if (lane == 0 && kw + 32 * e < T_ && (KS >= 2 || (grp & 1) == 0))
+          kexp[(int64_t)bh * ((T_ + 31) / 32) + (kw >> 5) + e] = ekw[e];
+      }
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const float fk = ldexpf(1.f, ekw[ks / 2]);
 #pragma unroll
         for (int kk = 0; kk < KK; ++kk) bfr[ks][kk] = to_f16x8s<T>(bfr[ks][kk], fk);
+      }
     }
   }
   // S layout: lane (g, li) element j holds q = qh + 4 g + j, key = kw + 16 ks + li
@@ -965,12 +986,18 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
   // bias in use (negated for query chunks wholly below this wave's keys in
   // non-causal mode). S comes out of the MFMA scaled by 2^(eq + ekw) (eq: the
   // Q16 tile's exponent): cbx carries that factor and sc = scale 2^-(eq + ekw)
-  // removes it; the dK accumulators hold 2^(eq + kq) times the sum (kq: the
-  // query tile's dS exponent), rescaled when a tile brings other exponents.
+  // removes it (one of each per K16 exponent); the dK accumulators hold
+  // 2^(eq + kq) times the sum (kq: the query tile's dS exponent), rescaled
+  // when a tile brings other exponents.
   int eq = 0, kq = 0;
-  float sfac = ldexpf(1.f, ekw);  // 2^(eq + ekw)
-  f32x4 cbx = cb * sfac;
-  float sc = ldexpf(scale, -ekw);
+  float sfac[NE], sc[NE];  // 2^(eq + ekw), scale 2^-(eq + ekw)
+  f32x4 cbx[NE];
+#pragma unroll
+  for (int e = 0; e < NE; ++e) {
+    sfac[e] = ldexpf(1.f, ekw[e]);
+    cbx[e] = cb * sfac[e];
+    sc[e] = ldexpf(scale, -ekw[e]);
+  }
   float slx = slope;
   // Padding mask: a dropped key's P and dS column is zero, so its dK / dV
   // rows are zero and the other keys' rows do not depend on it. The kernel
@@ -1021,7 +1048,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
   auto m1 = [&](auto role, int hr, f32x4 (&s_)[KS], const short* as_) __attribute__((always_inline)) {
     constexpr bool P = decltype(role)::value;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) s_[ks] = P ? cbx : f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int ks = 0; ks < KS; ++ks) s_[ks] = P ? cbx[ks / 2] : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {
       const i16x8 fa = lds16(as_ + soff<D>(hr + li, 32 * kk + 8 * g));
@@ -1046,7 +1073,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
       f32x4 wv;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        float s = fmaf(s_[ks][j], sc, tterm);
+        float s = fmaf(s_[ks][j], sc[ks / 2], tterm);
         if constexpr (DIAG && !kCausal) {
           const int dkq = (kw + 16 * ks + li) - (qh + 4 * g + j);
           if (dkq > 0) s = fmaf(-2.f * slope, (float)dkq, s);
@@ -1112,8 +1139,12 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
   if (n_it > 0) issue(0, qbase);
   if (prole) dma_wait();
   __syncthreads();
-  f32x4 dpA[2][KS], dpB[2][KS];  // D role: dP of the current and the next chunk
-  if (!prole && needc(0)) {
+  // D role: dP of the current and the next chunk. At KS = 4 the registers of
+  // the next chunk's dP do not fit beside the rest: dP is computed in its own
+  // step, after the barrier (its MFMAs then cover the reads of w)
+  constexpr bool kAhead = KS <= 2;
+  f32x4 dpA[2][KS], dpB[2][KS];
+  if (kAhead && !prole && needc(0)) {
     m1(std::false_type{}, 0, dpA[0], sm.o[0]);
     m1(std::false_type{}, 16, dpA[1], sm.o[0]);
   }
@@ -1134,9 +1165,12 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
       const int eqt = qexp_h[(qbase >> 6) + it], kqt = ktile_h[(qbase >> 6) + it];
       if (eqt != eq) {
         const float f = ldexpf(1.f, eqt - eq);
-        sfac *= f;
-        sc = ldexpf(sc, eq - eqt);
-        if constexpr (kCausal) cbx *= f;
+#pragma unroll
+        for (int e = 0; e < NE; ++e) {
+          sfac[e] *= f;
+          sc[e] = ldexpf(sc[e], eq - eqt);
+          if constexpr (kCausal) cbx[e] *= f;
+        }
       }
       p4 = ldexpf(0.25f, -kqt);
       // D role: this query tile's dS^T tile (both of its chunks)
@@ -1153,7 +1187,8 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
     }
     if constexpr (!kCausal) {
       const bool above = kw > qc + 31;
-      cbx = (above ? -cb : cb) * sfac;
+#pragma unroll
+      for (int e = 0; e < NE; ++e) cbx[e] = (above ? -cb : cb) * sfac[e];
       slx = above ? -slope : slope;
     }
     if (prole && need) {
@@ -1183,14 +1218,22 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
       // w of this chunk (read whether or not the chunk is needed: the buffer
       // always exists, and a conditional read leaves the compiler zeroing the
       // registers on the other path every chunk)
+      // (KS = 4: each half's w just before its use)
       f32x4 wv[2 * KS];
+      if constexpr (kAhead) {
 #pragma unroll
-      for (int u = 0; u < 2 * KS; ++u) wv[u] = xw[u][lane];
-      if (needc(c + 1)) {
-        constexpr int r1 = 32 * ((CM + 1) & 1);
-        const short* os1 = sm.o[((CM + 1) >> 1) & 1];
-        m1(std::false_type{}, r1, pnext[0], os1);
-        m1(std::false_type{}, r1 + 16, pnext[1], os1);
+        for (int u = 0; u < 2 * KS; ++u) wv[u] = xw[u][lane];
+      }
+      if constexpr (kAhead) {
+        if (needc(c + 1)) {
+          constexpr int r1 = 32 * ((CM + 1) & 1);
+          const short* os1 = sm.o[((CM + 1) >> 1) & 1];
+          m1(std::false_type{}, r1, pnext[0], os1);
+          m1(std::false_type{}, r1 + 16, pnext[1], os1);
+        }
+      } else if (need) {
+        m1(std::false_type{}, r0, pcur[0], sm.o[buf]);
+        m1(std::false_type{}, r0 + 16, pcur[1], sm.o[buf]);
       }
       if (need) {
 #pragma unroll
@@ -1198,6 +1241,10 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
           const f32x4 c4v = *reinterpret_cast<const f32x4*>(sm.st[buf] + r0 + 16 * hh + 4 * g);
           const f32x4 ndv = *reinterpret_cast<const f32x4*>(sm.st[buf] + kBN + r0 + 16 * hh + 4 * g);
           uint32_t (&dp)[KS][2] = hh ? pb : pa;
+          if constexpr (!kAhead) {
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) wv[KS * hh + ks] = xw[KS * hh + ks][lane];
+          }
 #pragma unroll
           for (int ks = 0; ks < KS; ++ks) {
             float dv[4];
@@ -1223,7 +1270,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
 #pragma unroll
           for (int ks = 0; ks < KS; ++ks)
             __builtin_nontemporal_store(pack_frag(pa[ks][0], pa[ks][1], pb[ks][0], pb[ks][1]),
-                                        reinterpret_cast<i16x8*>(tb + dso + 512 * (dsk + ks)));
+                                        reinterpret_cast<i16x8*>(tb + dso[ks]));
         }
         m2(std::false_type{}, r0, pa, pb, sm.q[buf]);
       } else if (dst_ok && c < n_ch && (!kCausal || (c >> 1) >= ((KR * grp) >> 6))) {
@@ -1232,7 +1279,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks)
           __builtin_nontemporal_store(i16x8{0, 0, 0, 0, 0, 0, 0, 0},
-                                      reinterpret_cast<i16x8*>(tb + dso + 512 * (dsk + ks)));
+                                      reinterpret_cast<i16x8*>(tb + dso[ks]));
       }
     }
   };
@@ -1251,11 +1298,12 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
   const int64_t ostr = prole ? a.sdv[2] : a.sdk[2];
   const float osc = prole ? 1.f : ldexpf(scale, -(kq + eq));  // dK: dS's 2^kq and Q16's 2^eq undone (exact)
   // the wave's KR rows (keys) through its own KR x D staging tile in the now
-  // idle tile buffers (8 waves x KR x D x 2 bytes within the Q16 and dO buffers)
+  // idle tile and exchange buffers (8 waves x KR x D x 2 bytes within the
+  // Q16, dO and w buffers)
   typedef DkvSmem<D, KS> Smem;
-  static_assert(sizeof(sm.q) + sizeof(sm.o) >= 8 * KR * D * 2 && offsetof(Smem, q) == 0 &&
-                    offsetof(Smem, o) == sizeof(sm.q),
-                "staging tiles fit the tile buffers");
+  static_assert(sizeof(sm.q) + sizeof(sm.o) + sizeof(sm.x) >= 8 * KR * D * 2 && offsetof(Smem, q) == 0 &&
+                    offsetof(Smem, o) == sizeof(sm.q) && offsetof(Smem, x) == sizeof(sm.q) + sizeof(sm.o),
+                "staging tiles fit the tile and exchange buffers");
   short* const et = reinterpret_cast<short*>(&sm) + w * KR * D;
   __syncthreads();  // every wave is done with the tile buffers
 #pragma unroll
@@ -1381,7 +1429,7 @@ int launch_bwd(const AttnArgs& a, void* ws, hipStream_t st) {
   if (int rc = check_launch("kat_attn_bwd (stats scale)")) return rc;
   // per group of heads (and per band of key tiles): dK, dV (and the dS^T
   // tiles), then dQ from those tiles
-  constexpr int KR = D == 256 ? 16 : kRows, BK = kNW * KR;  // keys per wave pair and per dK/dV block
+  constexpr int KR = dkv_keys<D>(), BK = kNW * KR;  // keys per wave pair and per dK/dV block
   constexpr int BQ = dq_block_queries<D>();                 // queries per dQ block
   const int nt = (a.T + 63) / 64, nqb = (a.T + BQ - 1) / BQ;
   for (int bh0 = 0; bh0 < BH; bh0 += w.group) {

@@ -315,7 +315,8 @@ def test_mfma_backward_key_groups_of_different_magnitude(gpu, D, dtype, width, m
     # exponent for any group would move that group's share of dq or dk by 2^s.
     # width 16: the two 16-key halves of a 32-key group differ (at D = 256 two
     # wave pairs own them and must agree on the group's exponent: one from
-    # the smaller half would overflow the larger half's fp16 copy).
+    # the smaller half would overflow the larger half's fp16 copy). At D = 64
+    # one wave pair owns 64 keys, two groups with an exponent each.
     _pin_mfma(monkeypatch, D)
     B, H, T = 1, 2, 300
     q, k, v, do = (t.float() for t in _inputs(47 + D, B, H, T, D, torch.float32))
