@@ -818,9 +818,10 @@ __global__ __launch_bounds__(64 * kDqW, 1) void attn_bwd_dq_k(AttnArgs a, const 
 }
 
 // ============================================================================
-// dK, dV: 128 keys per block, 8 waves in two roles. Waves w and w + 4 share the
-// 32 keys kw = k0 + 32 (w % 4) and one SIMD; each role holds one B-operand set
-// and one accumulator set (~200 VGPRs, two waves per SIMD):
+// dK, dV: 4 KR keys per block, 8 waves in two roles. Waves w and w + 4 share the
+// KR keys kw = k0 + KR (w % 4) and one SIMD (KR = 32 at D = 128, see
+// dkv_keys); each role holds one B-operand set and one accumulator set
+// (~200 VGPRs, two waves per SIMD):
 //   P role (w < 4)   S  = Q16 K16^T (+bias)  A = Q16 (LDS rows)         B = K16^T (VGPRs)
 //                    dV^T += dO^T P          A = dO^T (LDS transposed)  B = P (from S)
 //   D role (w >= 4)  dP = dO V^T             A = dO  (LDS rows)         B = V^T   (VGPRs)
@@ -836,8 +837,8 @@ __global__ __launch_bounds__(64 * kDqW, 1) void attn_bwd_dq_k(AttnArgs a, const 
 // through LDS; a tile is worked in two 32-query chunks with one barrier each:
 //   phase 1: P role S, P, w of chunk c                    | barrier
 //   phase 2: P role dV(c); D role dP(c + 1), dS(c), dK(c)
-// The D role computes dP one chunk ahead so that the reads of w issued after
-// the barrier overlap with MFMAs.
+// The D role computes dP one chunk ahead (KR <= 32) so that the reads of w
+// issued after the barrier overlap with MFMAs.
 // ============================================================================
 template <int D, int KS>
 struct DkvSmem {
@@ -1001,8 +1002,8 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
   float slx = slope;
   // Padding mask: a dropped key's P and dS column is zero, so its dK / dV
   // rows are zero and the other keys' rows do not depend on it. The kernel
-  // computes every key and stores zeros for dropped ones; a wave group whose
-  // 32 keys are all dropped skips the work.
+  // computes every key and stores zeros for dropped ones; a wave pair whose
+  // KR keys are all dropped skips the work.
   bool kval[KS];
   bool gany = true;
 #pragma unroll
