@@ -1431,6 +1431,7 @@ int launch_bwd(const AttnArgs& a, void* ws, hipStream_t st) {
   // per group of heads (and per band of key tiles): dK, dV (and the dS^T
   // tiles), then dQ from those tiles
   constexpr int KR = dkv_keys<D>(), BK = kNW * KR;  // keys per wave pair and per dK/dV block
+  static_assert((kQB * 64) % BK == 0, "dK/dV blocks tile a band (bands start at multiples of kQB tiles)");
   constexpr int BQ = dq_block_queries<D>();                 // queries per dQ block
   const int nt = (a.T + 63) / 64, nqb = (a.T + BQ - 1) / BQ;
   for (int bh0 = 0; bh0 < BH; bh0 += w.group) {
