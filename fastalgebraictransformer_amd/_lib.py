@@ -91,7 +91,14 @@ def dtype_code(t):
         raise TypeError(f"unsupported dtype {t.dtype}; expected float32/bfloat16/float16/float64")
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream(t):
+    """The current torch stream of t's device as a hipStream_t (the raw-pointer
+    query, where torch has it, skips building a Stream object on every launch)."""
+    if _raw_stream is not None:
+        return ctypes.c_void_p(_raw_stream(t.device.index))
     return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
 
 

@@ -95,6 +95,15 @@ def _warn_if_tiled(tensors, D, dtype, mfma_inputs=None):
         return
     T = tensors[0].shape[2]
     elem = tensors[0].element_size()
+    # the common case in a few attribute reads (it runs on every call): every
+    # operand with the (b, h, t) strides of a contiguous [B, H, T, D] tensor
+    # (multiples of D, row stride D) and a 16-byte aligned start
+    H = tensors[0].shape[1]
+    dense = (H * T * D, T * D, D)
+    if _mfma_head_dim(D, elem) and (T + _MFMA_ROW_PAD) * D * elem <= _MFMA_OFFSET_LIMIT and \
+            (elem != 2 or (T * D * 2 < _MFMA_OFFSET_LIMIT and T * 8 < _MFMA_OFFSET_LIMIT)) and \
+            all(t.stride()[:3] == dense and t.data_ptr() % 16 == 0 for t in tensors):
+        return
     align = [(t.stride()[:3], t.data_ptr()) for t in tensors]
     reason = _tiled_reason(align, D, T, elem)
     if reason is None and mfma_inputs is not None:
