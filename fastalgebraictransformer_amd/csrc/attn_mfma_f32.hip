@@ -275,21 +275,37 @@ __device__ __forceinline__ void p_ds(float s, float dp, float ci, float dl, floa
   ds = p * (4.f * r * r * __builtin_amdgcn_rcpf(t + eps2)) * (dp - dl);
 }
 
+// the LDS of the dQ and of the dK/dV blocks, which share one launch
+template <int D> struct F32DqSmem {
+  short k[2][f32_kt<D>() * 2 * D];
+  short v[2][f32_kt<D>() * 2 * D];
+};
+template <int D> struct F32DkvSmem {
+  short q[2][f32_qt<D>() * 2 * D];
+  short g[2][f32_qt<D>() * 2 * D];
+  float st[2][2][f32_qt<D>()];  // per tile: cinv, then Delta, of its queries
+};
+template <int D> union F32BwdSmem {
+  F32DqSmem<D> dq;
+  F32DkvSmem<D> dkv;
+};
+
+// bid: the block's index among the dQ blocks
 template <int D, int MODE>
-__global__ __launch_bounds__(64 * kF32W, D >= 256 ? 1 : 2) void attn_bwd_dq_f32_k(AttnArgs a, const float* __restrict__ delta,
-                                                                 const float* __restrict__ cinv) {
+__device__ __forceinline__ void bwd_dq_f32(const AttnArgs& a, const float* __restrict__ delta,
+                                           const float* __restrict__ cinv, int bid, F32DqSmem<D>& sm) {
   constexpr int D16 = 2 * D;
   constexpr int KT = f32_kt<D>();
   constexpr int M = D / 16;
   constexpr bool kCausal = (MODE & kModeCausalF) != 0;
   constexpr bool kKM = (MODE & kModeKeyMaskF) != 0;
   constexpr uint64_t kAll = KT == 64 ? ~0ull : (1ull << KT) - 1ull;
-  __shared__ short sk[2][KT * D16];
-  __shared__ short sv[2][KT * D16];
+  short (&sk)[2][KT * D16] = sm.k;
+  short (&sv)[2][KT * D16] = sm.v;
 
   const int T_ = a.T, H = a.H;
   int bh, rank;
-  block_order((int)blockIdx.x, a.B * H, bh, rank);
+  block_order(bid, a.B * H, bh, rank);
   const int n_qt = (T_ + kF32BM - 1) / kF32BM;
   const int q0 = (n_qt - 1 - rank) * kF32BM;
   const int b = bh / H, h = bh - b * H;
@@ -442,21 +458,22 @@ __global__ __launch_bounds__(64 * kF32W, D >= 256 ? 1 : 2) void attn_bwd_dq_f32_
 
 // D = 256: the K^T and V^T fragments and the dV^T and dK^T accumulators alone
 // take 256 VGPRs, so one block per CU (one wave per SIMD, 512 registers)
+// bid: the block's index among the dK/dV blocks
 template <int D, int MODE>
-__global__ __launch_bounds__(64 * kF32W, D >= 256 ? 1 : 2) void attn_bwd_dkv_f32_k(AttnArgs a, const float* __restrict__ delta,
-                                                                  const float* __restrict__ cinv) {
+__device__ __forceinline__ void bwd_dkv_f32(const AttnArgs& a, const float* __restrict__ delta,
+                                            const float* __restrict__ cinv, int bid, F32DkvSmem<D>& sm) {
   constexpr int D16 = 2 * D;
   constexpr int QT = f32_qt<D>();
   constexpr int M = D / 16;
   constexpr bool kCausal = (MODE & kModeCausalF) != 0;
   constexpr bool kKM = (MODE & kModeKeyMaskF) != 0;
-  __shared__ short sq[2][QT * D16];
-  __shared__ short sg[2][QT * D16];
-  __shared__ float sst[2][2][QT];  // per tile: cinv, then Delta, of its queries
+  short (&sq)[2][QT * D16] = sm.q;
+  short (&sg)[2][QT * D16] = sm.g;
+  float (&sst)[2][2][QT] = sm.st;
 
   const int T_ = a.T, H = a.H;
   int bh, rank;
-  block_order((int)blockIdx.x, a.B * H, bh, rank);  // rank 0: the first keys (most queries)
+  block_order(bid, a.B * H, bh, rank);  // rank 0: the first keys (most queries)
   const int k0 = rank * kF32KB;
   const int b = bh / H, h = bh - b * H;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -608,6 +625,24 @@ __global__ __launch_bounds__(64 * kF32W, D >= 256 ? 1 : 2) void attn_bwd_dkv_f32
   }
 }
 
+// The backward's dK/dV and dQ blocks in one launch (they are independent: both
+// take Delta and cinv from attn_delta): blocks [0, nk) run dK/dV, blocks
+// [nkp, nkp + nq) dQ, nkp = nk rounded up to a multiple of 8 (the blocks in
+// between exit at once) so that each part's block ids keep their XCD (id % 8)
+// for block_order. Small problems run both parts side by side (config 1,
+// B=2, H=12, S=512: 192 + 192 blocks on 256 CUs) instead of one after the
+// other; the LDS of the two parts is shared, registers are the larger part's.
+template <int D, int MODE>
+__global__ __launch_bounds__(64 * kF32W, D >= 256 ? 1 : 2) void attn_bwd_f32_k(AttnArgs a, const float* __restrict__ delta,
+                                                              const float* __restrict__ cinv, int nk, int nkp) {
+  __shared__ F32BwdSmem<D> sm;
+  const int id = (int)blockIdx.x;
+  if (id < nk)
+    bwd_dkv_f32<D, MODE>(a, delta, cinv, id, sm.dkv);
+  else if (id >= nkp)
+    bwd_dq_f32<D, MODE>(a, delta, cinv, id - nkp, sm.dq);
+}
+
 // layout widths of the fp32 kernels: 32, 64, 128, 256 (a head dim between
 // them, a multiple of 4, runs in the next width with its columns past D as zeros)
 int f32_width(int D) { return D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : 256; }
@@ -630,10 +665,10 @@ template <int D, int MODE>
 int launch_bwd_f32(const AttnArgs& a, const float* delta, const float* cinv, hipStream_t st) {
   const int64_t nq = (int64_t)((a.T + kF32BM - 1) / kF32BM) * a.B * a.H;
   const int64_t nk = (int64_t)((a.T + kF32KB - 1) / kF32KB) * a.B * a.H;
-  hipLaunchKernelGGL((attn_bwd_dkv_f32_k<D, MODE>), dim3((unsigned)nk), dim3(64 * kF32W), 0, st, a, delta, cinv);
-  if (int rc = check_launch("kat_attn_bwd (fp32 mfma dkv)")) return rc;
-  hipLaunchKernelGGL((attn_bwd_dq_f32_k<D, MODE>), dim3((unsigned)nq), dim3(64 * kF32W), 0, st, a, delta, cinv);
-  return check_launch("kat_attn_bwd (fp32 mfma dq)");
+  const int64_t nkp = (nk + 7) & ~(int64_t)7;
+  hipLaunchKernelGGL((attn_bwd_f32_k<D, MODE>), dim3((unsigned)(nkp + nq)), dim3(64 * kF32W), 0, st, a, delta,
+                     cinv, (int)nk, (int)nkp);
+  return check_launch("kat_attn_bwd (fp32 mfma)");
 }
 
 // 31-bit byte offsets per (b, h) slice for every row the kernels address
@@ -642,7 +677,8 @@ bool f32_offsets_ok(const AttnArgs& a, bool bwd) {
   const int64_t* s2[4] = {&a.sq[2], &a.sk[2], &a.sv[2], &a.sdo[2]};
   for (int t = 0; t < (bwd ? 4 : 3); ++t)
     if (*s2[t] < a.D || ((int64_t)a.T + 128) * *s2[t] * 4 > lim) return false;
-  return (int64_t)((a.T + kF32BM - 1) / kF32BM) * a.B * a.H <= 0x7fffffffLL;
+  // the backward's launch: dK/dV blocks (rounded up to 8) and dQ blocks
+  return 2 * ((int64_t)((a.T + kF32BM - 1) / kF32BM) * a.B * a.H + 8) <= 0x7fffffffLL;
 }
 
 }  // namespace
