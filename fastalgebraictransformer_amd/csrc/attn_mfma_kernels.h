@@ -837,7 +837,7 @@ __global__ __launch_bounds__(64 * kDqW, 1) void attn_bwd_dq_k(AttnArgs a, const 
 // through LDS; a tile is worked in two 32-query chunks with one barrier each:
 //   phase 1: P role S, P, w of chunk c                    | barrier
 //   phase 2: P role dV(c); D role dP(c + 1), dS(c), dK(c)
-// The D role computes dP one chunk ahead (KR <= 32) so that the reads of w
+// The D role computes dP one chunk ahead (KR = 32) so that the reads of w
 // issued after the barrier overlap with MFMAs.
 // ============================================================================
 template <int D, int KS>
@@ -1140,10 +1140,12 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv_k(AttnArgs a, const float
   if (n_it > 0) issue(0, qbase);
   if (prole) dma_wait();
   __syncthreads();
-  // D role: dP of the current and the next chunk. At KS = 4 the registers of
-  // the next chunk's dP do not fit beside the rest: dP is computed in its own
-  // step, after the barrier (its MFMAs then cover the reads of w)
-  constexpr bool kAhead = KS <= 2;
+  // D role: dP of the current and the next chunk (KS = 2). At KS = 4 the
+  // registers of the next chunk's dP do not fit beside the rest, and at KS = 1
+  // (D = 256) they cost spills in the non-causal modes: dP is then computed in
+  // its own step, after the barrier (its MFMAs cover the reads of w; D = 256
+  // measured 0-3% faster causal and 8% non-causal, bit-identical)
+  constexpr bool kAhead = KS == 2;
   f32x4 dpA[2][KS], dpB[2][KS];
   if (kAhead && !prole && needc(0)) {
     m1(std::false_type{}, 0, dpA[0], sm.o[0]);
