@@ -253,15 +253,16 @@ __global__ __launch_bounds__(64 * kF32W, D >= 256 ? 1 : 2) void attn_fwd_f32_k(A
 //   dS = p g (dP - Delta),  dQ = scale dS K,  dK = scale dS^T Q,  dV = P^T dO;
 // with t = 2 sigma = 1 + s r, r = 1 / (|s| + 1) and cinv = 1 / (16 (L + eps)):
 // p = t^4 cinv and g = 4 r^2 / (t + 2 eps).
-//   attn_bwd_dq_f32_k   query blocks as in the forward: S^T = K Q^T and
-//                       dP^T = V dO^T (A = K, V rows; B = Q^T, dO^T in VGPRs),
-//                       dS^T, dQ^T += K^T dS^T (A = K read by columns, B = dS^T
-//                       in its C registers as they stand)
-//   attn_bwd_dkv_f32_k  key blocks, 16 keys per wave: S = Q K^T, dP = dO V^T
-//                       (A = Q, dO rows; B = K^T, V^T in VGPRs), P and dS,
-//                       dV^T += dO^T P, dK^T += Q^T dS (A = dO, Q read by
-//                       columns; B = P, dS as they stand)
-// Delta and cinv come from attn_delta (the tiled path's first pass).
+//   bwd_dq_f32   query blocks as in the forward: S^T = K Q^T and
+//                dP^T = V dO^T (A = K, V rows; B = Q^T, dO^T in VGPRs),
+//                dS^T, dQ^T += K^T dS^T (A = K read by columns, B = dS^T
+//                in its C registers as they stand)
+//   bwd_dkv_f32  key blocks, 16 keys per wave: S = Q K^T, dP = dO V^T
+//                (A = Q, dO rows; B = K^T, V^T in VGPRs), P and dS,
+//                dV^T += dO^T P, dK^T += Q^T dS (A = dO, Q read by
+//                columns; B = P, dS as they stand)
+// Both run as the blocks of one launch, attn_bwd_f32_k. Delta and cinv come
+// from attn_delta (the tiled path's first pass).
 // ============================================================================
 constexpr int kF32KB = kF32W * 16;  // keys per dK/dV block
 template <int D> constexpr int f32_qt() { return D >= 256 ? 16 : D >= 128 ? 32 : 64; }  // queries per LDS tile
