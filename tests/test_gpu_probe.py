@@ -42,3 +42,15 @@ def test_probe_rejects_bad_arguments():
     flops = ctypes.c_double(0.0)
     assert lib.kat_probe_mfma_bf16(None, 4, 10, ctypes.byref(flops), None) != 0
     assert lib.kat_probe_mfma_bf16_random(None, 4, 10, ctypes.byref(flops), None) != 0
+
+
+def test_launch_stream_is_the_current_torch_stream(gpu):
+    # every libkat call is queued on torch's current stream of the tensor's
+    # device (the raw-pointer query in _lib.stream), also inside a
+    # torch.cuda.stream(...) block
+    x = torch.empty(1, device="cuda")
+    assert (_lib.stream(x).value or 0) == torch.cuda.current_stream().cuda_stream
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        assert (_lib.stream(x).value or 0) == s.cuda_stream
+    assert (_lib.stream(x).value or 0) == torch.cuda.current_stream().cuda_stream
