@@ -269,7 +269,9 @@ int kat_attn_decode(const void* q, const void* k, const void* v, void* out, floa
  * splits as kat_attn_decode picks them; kat_attn_decode_workspace_size gives
  * the byte count) exceed the array fail with KAT_EUNSUPPORTED. The call
  * allocates nothing; the first call on a device looks up the array's device
- * address (hipGetSymbolAddress) once. Every call on one GPU shares that
+ * address (hipGetSymbolAddress) once and keeps it for the process, so the
+ * entry point must not be used on a device after hipDeviceReset (which
+ * invalidates that address). Every call on one GPU shares that
  * GPU's array: calls that overlap in time on one GPU (different streams or
  * host threads) race; calls ordered on one stream do not. */
 #define KAT_DECODE_SCRATCH_BYTES ((size_t)8 << 20)
